@@ -1,0 +1,120 @@
+/*
+ * CPU oracle for the attention path: test infrastructure only.
+ *
+ * A double-precision restatement of the reference's attention semantics, used to check the HIP kernels and
+ * timed as the CPU baseline. Nothing in the product library links or calls it.
+ *
+ * Followed, function by function (reference file:line):
+ *   oracle_attn_dense   - tests/sparse_attn_test.cpp:143-173 (double softmax over an explicit key list),
+ *                         generalised with the mask rule of src/kernels/ops.metal:289 (j < n_k && (j <= pos ||
+ *                         (pos >= block && j >= block)), pos = q_pos0 + row), the GQA head map of ops.metal:242
+ *                         (kv head = h / (heads / kv_heads)), fully masked rows -> 0 (ops.metal:355), rows >= n_q
+ *                         not stored (ops.metal:359-362), and lse = max + log(sum) (natural log).
+ *   oracle_attn_sparse  - the pass list of ops.metal:1079-1098 (selected 64-row cubes, then dense rows
+ *                         [dense0, dense1); tiles past n_cubes see [0, n_k)), the validity mask of ops.metal:1109,
+ *                         and the row map of ops.metal:1173-1184; plus a causal flag (j <= row) that the
+ *                         reference does not have.
+ *   oracle_cube_select  - cube_pool / cube_scores / cube_topk (ops.metal:926-1027): mean of the 64 rows over
+ *                         cnt[c], dot products, local picks first, then repeated argmax, ties to the smaller index;
+ *                         the CPU form of tests/sparse_attn_test.cpp:103-128.
+ *   oracle_attn_decode  - one query row per sequence at position ctx - 1 against keys [0, ctx): the dense rule
+ *                         with n_q = 1, q_pos0 = ctx - 1 (ops.metal:289), batched.
+ *   oracle_lse_merge    - the split-K merge: o = sum_i exp(lse_i - lse) o_i, lse = log sum_i exp(lse_i).
+ *
+ * Inputs are raw element arrays of a stated type (f32, f16 or bf16 bits), widened exactly to double.
+ */
+#ifndef MAKO_ATTN_ORACLE_H
+#define MAKO_ATTN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_BF16 = 2 };
+
+/* The reference's AttnArgs (src/kernels/ops.metal:54-64), field for field. */
+typedef struct oracle_attn_args {
+    uint32_t n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, width;
+    float scale;
+} oracle_attn_args;
+
+/* The reference's SparseAttnArgs (src/kernels/ops.metal:1029-1034) plus causal and sel_heads. */
+typedef struct oracle_sparse_args {
+    uint32_t n_q, q_pad, n_k, k_pad, heads, kv_heads, width;
+    float scale;
+    uint32_t n_cubes, max_sel, dense0, dense1;
+    uint32_t causal;    /* 1: key j is seen by tile row r only when j <= r */
+    uint32_t sel_heads; /* rows of sel / nsel: heads (one list per query head) or kv_heads (shared by a group) */
+} oracle_sparse_args;
+
+/* Element i of a raw array of type `dtype`, widened exactly. */
+double oracle_load(const void* p, int dtype, size_t i);
+/* f32 -> f16 / bf16 bits, round to nearest even (NaN stays NaN). */
+uint16_t oracle_f32_to_f16(float f);
+uint16_t oracle_f32_to_bf16(float f);
+float oracle_f16_to_f32(uint16_t h);
+
+/*
+ * Dense attention (causal / bidirectional / prefix-causal by `block`). q [heads][q_pad][dim], k and v
+ * [kv_heads][k_pad][dim]; o [n_q][width] (head h at column h * dim), lse [heads][n_q] (may be NULL).
+ * nthreads 0: all online cores. Returns 0, or -1 on a shape it cannot take.
+ */
+int oracle_attn_dense(const oracle_attn_args* a, uint32_t dim, int dtype, const void* q, const void* k,
+                      const void* v, double* o, double* lse, int nthreads);
+
+/*
+ * The same for a list of (head, row) pairs only: o_rows [n][dim], lse_rows [n]. For sampled checks and the
+ * CPU baseline's bounded sample.
+ */
+int oracle_attn_dense_rows(const oracle_attn_args* a, uint32_t dim, int dtype, const void* q, const void* k,
+                           const void* v, const uint32_t* head_row, size_t n, double* o_rows, double* lse_rows,
+                           int nthreads);
+
+/*
+ * Block-sparse attention, D = 128 (64-row tiles and cubes). sel u16 [sel_heads][n_cubes][max_sel], nsel u16
+ * [sel_heads][n_cubes], valid u8 [k_pad], map i32 [q_pad]; o has o_rows rows of width (rows with map < 0 or
+ * row >= n_q are not written), lse [heads][q_pad] indexed by tile row (may be NULL; written where o is).
+ */
+int oracle_attn_sparse(const oracle_sparse_args* a, int dtype, const void* q, const void* k, const void* v,
+                       const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map,
+                       double* o, uint32_t o_rows, double* lse, int nthreads);
+
+/* The sparse rule for a list of (head, tile row) pairs: o_rows [n][128], lse_rows [n]. */
+int oracle_attn_sparse_rows(const oracle_sparse_args* a, int dtype, const void* q, const void* k, const void* v,
+                            const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
+                            const uint32_t* head_row, size_t n, double* o_rows, double* lse_rows, int nthreads);
+
+/*
+ * cube_select: q [heads][q_pad][dim], k [heads][k_pad][dim]; cnt u32 [n_cubes]; sel u16 [heads][n_cubes][kk],
+ * nsel u16 [heads][n_cubes] with kk = min(topk, n_cubes). qp / kp / sc may be NULL (else [heads][n][dim],
+ * [heads][n][dim], [heads][n][n] doubles). Returns 0, or -1 on the arguments the reference refuses.
+ */
+int oracle_cube_select(uint32_t heads, uint32_t dim, int dtype, const void* q, uint32_t q_pad, const void* k,
+                       uint32_t k_pad, uint32_t n_cubes, const uint32_t* cnt, uint32_t topk, uint32_t local,
+                       uint32_t stride, uint16_t* sel, uint16_t* nsel, double* qp, double* kp, double* sc);
+
+/*
+ * Batched single-token decode: q [batch][heads][dim] (one row a sequence), k and v [batch][kv_heads][cap][dim],
+ * ctx u32 [batch] (keys [0, ctx) of each sequence); o [batch][heads * dim], lse [batch][heads] (may be NULL).
+ */
+int oracle_attn_decode(uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t dim, uint32_t cap, float scale,
+                       int dtype, const void* q, const void* k, const void* v, const uint32_t* ctx, double* o,
+                       double* lse, int nthreads);
+
+/* The decode rule for a list of (sequence, head) pairs: o_rows [n][dim], lse_rows [n]. */
+int oracle_attn_decode_rows(uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t dim, uint32_t cap,
+                            float scale, int dtype, const void* q, const void* k, const void* v,
+                            const uint32_t* ctx, const uint32_t* seq_head, size_t n, double* o_rows,
+                            double* lse_rows, int nthreads);
+
+/* Merges n partial results of one row: o_i [n][dim] (each normalised), lse_i [n] -> o [dim], *lse. */
+void oracle_lse_merge(uint32_t n, uint32_t dim, const double* o_i, const double* lse_i, double* o, double* lse);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,256 @@
+"""ctypes binding of the CPU oracle (oracle/attn_oracle.c): test infrastructure only.
+
+Only the tests, the smoke check and the benchmark's CPU-baseline leg use this module, and only as the checker or
+the timed CPU baseline. Inputs are numpy arrays of float32, or uint16 bit patterns of float16 / bfloat16; outputs
+are float64.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32, F16, BF16 = 0, 1, 2
+
+
+class AttnArgs(ctypes.Structure):
+    """The reference's AttnArgs (src/kernels/ops.metal:54-64)."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in ("n_q", "q_pad", "n_k", "k_pad", "heads", "kv_heads", "q_pos0",
+                                               "block", "width")] + [("scale", ctypes.c_float)]
+
+
+class SparseArgs(ctypes.Structure):
+    """The reference's SparseAttnArgs (src/kernels/ops.metal:1029-1034) plus causal and sel_heads."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in ("n_q", "q_pad", "n_k", "k_pad", "heads", "kv_heads", "width")] + \
+        [("scale", ctypes.c_float)] + \
+        [(n, ctypes.c_uint32) for n in ("n_cubes", "max_sel", "dense0", "dense1", "causal", "sel_heads")]
+
+
+def build(name="liboracle.so", mutant=None):
+    """Builds the oracle library (or a mutant with one planted mistake) and returns its path."""
+    target = name if mutant is None else f"liboracle_mutant{mutant}.so"
+    subprocess.run(["make", "-s", "-C", HERE, target], check=True)
+    return os.path.join(HERE, target)
+
+
+_libs = {}
+
+
+def lib(mutant=None):
+    """The oracle library (built on first use when missing)."""
+    if mutant not in _libs:
+        path = os.path.join(HERE, "liboracle.so" if mutant is None else f"liboracle_mutant{mutant}.so")
+        if not os.path.exists(path) or mutant is not None:
+            path = build(mutant=mutant)
+        L = ctypes.CDLL(path)
+        P, U32, I, SZ, F = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+        L.oracle_attn_dense.argtypes = [ctypes.POINTER(AttnArgs), U32, I, P, P, P, P, P, I]
+        L.oracle_attn_dense_rows.argtypes = [ctypes.POINTER(AttnArgs), U32, I, P, P, P, P, SZ, P, P, I]
+        L.oracle_attn_sparse.argtypes = [ctypes.POINTER(SparseArgs), I, P, P, P, P, P, P, P, P, U32, P, I]
+        L.oracle_attn_sparse_rows.argtypes = [ctypes.POINTER(SparseArgs), I, P, P, P, P, P, P, P, SZ, P, P, I]
+        L.oracle_cube_select.argtypes = [U32, U32, I, P, U32, P, U32, U32, P, U32, U32, U32, P, P, P, P, P]
+        L.oracle_attn_decode.argtypes = [U32, U32, U32, U32, U32, F, I, P, P, P, P, P, P, I]
+        L.oracle_attn_decode_rows.argtypes = [U32, U32, U32, U32, U32, F, I, P, P, P, P, P, SZ, P, P, I]
+        L.oracle_lse_merge.argtypes = [U32, U32, P, P, P, P]
+        L.oracle_lse_merge.restype = None
+        L.oracle_f32_to_f16.argtypes = [F]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_f32_to_bf16.argtypes = [F]
+        L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_f16_to_f32.restype = F
+        _libs[mutant] = L
+    return _libs[mutant]
+
+
+def _p(x):
+    return None if x is None else x.ctypes.data_as(ctypes.c_void_p)
+
+
+def _dtype_code(x):
+    if x.dtype == np.float32:
+        return F32
+    raise TypeError("pass float32 arrays, or uint16 bit patterns with an explicit dtype")
+
+
+def _raw(x, dtype):
+    x = np.ascontiguousarray(x)
+    if dtype is None:
+        return x, _dtype_code(x)
+    assert x.dtype == np.uint16 and dtype in (F16, BF16)
+    return x, dtype
+
+
+def attn_dense(q, k, v, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, scale=None, dtype=None,
+               width=None, nthreads=0, mutant=None):
+    """Dense attention: returns (o [n_q][width], lse [heads][n_q])."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    v, _ = _raw(v, dtype)
+    width = heads * dim if width is None else width
+    scale = np.float32(1.0 / np.sqrt(dim)) if scale is None else scale
+    a = AttnArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block & 0xFFFFFFFF, width, scale)
+    o = np.zeros((n_q, width), np.float64)
+    lse = np.zeros((heads, n_q), np.float64)
+    rc = lib(mutant).oracle_attn_dense(ctypes.byref(a), dim, code, _p(q), _p(k), _p(v), _p(o), _p(lse), nthreads)
+    if rc:
+        raise ValueError("oracle_attn_dense: shape refused")
+    return o, lse
+
+
+def attn_dense_rows(q, k, v, head_row, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, scale=None,
+                    dtype=None, nthreads=0, mutant=None):
+    """Dense attention for (head, row) pairs: returns (o [n][dim], lse [n])."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    v, _ = _raw(v, dtype)
+    hr = np.ascontiguousarray(head_row, np.uint32).reshape(-1, 2)
+    scale = np.float32(1.0 / np.sqrt(dim)) if scale is None else scale
+    a = AttnArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block & 0xFFFFFFFF, heads * dim, scale)
+    o = np.zeros((len(hr), dim), np.float64)
+    lse = np.zeros(len(hr), np.float64)
+    rc = lib(mutant).oracle_attn_dense_rows(ctypes.byref(a), dim, code, _p(q), _p(k), _p(v), _p(hr), len(hr),
+                                            _p(o), _p(lse), nthreads)
+    if rc:
+        raise ValueError("oracle_attn_dense_rows: shape refused")
+    return o, lse
+
+
+def attn_sparse(q, k, v, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, n_cubes, max_sel,
+                dense0, dense1, causal=0, sel_heads=None, o_rows=None, width=None, dtype=None, o_fill=None,
+                nthreads=0, mutant=None):
+    """Block-sparse attention: returns (o [o_rows][width], lse [heads][q_pad]); o starts as o_fill."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    v, _ = _raw(v, dtype)
+    width = heads * 128 if width is None else width
+    o_rows = q_pad if o_rows is None else o_rows
+    sel_heads = heads if sel_heads is None else sel_heads
+    a = SparseArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, width, np.float32(1.0 / np.sqrt(128.0)), n_cubes,
+                   max_sel, dense0, dense1, causal, sel_heads)
+    o = np.zeros((o_rows, width), np.float64) if o_fill is None else np.array(o_fill, np.float64)
+    lse = np.full((heads, q_pad), np.nan, np.float64)
+    sel = np.ascontiguousarray(sel, np.uint16)
+    nsel = np.ascontiguousarray(nsel, np.uint16)
+    valid = np.ascontiguousarray(valid, np.uint8)
+    map_ = np.ascontiguousarray(map_, np.int32)
+    rc = lib(mutant).oracle_attn_sparse(ctypes.byref(a), code, _p(q), _p(k), _p(v), _p(sel), _p(nsel), _p(valid),
+                                        _p(map_), _p(o), o_rows, _p(lse), nthreads)
+    if rc:
+        raise ValueError("oracle_attn_sparse: shape refused")
+    return o, lse
+
+
+def attn_sparse_rows(q, k, v, sel, nsel, valid, head_row, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, n_cubes,
+                     max_sel, dense0, dense1, causal=0, sel_heads=None, dtype=None, nthreads=0, mutant=None):
+    """Block-sparse attention for (head, tile row) pairs: returns (o [n][128], lse [n])."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    v, _ = _raw(v, dtype)
+    sel_heads = heads if sel_heads is None else sel_heads
+    a = SparseArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, heads * 128, np.float32(1.0 / np.sqrt(128.0)),
+                   n_cubes, max_sel, dense0, dense1, causal, sel_heads)
+    hr = np.ascontiguousarray(head_row, np.uint32).reshape(-1, 2)
+    o = np.zeros((len(hr), 128), np.float64)
+    lse = np.zeros(len(hr), np.float64)
+    sel = np.ascontiguousarray(sel, np.uint16)
+    nsel = np.ascontiguousarray(nsel, np.uint16)
+    valid = np.ascontiguousarray(valid, np.uint8)
+    rc = lib(mutant).oracle_attn_sparse_rows(ctypes.byref(a), code, _p(q), _p(k), _p(v), _p(sel), _p(nsel),
+                                             _p(valid), _p(hr), len(hr), _p(o), _p(lse), nthreads)
+    if rc:
+        raise ValueError("oracle_attn_sparse_rows: shape refused")
+    return o, lse
+
+
+def cube_select(q, k, cnt, *, heads, dim, q_pad, k_pad, n_cubes, topk, local=0, stride=0, dtype=None,
+                mutant=None, want_scores=False):
+    """cube_select: returns (sel [heads][n][kk] u16, nsel [heads][n] u16[, qp, kp, sc])."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    kk = min(topk, n_cubes)
+    sel = np.zeros((heads, n_cubes, max(kk, 1)), np.uint16)
+    nsel = np.zeros((heads, n_cubes), np.uint16)
+    cnt = np.ascontiguousarray(cnt, np.uint32)
+    qp = np.zeros((heads, n_cubes, dim)) if want_scores else None
+    kp = np.zeros((heads, n_cubes, dim)) if want_scores else None
+    sc = np.zeros((heads, n_cubes, n_cubes)) if want_scores else None
+    rc = lib(mutant).oracle_cube_select(heads, dim, code, _p(q), q_pad, _p(k), k_pad, n_cubes, _p(cnt), topk, local,
+                                        stride, _p(sel), _p(nsel), _p(qp), _p(kp), _p(sc))
+    if rc:
+        raise ValueError("cube_select: refused")
+    if want_scores:
+        return sel, nsel, qp, kp, sc
+    return sel, nsel
+
+
+def attn_decode(q, k, v, ctx, *, batch, heads, kv_heads, dim, cap, scale=None, dtype=None, nthreads=0,
+                mutant=None):
+    """Batched decode: returns (o [batch][heads*dim], lse [batch][heads])."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    v, _ = _raw(v, dtype)
+    ctx = np.ascontiguousarray(ctx, np.uint32)
+    scale = np.float32(1.0 / np.sqrt(dim)) if scale is None else scale
+    o = np.zeros((batch, heads * dim), np.float64)
+    lse = np.zeros((batch, heads), np.float64)
+    rc = lib(mutant).oracle_attn_decode(batch, heads, kv_heads, dim, cap, scale, code, _p(q), _p(k), _p(v), _p(ctx),
+                                        _p(o), _p(lse), nthreads)
+    if rc:
+        raise ValueError("oracle_attn_decode: refused")
+    return o, lse
+
+
+def attn_decode_rows(q, k, v, ctx, seq_head, *, batch, heads, kv_heads, dim, cap, scale=None, dtype=None,
+                     nthreads=0, mutant=None):
+    """Batched decode for (sequence, head) pairs: returns (o [n][dim], lse [n])."""
+    q, code = _raw(q, dtype)
+    k, _ = _raw(k, dtype)
+    v, _ = _raw(v, dtype)
+    ctx = np.ascontiguousarray(ctx, np.uint32)
+    sh = np.ascontiguousarray(seq_head, np.uint32).reshape(-1, 2)
+    scale = np.float32(1.0 / np.sqrt(dim)) if scale is None else scale
+    o = np.zeros((len(sh), dim), np.float64)
+    lse = np.zeros(len(sh), np.float64)
+    rc = lib(mutant).oracle_attn_decode_rows(batch, heads, kv_heads, dim, cap, scale, code, _p(q), _p(k), _p(v),
+                                             _p(ctx), _p(sh), len(sh), _p(o), _p(lse), nthreads)
+    if rc:
+        raise ValueError("oracle_attn_decode_rows: refused")
+    return o, lse
+
+
+def lse_merge(o_i, lse_i, mutant=None):
+    """Merges partial rows (o_i [n][dim] normalised, lse_i [n]) into (o [dim], lse)."""
+    o_i = np.ascontiguousarray(o_i, np.float64)
+    lse_i = np.ascontiguousarray(lse_i, np.float64)
+    n, dim = o_i.shape
+    o = np.zeros(dim, np.float64)
+    lse = np.zeros(1, np.float64)
+    lib(mutant).oracle_lse_merge(n, dim, _p(o_i), _p(lse_i), _p(o), _p(lse))
+    return o, float(lse[0])
+
+
+def to_f16_bits(x):
+    """float32 array -> float16 bit patterns (round to nearest even), by numpy."""
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def to_bf16_bits(x):
+    """float32 array -> bfloat16 bit patterns, round to nearest even (NaN kept quiet)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7F800000) == 0x7F800000
+    nan &= (u & 0x007FFFFF) != 0
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bits_to_f32(bits, dtype):
+    """float16 / bfloat16 bit patterns -> float32 (exact)."""
+    bits = np.asarray(bits, np.uint16)
+    if dtype == F16:
+        return bits.view(np.float16).astype(np.float32)
+    return (bits.astype(np.uint32) << 16).view(np.float32)

@@ -1,0 +1,285 @@
+"""Checks that pin the CPU oracle (oracle/attn_oracle.c) to facts it does not compute itself.
+
+Each check returns (ok, message) for a given oracle build (mutant=None is the real oracle; a mutant carries one
+planted mistake), so the same checks both pass on the oracle and are shown to fail on every mutant:
+  goldens        - the fixtures of tests/golden/ (explicit mask matrices + scipy softmax / logsumexp)
+  closed forms   - q = 0 gives the mean of the visible values and lse = log(count); one visible key gives its
+                   value row and lse = its score; no visible key gives 0 and lse = -inf
+  invariants     - GQA equals MHA with the kv heads repeated; block = 0 is bidirectional (invariant to permuting
+                   keys and values together); causal row i does not depend on keys past i
+  sparse         - all cubes selected equals dense over the valid keys; rows with map < 0 stay untouched
+  cube_select    - the order numpy's stable argsort of (-score) gives; local cubes lead without duplicates
+  decode, merge  - decode equals the dense rule at q_pos0 = ctx - 1; merging splits equals the whole row
+"""
+import glob
+import os
+
+import numpy as np
+from scipy.special import logsumexp, softmax
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+U32 = 0xFFFFFFFF
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _f16(x):
+    return O.to_f16_bits(x)
+
+
+def _close(a, b, tol=1e-9):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    same_inf = np.isinf(a) & np.isinf(b) & (np.sign(a) == np.sign(b))
+    with np.errstate(invalid="ignore"):
+        err = np.where(same_inf, 0.0, np.abs(a - b))
+    return bool(np.all(err <= tol * (1.0 + np.abs(np.where(same_inf, 0.0, b)))))
+
+
+def check_goldens(mutant=None):
+    bad = []
+    for f in sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))):
+        with np.load(f) as z:
+            g = {k: z[k] for k in z.files}
+        kind = str(g["kind"])
+        if kind == "dense":
+            n_q, q_pad, n_k, k_pad, heads, kv, q_pos0, block, width, dim, dt = [int(x) for x in g["args"]]
+            o, lse = O.attn_dense(g["q"], g["k"], g["v"], n_q=n_q, q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads,
+                                  kv_heads=kv, q_pos0=q_pos0, block=block, dim=dim, dtype=dt, mutant=mutant)
+        elif kind == "sparse":
+            n_q, q_pad, n_k, k_pad, heads, kv, width, cubes, kk, d0, d1, causal, sh, topk, dt = \
+                [int(x) for x in g["args"]]
+            o, lse = O.attn_sparse(g["q"], g["k"], g["v"], g["sel"], g["nsel"], g["valid"], g["map"], n_q=n_q,
+                                   q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads, kv_heads=kv, n_cubes=cubes,
+                                   max_sel=kk, dense0=d0, dense1=d1, causal=causal, sel_heads=sh, dtype=dt,
+                                   o_fill=np.full((q_pad, width), 12345.0), mutant=mutant)
+            lse = np.where(np.isnan(g["lse"]), np.nan, lse)
+        else:
+            batch, heads, kv, dim, cap, dt = [int(x) for x in g["args"]]
+            o, lse = O.attn_decode(g["q"], g["k"], g["v"], g["ctx"], batch=batch, heads=heads, kv_heads=kv,
+                                   dim=dim, cap=cap, dtype=dt, mutant=mutant)
+        ok_o = _close(o, g["o"], 2e-6)
+        gl = np.nan_to_num(g["lse"], nan=0.0)
+        ml = np.nan_to_num(lse, nan=0.0)
+        ok_l = _close(ml, gl, 2e-6)
+        if not (ok_o and ok_l):
+            bad.append(os.path.basename(f))
+    return not bad, f"golden mismatches: {bad}"
+
+
+def check_closed_forms(mutant=None):
+    msgs = []
+    rng = _rng(1)
+    heads, kv, dim, n = 2, 1, 64, 20
+    q_pad, k_pad = 64, 128
+    qz = np.zeros((heads, q_pad, dim), np.uint16)  # q = 0: every visible key weighs the same
+    k = _f16(rng.standard_normal((kv, k_pad, dim)))
+    v = _f16(rng.standard_normal((kv, k_pad, dim)))
+    vf = O.bits_to_f32(v, O.F16).astype(np.float64)
+    o, lse = O.attn_dense(qz, k, v, n_q=n, q_pad=q_pad, n_k=n, k_pad=k_pad, heads=heads, kv_heads=kv, q_pos0=0,
+                          block=U32, dim=dim, dtype=O.F16, mutant=mutant)
+    want = np.stack([vf[0, :r + 1].mean(0) for r in range(n)])
+    if not (_close(o[:, :dim], want) and _close(o[:, dim:], want)):
+        msgs.append("q=0 causal: not the mean of the visible values")
+    if not _close(lse, np.log(np.arange(1, n + 1))[None, :].repeat(heads, 0)):
+        msgs.append("q=0 causal: lse is not log(count)")
+    # one visible key: row 0 of a causal pass sees key 0 alone
+    q = _f16(rng.standard_normal((heads, q_pad, dim)))
+    qf = O.bits_to_f32(q, O.F16).astype(np.float64)
+    kf = O.bits_to_f32(k, O.F16).astype(np.float64)
+    o, lse = O.attn_dense(q, k, v, n_q=n, q_pad=q_pad, n_k=n, k_pad=k_pad, heads=heads, kv_heads=kv, q_pos0=0,
+                          block=U32, dim=dim, dtype=O.F16, mutant=mutant)
+    scale = float(np.float32(1 / np.sqrt(dim)))
+    if not _close(o[0, :dim], vf[0, 0]):
+        msgs.append("one visible key: output is not its value row")
+    if not _close(lse[:, 0], [qf[h, 0] @ kf[0, 0] * scale for h in range(heads)]):
+        msgs.append("one visible key: lse is not its score")
+    # no visible key: n_k = 0
+    o, lse = O.attn_dense(q, k, v, n_q=4, q_pad=q_pad, n_k=0, k_pad=k_pad, heads=heads, kv_heads=kv, q_pos0=0,
+                          block=U32, dim=dim, dtype=O.F16, mutant=mutant)
+    if not (np.all(o == 0) and np.all(np.isneginf(lse))):
+        msgs.append("no visible key: not 0 and -inf")
+    return not msgs, "; ".join(msgs)
+
+
+def check_invariants(mutant=None):
+    msgs = []
+    rng = _rng(2)
+    heads, kv, dim, n = 4, 2, 128, 70
+    q_pad, k_pad = 128, 128
+    q = _f16(rng.standard_normal((heads, q_pad, dim)))
+    k = _f16(rng.standard_normal((kv, k_pad, dim)))
+    v = _f16(rng.standard_normal((kv, k_pad, dim)))
+    common = dict(n_q=n, q_pad=q_pad, n_k=n, k_pad=k_pad, dim=dim, dtype=O.F16, mutant=mutant)
+    # GQA equals MHA over the kv heads repeated (head h reads kv head h / (heads / kv_heads))
+    o_g, l_g = O.attn_dense(q, k, v, heads=heads, kv_heads=kv, q_pos0=0, block=U32, **common)
+    kr, vr = np.repeat(k, heads // kv, axis=0), np.repeat(v, heads // kv, axis=0)
+    o_m, l_m = O.attn_dense(q, kr, vr, heads=heads, kv_heads=heads, q_pos0=0, block=U32, **common)
+    if not (_close(o_g, o_m) and _close(l_g, l_m)):
+        msgs.append("GQA differs from MHA with the kv heads repeated")
+    # block = 0: bidirectional, so permuting keys and values together changes nothing; and it matches scipy
+    o_b, l_b = O.attn_dense(q, k, v, heads=heads, kv_heads=kv, q_pos0=0, block=0, **common)
+    perm = np.concatenate([rng.permutation(n), np.arange(n, k_pad)])
+    o_p, l_p = O.attn_dense(q, k[:, perm], v[:, perm], heads=heads, kv_heads=kv, q_pos0=0, block=0, **common)
+    if not (_close(o_b, o_p) and _close(l_b, l_p)):
+        msgs.append("bidirectional output changes when keys and values are permuted together")
+    qf, kf, vf = (O.bits_to_f32(x, O.F16).astype(np.float64) for x in (q, k, v))
+    s = qf[0, :n] @ kf[0, :n].T * float(np.float32(1 / np.sqrt(dim)))
+    if not (_close(o_b[:, :dim], softmax(s, axis=1) @ vf[0, :n]) and _close(l_b[0], logsumexp(s, axis=1))):
+        msgs.append("bidirectional head 0 differs from scipy's softmax")
+    # causal: row i does not depend on keys and values past i
+    k2, v2 = k.copy(), v.copy()
+    cut = 30
+    k2[:, cut + 1:n] = _f16(rng.standard_normal((kv, n - cut - 1, dim)))
+    v2[:, cut + 1:n] = _f16(rng.standard_normal((kv, n - cut - 1, dim)))
+    o_c2, _ = O.attn_dense(q, k2, v2, heads=heads, kv_heads=kv, q_pos0=0, block=U32, **common)
+    if not _close(o_g[:cut + 1], o_c2[:cut + 1]):
+        msgs.append("causal rows depend on later keys")
+    if _close(o_g[cut + 1:], o_c2[cut + 1:]):
+        msgs.append("causal rows past the cut ignore their own keys")
+    # prefix-causal: rows >= block see all keys, rows below it are causal
+    blk = 25
+    o_x, _ = O.attn_dense(q, k, v, heads=heads, kv_heads=kv, q_pos0=0, block=blk, **common)
+    if not (_close(o_x[blk:], o_b[blk:]) and _close(o_x[:blk], o_g[:blk])):
+        msgs.append("prefix-causal rows differ from bidirectional / causal rows")
+    return not msgs, "; ".join(msgs)
+
+
+def check_sparse(mutant=None):
+    msgs = []
+    rng = _rng(3)
+    heads, kv, cubes, D = 2, 1, 3, 128
+    n = cubes * 64
+    q_pad = k_pad = 256
+    q = _f16(rng.standard_normal((heads, q_pad, D)))
+    k = _f16(rng.standard_normal((kv, k_pad, D)))
+    v = _f16(rng.standard_normal((kv, k_pad, D)))
+    valid = np.zeros(k_pad, np.uint8)
+    valid[:n] = 1
+    valid[40:44] = 0  # a few invalid keys
+    sel = np.tile(np.arange(cubes, dtype=np.uint16), (heads, cubes, 1))
+    nsel = np.full((heads, cubes), cubes, np.uint16)
+    map_ = np.where(np.arange(q_pad) < n, np.arange(q_pad), -1).astype(np.int32)
+    map_[7] = -1
+    fill = np.full((q_pad, heads * D), 12345.0)
+    o, _ = O.attn_sparse(q, k, v, sel, nsel, valid, map_, n_q=n, q_pad=q_pad, n_k=n, k_pad=k_pad, heads=heads,
+                         kv_heads=kv, n_cubes=cubes, max_sel=cubes, dense0=n, dense1=n, dtype=O.F16, o_fill=fill,
+                         mutant=mutant)
+    # dense bidirectional over the valid keys: mask invalid keys by zeroing them out of an explicit softmax
+    qf, kf, vf = (O.bits_to_f32(x, O.F16).astype(np.float64) for x in (q, k, v))
+    keys = np.nonzero(valid[:n])[0]
+    scale = float(np.float32(1 / np.sqrt(D)))
+    for h in range(heads):
+        s = qf[h, :n] @ kf[0, keys].T * scale
+        want = softmax(s, axis=1) @ vf[0, keys]
+        rows = np.array([r for r in range(n) if map_[r] >= 0])
+        if not _close(o[rows, h * D:(h + 1) * D], want[rows]):
+            msgs.append(f"all cubes selected: head {h} differs from dense over the valid keys")
+    if not np.all(o[7] == 12345.0) or not np.all(o[n:] == 12345.0):
+        msgs.append("rows with map < 0 or past n_q were written")
+    # dense rows respect validity too: a layout with dense rows, one of them invalid
+    cubes2, dense = 2, 40
+    n2 = cubes2 * 64 + dense
+    valid2 = np.zeros(k_pad, np.uint8)
+    valid2[:n2] = 1
+    valid2[cubes2 * 64 + 5] = 0
+    sel2 = np.tile(np.arange(cubes2, dtype=np.uint16), (heads, cubes2, 1))
+    nsel2 = np.full((heads, cubes2), cubes2, np.uint16)
+    map2 = np.where(np.arange(q_pad) < n2, np.arange(q_pad), -1).astype(np.int32)
+    o2, _ = O.attn_sparse(q, k, v, sel2, nsel2, valid2, map2, n_q=n2, q_pad=q_pad, n_k=n2, k_pad=k_pad,
+                          heads=heads, kv_heads=kv, n_cubes=cubes2, max_sel=cubes2, dense0=cubes2 * 64, dense1=n2,
+                          dtype=O.F16, mutant=mutant)
+    keys2 = np.nonzero(valid2[:n2])[0]
+    s = qf[0, :n2] @ kf[0, keys2].T * scale
+    if not _close(o2[:n2, :D], softmax(s, axis=1) @ vf[0, keys2]):
+        msgs.append("cubes plus dense rows differ from dense over the valid keys")
+    return not msgs, "; ".join(msgs)
+
+
+def check_cube_select(mutant=None):
+    msgs = []
+    rng = _rng(4)
+    heads, D, cubes = 2, 128, 7
+    q_pad = k_pad = cubes * 64
+    cnt = np.array([64, 64, 30, 64, 64, 1, 64], np.uint32)
+    q = _f16(rng.standard_normal((heads, q_pad, D)))
+    k = _f16(rng.standard_normal((heads, k_pad, D)))
+    rowmask = np.concatenate([np.arange(64) < c for c in cnt]).astype(np.float32)
+    q = _f16(O.bits_to_f32(q, O.F16) * rowmask[None, :, None])
+    k = _f16(O.bits_to_f32(k, O.F16) * rowmask[None, :, None])
+    for topk in (3, 9):
+        sel, nsel = O.cube_select(q, k, cnt, heads=heads, dim=D, q_pad=q_pad, k_pad=k_pad, n_cubes=cubes, topk=topk,
+                                  dtype=O.F16, mutant=mutant)
+        qf, kf = O.bits_to_f32(q, O.F16).astype(np.float64), O.bits_to_f32(k, O.F16).astype(np.float64)
+        kk = min(topk, cubes)
+        for h in range(heads):
+            qp = qf[h].reshape(cubes, 64, D).sum(1) / cnt[:, None]
+            kp = kf[h].reshape(cubes, 64, D).sum(1) / cnt[:, None]
+            sc = qp @ kp.T
+            want = np.argsort(-sc, axis=1, kind="stable")[:, :kk]
+            if not np.array_equal(sel[h], want) or not np.all(nsel[h] == kk):
+                msgs.append(f"top {topk}: head {h} differs from the stable sort")
+    # ties go to the smaller index: identical key cubes score the same
+    k_t = k.copy()
+    k_t[:, 3 * 64:4 * 64] = k_t[:, 1 * 64:2 * 64]
+    cnt_t = cnt.copy()
+    cnt_t[3] = cnt_t[1]
+    sel, _ = O.cube_select(q, k_t, cnt_t, heads=heads, dim=D, q_pad=q_pad, k_pad=k_pad, n_cubes=cubes, topk=cubes,
+                           dtype=O.F16, mutant=mutant)
+    for h in range(heads):
+        for qc in range(cubes):
+            row = list(sel[h, qc])
+            if row.index(1) > row.index(3):
+                msgs.append("a tie went to the larger index")
+                break
+    # local = 3, stride 1: the cube and its neighbours lead, no cube twice (tests/sparse_attn_test.cpp:183-207)
+    sel, _ = O.cube_select(q, k, cnt, heads=heads, dim=D, q_pad=q_pad, k_pad=k_pad, n_cubes=cubes, topk=4, local=3,
+                           stride=1, dtype=O.F16, mutant=mutant)
+    for h in range(heads):
+        for qc in range(cubes):
+            want = [qc] + ([qc - 1] if qc >= 1 else []) + ([qc + 1] if qc + 1 < cubes else [])
+            row = list(sel[h, qc])
+            if row[:len(want)] != want or len(set(row)) != len(row):
+                msgs.append(f"local cubes: head {h} cube {qc} gives {row}")
+    return not msgs, "; ".join(msgs)
+
+
+def check_decode_and_merge(mutant=None):
+    msgs = []
+    rng = _rng(5)
+    batch, heads, kv, dim, cap = 3, 4, 2, 128, 200
+    ctx = np.array([1, 77, 200], np.uint32)
+    q = _f16(rng.standard_normal((batch, heads, dim)))
+    k = _f16(rng.standard_normal((batch, kv, cap, dim)))
+    v = _f16(rng.standard_normal((batch, kv, cap, dim)))
+    o, lse = O.attn_decode(q, k, v, ctx, batch=batch, heads=heads, kv_heads=kv, dim=dim, cap=cap, dtype=O.F16,
+                           mutant=mutant)
+    for b in range(batch):
+        qt = np.zeros((heads, 64, dim), np.uint16)
+        qt[:, 0] = q[b]
+        od, ld = O.attn_dense(qt, k[b], v[b], n_q=1, q_pad=64, n_k=int(ctx[b]), k_pad=cap, heads=heads, kv_heads=kv,
+                              q_pos0=int(ctx[b]) - 1, block=U32, dim=dim, dtype=O.F16, mutant=mutant)
+        if not (_close(o[b], od[0]) and _close(lse[b], ld[:, 0])):
+            msgs.append(f"decode of sequence {b} differs from the dense row at q_pos0 = ctx - 1")
+    # merging splits of one row equals the whole row (scipy softmax over each split)
+    qf = O.bits_to_f32(q, O.F16).astype(np.float64)[2, 0]
+    kf = O.bits_to_f32(k, O.F16).astype(np.float64)[2, 0]
+    vf = O.bits_to_f32(v, O.F16).astype(np.float64)[2, 0]
+    s = kf @ qf * float(np.float32(1 / np.sqrt(dim)))
+    parts = [(0, 64), (64, 150), (150, 200)]
+    o_i = np.stack([softmax(s[a:b]) @ vf[a:b] for a, b in parts])
+    l_i = np.array([logsumexp(s[a:b]) for a, b in parts])
+    om, lm = O.lse_merge(o_i, l_i, mutant=mutant)
+    if not (_close(om, softmax(s) @ vf) and _close(lm, logsumexp(s))):
+        msgs.append("merging splits differs from the whole row")
+    om, lm = O.lse_merge(np.stack([o_i[0], o_i[0]]), np.array([l_i[0], l_i[0]]), mutant=mutant)
+    if not (_close(om, o_i[0]) and _close(lm, l_i[0] + np.log(2.0))):
+        msgs.append("merging two equal partials is not the same row with lse + log 2")
+    return not msgs, "; ".join(msgs)
+
+
+ALL_CHECKS = [check_goldens, check_closed_forms, check_invariants, check_sparse, check_cube_select,
+              check_decode_and_merge]
