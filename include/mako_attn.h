@@ -1,0 +1,142 @@
+/*
+ * mako_attn: the attention path of mako-common on MI355X (gfx950), as a C ABI.
+ *
+ * Each entry point replaces one kernel dispatch (or one group of dispatches) that the reference's
+ * TransformerRuntime encodes into a Metal command encoder; the reference interface it stands for is cited
+ * beside it. Buffers are device pointers (hipMalloc'd, or any device-resident memory), sizes are element
+ * counts, `stream` is a hipStream_t passed as void* (NULL: the default stream). Every call only enqueues
+ * work; results are visible once the stream is synchronised, as they were after Runtime::finish
+ * (src/gpu/runtime.cpp:453-475). Calls never throw; they return MAKO_OK or an error code, and
+ * mako_last_error() gives the message for the calling thread.
+ *
+ * Layouts (as the reference's tiles, src/models/runtime.hpp:90-111):
+ *   q    [heads][q_pad][dim]        query tiles, one head after another
+ *   k, v [kv_heads][k_pad][dim]     key / value tiles; head h reads kv head h / (heads / kv_heads)
+ *   o    [n_q][width]               head h at columns [h * dim, (h + 1) * dim); rows >= n_q untouched
+ *   lse  [heads][n_q] float          natural-log sum of exponentials of the scaled scores (may be NULL)
+ * Element types: q, k, v in f16 or bf16; o in f32 (the reference's output), or the input's type.
+ */
+#ifndef MAKO_ATTN_H
+#define MAKO_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MAKO_ATTN_ABI_VERSION 1
+
+typedef enum mako_dtype { MAKO_F32 = 0, MAKO_F16 = 1, MAKO_BF16 = 2 } mako_dtype;
+
+enum mako_status {
+    MAKO_OK = 0,
+    MAKO_EINVAL = 1,       /* arguments the reference refuses, or a precondition not met */
+    MAKO_EUNSUPPORTED = 2, /* a head width or element type with no kernel in this build */
+    MAKO_EWORKSPACE = 3,   /* workspace missing or smaller than the matching *_workspace() size */
+    MAKO_EHIP = 4          /* a HIP call failed (launch or stream error) */
+};
+
+/* AttnArgs, field for field (src/kernels/ops.metal:54-64; src/models/runtime.cpp:26-29). */
+typedef struct mako_attn_args {
+    uint32_t n_q;      /* queries */
+    uint32_t q_pad;    /* rows of a query head in q (>= n_q) */
+    uint32_t n_k;      /* keys */
+    uint32_t k_pad;    /* rows of a key / value head in k and v (>= n_k) */
+    uint32_t heads, kv_heads;
+    uint32_t q_pos0;   /* the position of query 0 among the keys */
+    uint32_t block;    /* positions from here on see each other both ways; below, causal (0: bidirectional,
+                          UINT32_MAX: causal) */
+    uint32_t width;    /* o row length in elements (>= heads * dim) */
+    float scale;       /* softmax scale, 1 / sqrt(dim) in the reference */
+} mako_attn_args;
+
+/* SparseAttnArgs (src/kernels/ops.metal:1029-1034; src/models/runtime.cpp:279-283) and two fields the
+ * reference does not have: causal (a key j is seen by tile row r only when j <= r) and sel_heads (the rows of
+ * sel / nsel: heads, one list per query head as cube_select writes them, or kv_heads, one list shared by the
+ * query heads of a group). */
+typedef struct mako_sparse_args {
+    uint32_t n_q, q_pad, n_k, k_pad, heads, kv_heads, width;
+    float scale;
+    uint32_t n_cubes; /* the first n_cubes 64-row query tiles are cubes */
+    uint32_t max_sel; /* entries a row of sel holds (min(topk, n_cubes)) */
+    uint32_t dense0, dense1;
+    uint32_t causal;
+    uint32_t sel_heads;
+} mako_sparse_args;
+
+/* Batched single-token decode against a contiguous KV cache (no counterpart struct in the reference). */
+typedef struct mako_decode_args {
+    uint32_t batch;   /* sequences */
+    uint32_t heads, kv_heads;
+    uint32_t dim;     /* 128 */
+    uint32_t cap;     /* rows of a kv head of one sequence in the cache (the cache's k_pad) */
+    uint32_t max_ctx; /* an upper bound on every ctx_len[b] (<= cap); sizes the split-K partials */
+    uint32_t split;   /* keys per split (a multiple of 64; 0: chosen by the library) */
+    float scale;
+} mako_decode_args;
+
+/* ABI version of the loaded library (MAKO_ATTN_ABI_VERSION it was built with). */
+int mako_attn_abi_version(void);
+
+/* The message of the calling thread's last failed call ("" after a success). */
+const char* mako_last_error(void);
+
+/*
+ * Dense flash attention: causal (block = UINT32_MAX), bidirectional (block = 0) or prefix-causal, GQA, one
+ * launch. Replaces TransformerRuntime::attention (src/models/runtime.hpp:90-95; src/models/runtime.cpp:262-273)
+ * and the kernels it dispatches, flash_attn_coop_{64,128}_32 and flash_attn_sg_256_16x32_4
+ * (src/kernels/ops.metal:106-214, 230-369). dim 64, 128 or 256; heads a multiple of kv_heads. Keys past n_k
+ * are masked (their rows need not be zero); fully masked rows give 0 and lse = -inf.
+ */
+int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
+                  const void* k, const void* v, void* o, float* lse, void* stream);
+
+/*
+ * Cube selection for block-sparse attention: per head and query cube, the topk key cubes by the dot product
+ * of the cubes' mean q and k. Replaces TransformerRuntime::cube_select (src/models/runtime.hpp:96-107;
+ * src/models/runtime.cpp:286-303) and cube_pool / cube_scores / cube_topk (src/kernels/ops.metal:926-1027).
+ * q [heads][q_pad][128], k [heads][k_pad][128] (f16 or bf16), cnt u32 [n_cubes]; writes sel u16
+ * [heads][n_cubes][min(topk, n_cubes)] and nsel u16 [heads][n_cubes]. workspace: at least
+ * mako_cube_select_workspace(heads, n_cubes) bytes of device memory. Refuses (MAKO_EINVAL) what the reference
+ * refuses: n_cubes > 4096, topk == 0, local not 0, 1 or 3.
+ */
+size_t mako_cube_select_workspace(uint32_t heads, uint32_t n_cubes);
+int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_cubes, uint32_t topk,
+                     uint32_t local, uint32_t stride, mako_dtype in, const void* q, const void* k,
+                     const uint32_t* cnt, uint16_t* sel, uint16_t* nsel, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Block-sparse attention over a pass list, D = 128. Replaces TransformerRuntime::attention_sparse
+ * (src/models/runtime.hpp:108-111; src/models/runtime.cpp:305-317) and flash_attn_sparse_128
+ * (src/kernels/ops.metal:1036-1185). Query tile t < n_cubes attends the 64-row key cubes sel lists for it and the
+ * dense rows [dense0, dense1); a later tile attends [0, n_k); keys with valid[j] == 0 are masked; query row r's
+ * output goes to o row map[r] (dropped when map[r] < 0). Requires q_pad % 64 == 0, k_pad % 128 == 0,
+ * dense0 % 32 == 0 (the reference's checks) and n_cubes * 64 <= k_pad. lse [heads][q_pad] by tile row (may be
+ * NULL).
+ */
+int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                     const void* v, void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
+                     const int32_t* map, float* lse, void* stream);
+
+/*
+ * Batched single-token decode, split-K over each sequence's context with fp32 partials merged by their LSE.
+ * New beside TransformerRuntime::attention: the reference decodes one sequence at a time through attention()
+ * with n_q = 1, q_pos0 = ctx - 1 (src/kernels/ops.metal:289), and its split-K primitive attn_pv
+ * (src/kernels/gemm.metal:683-730) leaves the softmax and the merge to its caller; this does all three.
+ * q [batch][heads][dim]; k, v [batch][kv_heads][cap][dim]; ctx_len u32 [batch] in device memory (sequence b
+ * attends keys [0, ctx_len[b]), ctx_len[b] <= max_ctx); o [batch][heads * dim]; lse [batch][heads] (may be
+ * NULL). workspace: at least mako_attn_decode_workspace(a) bytes of device memory.
+ */
+size_t mako_attn_decode_workspace(const mako_decode_args* a);
+int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                     const void* v, const uint32_t* ctx_len, void* o, float* lse, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,311 @@
+// Dense flash attention for gfx950: causal, bidirectional and prefix-causal (by `block`), GQA, head width 64,
+// 128 or 256, f16 or bf16 in, f32 / f16 / bf16 out, optional LSE.
+//
+// The semantics are those of the reference's flash_attn_coop (src/kernels/ops.metal:216-369): key j is visible
+// to query row r (position pos = q_pos0 + r) when j < n_k && (j <= pos || (pos >= block && j >= block))
+// (ops.metal:289); head h reads kv head h / (heads / kv_heads) (:242); the running maximum moves only when a
+// score passes it by 8 in the base-2 domain (:303-316), so most key blocks leave the output unscaled; P is
+// rounded to the input type for the P V product and the row sum adds the unrounded exponentials (:328-330); a
+// fully masked row gives 0 (:355); rows >= n_q are not stored (:359-362).
+//
+// The design is this one's own, for CDNA4:
+// * A workgroup is 4 waves (256 threads). Each wave owns 32 query rows of one head; the workgroup's waves cover
+//   hq query heads of one GQA group (hq = 4, 2 or 1) x 128 / hq rows, so every key / value tile staged in LDS
+//   serves all four waves.
+// * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16: Q (the B operand) stays in
+//   registers for the whole kernel, K rows (the A operand) come from LDS. In the 32x32 result each lane holds
+//   one query row (its column) and 16 keys, so the row's softmax is lane-local but for one exchange with lane
+//   l ^ 32, and the output rescale is one scalar per lane.
+// * K rows are stored in LDS with bits 2 and 3 of the row swapped within each 32 (slot_of); that makes the
+//   registers of S^T, once exponentiated and packed, exactly the B operand of O^T = V^T P^T for 16 consecutive
+//   keys, so P never goes through LDS.
+// * V is stored transposed in LDS (one row per head dimension, 64 keys, XOR-swizzled 16-byte chunks), written
+//   with an in-register 4x8 transpose, so the V^T operand is one 16-byte LDS read.
+// * K / V tiles of 64 keys are double-buffered in LDS; the next tile's global loads are issued before the
+//   current tile's products, and one barrier per tile orders the buffers.
+// * Workgroups are launched heaviest rows first (causal work grows with the row), and the grid's fastest index
+//   is the head group, so with 8 kv heads each XCD's L2 holds one kv head's K / V.
+#include "device.hpp"
+
+namespace mako {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kKB = 64;  // keys a tile
+constexpr float kRescale = 8.0f;
+
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    uint32_t n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, width;
+    float scale_log2;  // scale * log2(e)
+    uint32_t group;    // heads / kv_heads
+    uint32_t hq;       // query heads a workgroup (4, 2 or 1; divides group)
+    uint32_t rows_wg;  // query rows a workgroup (128 / hq)
+    uint32_t n_qblk;   // workgroups along the rows
+};
+
+// LDS slot of K row `row` of a tile: bits 2 and 3 swapped within each 32 rows.
+__device__ __forceinline__ uint32_t slot_of(uint32_t row)
+{
+    return (row & ~12u) | ((row & 4u) << 1) | ((row & 8u) >> 1);
+}
+
+// XOR swizzle of the 16-byte key chunks in row d of the transposed V tile.
+__device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d ^ (d >> 3)) & 7u; }
+
+// Element e (0..7) of a 16-byte chunk of 16-bit values.
+__device__ __forceinline__ uint32_t half_of(const u32x4& c, int e)
+{
+    const uint32_t w = c[e >> 1];
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+template <class T, class TO, int D>
+__global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const FwdParams p)
+{
+    using E = Elem<T>;
+    using V8 = typename E::vec8;
+    constexpr int KS = D + 8;                 // K row stride in LDS (elements): 16 bytes of padding
+    constexpr int VS = kKB;                   // V^T row stride (elements)
+    constexpr int CPR = D / 8;                // 16-byte chunks a row
+    constexpr int NV = kKB * CPR / kThreads;  // chunks a thread loads per tile, K and V each (= D / 32)
+    constexpr int NDB = D / 32;               // 32-wide head-dimension blocks of the output
+    constexpr int NKK = D / 16;               // 16-wide head-dimension steps of Q K^T
+    static_assert(NV * kThreads == kKB * CPR && (NV == 2 || NV == 4 || NV == 8), "tile split");
+    __shared__ __attribute__((aligned(16))) T ks[2][kKB * KS];
+    __shared__ __attribute__((aligned(16))) T vt[2][D * VS];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t g = lane >> 5, c32 = lane & 31;
+    const uint32_t hg = blockIdx.x;
+    const uint32_t qb = p.n_qblk - 1 - blockIdx.y;  // the latest rows (the most keys) first
+    const uint32_t h = hg * p.hq + w % p.hq;
+    const uint32_t kvh = hg * p.hq / p.group;
+    const uint32_t wg_q0 = qb * p.rows_wg;
+    const uint32_t q0 = wg_q0 + (w / p.hq) * 32;  // this wave's first row
+
+    // Keys the workgroup visits (the causal bound), and this wave's own bound.
+    const uint32_t wg_last = p.q_pos0 + min(wg_q0 + p.rows_wg, p.n_q) - 1;
+    const uint32_t n_keys = wg_last >= p.block ? p.n_k : min(p.n_k, wg_last + 1);
+    const bool live = q0 < p.n_q;
+    const uint32_t w_last = p.q_pos0 + min(q0 + 32, p.n_q) - 1;
+    const uint32_t w_keys = !live ? 0u : (w_last >= p.block ? p.n_k : min(p.n_k, w_last + 1));
+    const uint32_t p0 = p.q_pos0 + q0;  // the wave's first position
+    const uint32_t pos = p0 + c32;      // this lane's row's position
+
+    // Q: the B operand, lane (c32, g) holds row q0 + c32, head dims 16 kk + 8 g .. + 7.
+    V8 qreg[NKK];
+    {
+        const uint32_t row = q0 + c32;
+        const T* src = static_cast<const T*>(p.q) + ((size_t)h * p.q_pad + row) * D + 8 * g;
+        for (int kk = 0; kk < NKK; ++kk)
+            qreg[kk] = row < p.n_q ? *reinterpret_cast<const V8*>(src + 16 * kk) : V8{};
+    }
+
+    const T* kbase = static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * D;
+    const T* vbase = static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * D;
+    // V loads: thread -> head-dim chunk cc and NV consecutive keys from NV * kg (kg XOR-ed by the half row so
+    // that the transposed LDS writes of a 16-lane group spread over the banks).
+    const uint32_t v_cc = tid % CPR;
+    const uint32_t v_kg = (tid / CPR) ^ ((tid / (CPR / 2)) & 1u);
+    u32x4 kreg[NV], vreg[NV];
+
+    auto load_tile = [&](uint32_t j0) {
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = tid + kThreads * i, row = c / CPR, col = c % CPR, key = j0 + row;
+            kreg[i] = key < p.n_k ? *reinterpret_cast<const u32x4*>(kbase + (size_t)key * D + col * 8) : u32x4{};
+        }
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t key = j0 + NV * v_kg + i;
+            vreg[i] = key < p.n_k ? *reinterpret_cast<const u32x4*>(vbase + (size_t)key * D + v_cc * 8) : u32x4{};
+        }
+    };
+    auto store_tile = [&](int buf) {
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = tid + kThreads * i, row = c / CPR, col = c % CPR;
+            *reinterpret_cast<u32x4*>(&ks[buf][slot_of(row) * KS + col * 8]) = kreg[i];
+        }
+        const uint32_t key0 = NV * v_kg, kc = key0 / 8, off = key0 % 8;
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t d = v_cc * 8 + e;
+            T* dst = &vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off];
+            if constexpr (NV == 2) {
+                *reinterpret_cast<uint32_t*>(dst) = half_of(vreg[0], e) | (half_of(vreg[1], e) << 16);
+            } else if constexpr (NV == 4) {
+                *reinterpret_cast<u32x2*>(dst) = u32x2{half_of(vreg[0], e) | (half_of(vreg[1], e) << 16),
+                                                       half_of(vreg[2], e) | (half_of(vreg[3], e) << 16)};
+            } else {
+                *reinterpret_cast<u32x4*>(dst) = u32x4{half_of(vreg[0], e) | (half_of(vreg[1], e) << 16),
+                                                       half_of(vreg[2], e) | (half_of(vreg[3], e) << 16),
+                                                       half_of(vreg[4], e) | (half_of(vreg[5], e) << 16),
+                                                       half_of(vreg[6], e) | (half_of(vreg[7], e) << 16)};
+            }
+        }
+    };
+
+    f32x16 oacc[NDB];
+    for (int db = 0; db < NDB; ++db)
+        oacc[db] = f32x16{};
+    float m = -INFINITY, l = 0.0f;  // running maximum (base-2 domain) and sum of this lane's keys
+    const float c = p.scale_log2;
+
+    const uint32_t nb = (n_keys + kKB - 1) / kKB;
+    if (nb > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (uint32_t jb = 0; jb < nb; ++jb) {
+        const int buf = jb & 1;
+        const uint32_t j0 = jb * kKB;
+        if (jb + 1 < nb)
+            load_tile(j0 + kKB);
+        if (j0 < w_keys) {
+            // S^T for keys j0 .. j0 + 63: two 32x32 tiles; register r of tile t holds key
+            // j0 + 32 t + 16 (r / 8) + 8 g + r % 8 for this lane's row.
+            f32x16 s[2];
+            for (int t = 0; t < 2; ++t) {
+                s[t] = f32x16{};
+                const T* kr = &ks[buf][(32 * t + c32) * KS + 8 * g];
+                for (int kk = 0; kk < NKK; ++kk)
+                    s[t] = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s[t]);
+            }
+            const bool plain = j0 + kKB <= p.n_k && (j0 + kKB - 1 <= p0 || (p0 >= p.block && j0 >= p.block));
+            float mx = -INFINITY;
+            for (int t = 0; t < 2; ++t)
+                for (int r = 0; r < 16; ++r) {
+                    float x = s[t][r];
+                    if (!plain) {
+                        const uint32_t j = j0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
+                        if (!(j < p.n_k && (j <= pos || (pos >= p.block && j >= p.block))))
+                            x = -INFINITY;
+                        s[t][r] = x;
+                    }
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, swap_halves(mx)) * c;  // the row's maximum, base 2 (c > 0)
+            float f = 1.0f;
+            if (mx > m + kRescale) {
+                f = exp2f(m - mx);  // 0 while nothing was seen
+                m = mx;
+            }
+            l *= f;
+            if (__any(f != 1.0f))
+                for (int db = 0; db < NDB; ++db)
+                    for (int r = 0; r < 16; ++r)
+                        oacc[db][r] *= f;
+            const float mu = m == -INFINITY ? 0.0f : m;
+            // P in the input type, packed as the B operand of O^T += V^T P^T: chunk 2 t + a holds keys
+            // j0 + 32 t + 16 a + 8 g + 0..7 of this lane's row.
+            V8 pb[4];
+            for (int t = 0; t < 2; ++t)
+                for (int a = 0; a < 2; ++a) {
+                    u32x4 pk;
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const float e0 = exp2f(fmaf(s[t][8 * a + 2 * jj], c, -mu));
+                        const float e1 = exp2f(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
+                        l += e0 + e1;
+                        pk[jj] = E::pack2(e0, e1);
+                    }
+                    pb[2 * t + a] = __builtin_bit_cast(V8, pk);
+                }
+            for (int cc = 0; cc < 4; ++cc)
+                for (int db = 0; db < NDB; ++db) {
+                    const uint32_t d = 32 * db + c32;
+                    const T* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
+                    oacc[db] = E::mfma32(*reinterpret_cast<const V8*>(vr), pb[cc], oacc[db]);
+                }
+        }
+        if (jb + 1 < nb)
+            store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // The row's sum over both halves of the wave; normalise and store. Register r of output block db holds head
+    // dim 32 db + 8 (r / 4) + 4 g + r % 4.
+    const float lt = l + swap_halves(l);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const uint32_t row = q0 + c32;
+    if (live && row < p.n_q) {
+        TO* orow = static_cast<TO*>(p.o) + (size_t)row * p.width + (size_t)h * D;
+        for (int db = 0; db < NDB; ++db)
+            for (int r4 = 0; r4 < 4; ++r4)
+                store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
+                           oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
+        if (p.lse && g == 0)
+            p.lse[(size_t)h * p.n_q + row] = lt > 0.0f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
+    }
+}
+
+template <class T, class TO>
+void launch_d(uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
+{
+    switch (dim) {
+    case 64:
+        hipLaunchKernelGGL((flash_fwd<T, TO, 64>), grid, dim3(kThreads), 0, s, p);
+        break;
+    case 128:
+        hipLaunchKernelGGL((flash_fwd<T, TO, 128>), grid, dim3(kThreads), 0, s, p);
+        break;
+    default:
+        hipLaunchKernelGGL((flash_fwd<T, TO, 256>), grid, dim3(kThreads), 0, s, p);
+        break;
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace mako
+
+using namespace mako;
+
+extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
+                             const void* k, const void* v, void* o, float* lse, void* stream)
+{
+    if (!a || !q || !k || !v || !o)
+        return fail(MAKO_EINVAL, "attention: a null argument");
+    if (dim != 64 && dim != 128 && dim != 256)
+        return fail(MAKO_EUNSUPPORTED, "attention: heads of %u", dim);
+    if (in != MAKO_F16 && in != MAKO_BF16)
+        return fail(MAKO_EUNSUPPORTED, "attention: input type %d (f16 or bf16)", (int)in);
+    if (out != MAKO_F32 && out != in)
+        return fail(MAKO_EUNSUPPORTED, "attention: output type %d (f32 or the input's)", (int)out);
+    if (!a->heads || !a->kv_heads || a->heads % a->kv_heads)
+        return fail(MAKO_EINVAL, "attention: %u heads over %u kv heads", a->heads, a->kv_heads);
+    if (a->n_q > a->q_pad || a->n_k > a->k_pad)
+        return fail(MAKO_EINVAL, "attention: %u queries in %u rows, %u keys in %u rows", a->n_q, a->q_pad, a->n_k,
+                    a->k_pad);
+    if ((uint64_t)a->heads * dim > a->width || a->width % 4)
+        return fail(MAKO_EINVAL, "attention: o rows of %u for %u heads of %u (a multiple of 4, at least their width)",
+                    a->width, a->heads, dim);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return fail(MAKO_EINVAL, "attention: q, k, v and o must be 16-byte aligned");
+    if (a->n_q == 0)
+        return ok();
+    const uint32_t group = a->heads / a->kv_heads;
+    const uint32_t hq = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    FwdParams p{q, k, v, o, lse, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads, a->kv_heads, a->q_pos0, a->block,
+                a->width, a->scale * kLog2e, group, hq, 128 / hq, 0};
+    p.n_qblk = (a->n_q + p.rows_wg - 1) / p.rows_wg;
+    if (p.n_qblk > 65535)
+        return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
+    const dim3 grid(a->heads / hq, p.n_qblk);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (in == MAKO_BF16) {
+        if (out == MAKO_F32)
+            launch_d<__bf16, float>(dim, p, grid, s);
+        else
+            launch_d<__bf16, __bf16>(dim, p, grid, s);
+    } else {
+        if (out == MAKO_F32)
+            launch_d<_Float16, float>(dim, p, grid, s);
+        else
+            launch_d<_Float16, _Float16>(dim, p, grid, s);
+    }
+    return check_launch("attention");
+}

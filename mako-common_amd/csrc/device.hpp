@@ -1,0 +1,106 @@
+// Device helpers shared by the attention kernels: vector types, the gfx950 MFMA wrappers per element type,
+// conversions, and the error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mako_attn.h"
+
+namespace mako {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Per input element type: the 8-wide operand of v_mfma_f32_32x32x16_{bf16,f16} and two floats packed into one
+// dword (round to nearest even).
+template <class T>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+    using vec8 = bf16x8;
+    static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c)
+    {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float lo, float hi)
+    {
+        bf16x2 v = {(__bf16)lo, (__bf16)hi};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+};
+
+template <>
+struct Elem<_Float16> {
+    using vec8 = f16x8;
+    static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c)
+    {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float lo, float hi)
+    {
+        f16x2 v = {(_Float16)lo, (_Float16)hi};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+};
+
+// Output stores: four consecutive floats of one row as the output type.
+template <class TO>
+__device__ __forceinline__ void store4(TO* p, float a, float b, float c, float d);
+
+template <>
+__device__ __forceinline__ void store4<float>(float* p, float a, float b, float c, float d)
+{
+    *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
+}
+
+template <>
+__device__ __forceinline__ void store4<__bf16>(__bf16* p, float a, float b, float c, float d)
+{
+    *reinterpret_cast<u32x2*>(p) = u32x2{Elem<__bf16>::pack2(a, b), Elem<__bf16>::pack2(c, d)};
+}
+
+template <>
+__device__ __forceinline__ void store4<_Float16>(_Float16* p, float a, float b, float c, float d)
+{
+    *reinterpret_cast<u32x2*>(p) = u32x2{Elem<_Float16>::pack2(a, b), Elem<_Float16>::pack2(c, d)};
+}
+
+template <class T>
+__device__ __forceinline__ float to_float(T x)
+{
+    return (float)x;
+}
+
+// The other half of a 64-lane wave (lane l <-> l ^ 32).
+__device__ __forceinline__ float swap_halves(float x)
+{
+    return __shfl_xor(x, 32);
+}
+
+__device__ __forceinline__ uint32_t as_u32(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+}  // namespace mako
+
+// ---- host side: error plumbing of the C ABI ----------------------------------------------------------------------
+
+namespace mako {
+
+// Records the message for mako_last_error() and returns code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the message; returns MAKO_OK.
+int ok();
+// MAKO_OK, or MAKO_EHIP with the launch error recorded (hipGetLastError after a launch).
+int check_launch(const char* what);
+
+}  // namespace mako

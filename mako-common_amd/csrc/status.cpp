@@ -1,0 +1,45 @@
+// The C ABI's error plumbing: a per-thread message for mako_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "mako_attn.h"
+
+namespace mako {
+
+namespace {
+thread_local std::string last_error;
+}
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    last_error = buf;
+    return code;
+}
+
+int ok()
+{
+    last_error.clear();
+    return MAKO_OK;
+}
+
+int check_launch(const char* what)
+{
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(MAKO_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+}  // namespace mako
+
+extern "C" int mako_attn_abi_version(void) { return MAKO_ATTN_ABI_VERSION; }
+
+extern "C" const char* mako_last_error(void) { return mako::last_error.c_str(); }

@@ -1,0 +1,138 @@
+"""Python binding of the C ABI in include/mako_attn.h (lib/libmako_attn.so), for the tests and the benchmark.
+
+Tensors are torch tensors on the GPU (torch supplies device memory and streams here: plumbing, not compute).
+Every call goes through the HIP kernels of libmako_attn.so; there is no fallback: a missing library raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libmako_attn.so")
+
+F32, F16, BF16 = 0, 1, 2
+OK, EINVAL, EUNSUPPORTED, EWORKSPACE, EHIP = 0, 1, 2, 3, 4
+U32_MAX = 0xFFFFFFFF
+
+# Every symbol include/mako_attn.h declares.
+EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
+           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode")
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("n_q", "q_pad", "n_k", "k_pad", "heads", "kv_heads", "q_pos0",
+                                               "block", "width")] + [("scale", ctypes.c_float)]
+
+
+class SparseArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("n_q", "q_pad", "n_k", "k_pad", "heads", "kv_heads", "width")] + \
+        [("scale", ctypes.c_float)] + \
+        [(n, ctypes.c_uint32) for n in ("n_cubes", "max_sel", "dense0", "dense1", "causal", "sel_heads")]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("batch", "heads", "kv_heads", "dim", "cap", "max_ctx", "split")] + \
+        [("scale", ctypes.c_float)]
+
+
+class MakoError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises when it has not been built (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it (python -c 'import __graft_entry__ as g; g.build()')")
+        L = ctypes.CDLL(LIB_PATH)
+        P, U32, I, SZ = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_size_t
+        L.mako_attn_abi_version.restype = I
+        L.mako_last_error.restype = ctypes.c_char_p
+        L.mako_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), U32, I, I, P, P, P, P, P, P]
+        L.mako_cube_select_workspace.argtypes = [U32, U32]
+        L.mako_cube_select_workspace.restype = SZ
+        L.mako_cube_select.argtypes = [U32, U32, U32, U32, U32, U32, U32, I, P, P, P, P, P, P, SZ, P]
+        L.mako_attn_sparse.argtypes = [ctypes.POINTER(SparseArgs), I, I, P, P, P, P, P, P, P, P, P, P]
+        L.mako_attn_decode_workspace.argtypes = [ctypes.POINTER(DecodeArgs)]
+        L.mako_attn_decode_workspace.restype = SZ
+        L.mako_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P, SZ, P]
+        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode"):
+            getattr(L, name).restype = I
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != OK:
+        raise MakoError(rc, lib().mako_last_error().decode())
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(stream)
+
+
+def dtype_code(t):
+    import torch
+
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[t.dtype]
+
+
+def attn_fwd(q, k, v, o, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, lse=None, scale=None,
+             width=None, stream=None):
+    """mako_attn_fwd on torch tensors q [heads][q_pad][dim], k, v [kv_heads][k_pad][dim], o [n_q][width]."""
+    width = heads * dim if width is None else width
+    scale = 1.0 / dim ** 0.5 if scale is None else scale
+    a = AttnArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block & U32_MAX, width, scale)
+    _check(lib().mako_attn_fwd(ctypes.byref(a), dim, dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v),
+                               _ptr(o), _ptr(lse), _stream(stream)))
+
+
+def cube_select_workspace(heads, n_cubes):
+    return lib().mako_cube_select_workspace(heads, n_cubes)
+
+
+def cube_select(q, k, cnt, sel, nsel, workspace, *, heads, q_pad, k_pad, n_cubes, topk, local=0, stride=0,
+                stream=None):
+    _check(lib().mako_cube_select(heads, q_pad, k_pad, n_cubes, topk, local, stride, dtype_code(q), _ptr(q), _ptr(k),
+                                  _ptr(cnt), _ptr(sel), _ptr(nsel), _ptr(workspace),
+                                  0 if workspace is None else workspace.numel() * workspace.element_size(),
+                                  _stream(stream)))
+
+
+def attn_sparse(q, k, v, o, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, n_cubes, max_sel,
+                dense0, dense1, causal=0, sel_heads=None, width=None, lse=None, stream=None):
+    width = heads * 128 if width is None else width
+    sel_heads = heads if sel_heads is None else sel_heads
+    a = SparseArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, width, 1.0 / 128 ** 0.5, n_cubes, max_sel, dense0,
+                   dense1, causal, sel_heads)
+    _check(lib().mako_attn_sparse(ctypes.byref(a), dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v), _ptr(o),
+                                  _ptr(sel), _ptr(nsel), _ptr(valid), _ptr(map_), _ptr(lse), _stream(stream)))
+
+
+def decode_args(*, batch, heads, kv_heads, dim, cap, max_ctx, split=0, scale=None):
+    scale = 1.0 / dim ** 0.5 if scale is None else scale
+    return DecodeArgs(batch, heads, kv_heads, dim, cap, max_ctx, split, scale)
+
+
+def decode_workspace(a):
+    return lib().mako_attn_decode_workspace(ctypes.byref(a))
+
+
+def attn_decode(a, q, k, v, ctx_len, o, workspace, *, lse=None, stream=None):
+    _check(lib().mako_attn_decode(ctypes.byref(a), dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v),
+                                  _ptr(ctx_len), _ptr(o), _ptr(lse), _ptr(workspace),
+                                  0 if workspace is None else workspace.numel() * workspace.element_size(),
+                                  _stream(stream)))

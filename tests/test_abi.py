@@ -1,0 +1,60 @@
+"""The C ABI without a GPU: the library loads, exports every function include/mako_attn.h declares, reports its
+ABI version, and refuses bad arguments (with the reference's messages) before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+import mako_attn as M
+
+HEADER = os.path.join(ROOT, "include", "mako_attn.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:int|size_t|const char\*)\s+(mako_\w+)\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert declared() == sorted(M.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = M.lib()
+    for name in declared():
+        assert hasattr(L, name), f"{name} is declared in include/mako_attn.h but not exported"
+    assert L.mako_attn_abi_version() == 1
+
+
+FAKE = ctypes.c_void_p(0x10000)  # aligned, never dereferenced: every call below fails validation first
+
+
+def fwd_rc(**kw):
+    a = dict(n_q=64, q_pad=64, n_k=64, k_pad=128, heads=4, kv_heads=2, q_pos0=0, block=0xFFFFFFFF, width=512,
+             scale=0.088)
+    a.update(kw.pop("args", {}))
+    args = M.AttnArgs(*[a[f] for f, _ in M.AttnArgs._fields_])
+    dim = kw.pop("dim", 128)
+    i, o = kw.pop("in_", M.BF16), kw.pop("out", M.BF16)
+    ptrs = [kw.pop(n, FAKE) for n in ("q", "k", "v", "o")]
+    rc = M.lib().mako_attn_fwd(ctypes.byref(args), dim, i, o, *ptrs, None, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dim=96), M.EUNSUPPORTED, "attention: heads of 96"),
+    (dict(in_=M.F32), M.EUNSUPPORTED, "input type"),
+    (dict(out=M.F16), M.EUNSUPPORTED, "output type"),
+    (dict(args=dict(heads=5)), M.EINVAL, "heads over"),
+    (dict(args=dict(n_q=65)), M.EINVAL, "queries in"),
+    (dict(args=dict(n_k=129)), M.EINVAL, "keys in"),
+    (dict(args=dict(width=256)), M.EINVAL, "o rows"),
+    (dict(q=None), M.EINVAL, "null"),
+    (dict(k=ctypes.c_void_p(0x10002)), M.EINVAL, "aligned"),
+])
+def test_fwd_refuses(kw, code, msg):
+    rc, err = fwd_rc(**kw)
+    assert rc == code and msg in err, (rc, err)

@@ -1,0 +1,137 @@
+"""Dense flash attention (mako_attn_fwd) on the GPU against the CPU oracle: the golden fixtures, the f16 S512
+causal GQA case in full, a sweep of masks / head widths / GQA groups / ragged sizes, untouched rows past n_q,
+and sampled rows of the Qwen3-8B-shape causal prefill (S4096) and the bidirectional S16384 case."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import golden_files, load_golden
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import gpu_util as G  # noqa: E402
+import mako_attn as M  # noqa: E402
+
+U32 = 0xFFFFFFFF
+
+
+def run_fwd(qb, kb, vb, dtype, out, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, o_rows=None,
+            fill=None):
+    q, k, v = G.to_dev(qb, dtype), G.to_dev(kb, dtype), G.to_dev(vb, dtype)
+    o_rows = n_q if o_rows is None else o_rows
+    odt = torch.float32 if out == O.F32 else G.TORCH[dtype]
+    o = torch.full((o_rows, heads * dim), float(fill) if fill is not None else float("nan"), dtype=odt,
+                   device="cuda")
+    lse = torch.full((heads, max(n_q, 1)), float("nan"), dtype=torch.float32, device="cuda")
+    M.attn_fwd(q, k, v, o, n_q=n_q, q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads, kv_heads=kv_heads,
+               q_pos0=q_pos0, block=block, dim=dim, lse=lse)
+    torch.cuda.synchronize()
+    return G.to_host(o), lse.cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("path", golden_files("dense"), ids=lambda p: p.split("/")[-1][:-4])
+@pytest.mark.parametrize("out", ["f32", "same"])
+def test_golden(path, out):
+    g = load_golden(path)
+    n_q, q_pad, n_k, k_pad, heads, kv, q_pos0, block, width, dim, dt = [int(x) for x in g["args"]]
+    print(f"golden {path.split('/')[-1]} out={out}", flush=True)
+    o, lse = run_fwd(g["q"], g["k"], g["v"], dt, O.F32 if out == "f32" else dt, n_q=n_q, q_pad=q_pad, n_k=n_k,
+                     k_pad=k_pad, heads=heads, kv_heads=kv, q_pos0=q_pos0, block=block, dim=dim)
+    G.assert_attn_close(o, g["o"], "output")
+    G.assert_lse_close(lse[:, :n_q], g["lse"], "lse")
+
+
+def test_causal_gqa_s512_f16_full():
+    """Batch 1, 16 query heads over 8 kv heads, D 128, S 512, f16 in, f32 out + LSE: every row."""
+    rng = np.random.default_rng(1234)
+    heads, kv, dim, S = 16, 8, 128, 512
+    qb, kb, vb = (G.randn_bits(rng, (h, S, dim), O.F16) for h in (heads, kv, kv))
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=heads, kv_heads=kv, q_pos0=0, block=U32, dim=dim)
+    print("causal S512 f16", flush=True)
+    o, lse = run_fwd(qb, kb, vb, O.F16, O.F32, **args)
+    want_o, want_l = O.attn_dense(qb, kb, vb, dtype=O.F16, **args)
+    G.assert_attn_close(o, want_o, "output")
+    G.assert_rows_l2(o, want_o, "output", dim)
+    G.assert_lse_close(lse, want_l, "lse")
+
+
+SWEEP = [
+    # heads, kv, dim, n_q, n_k, q_pos0, block, dtype, out
+    (4, 4, 128, 200, 200, 0, 0, O.BF16, "same"),        # bidirectional MHA, ragged
+    (8, 2, 128, 257, 257, 0, U32, O.BF16, "f32"),       # causal, group 4, one row past a tile
+    (6, 2, 128, 96, 96, 0, U32, O.F16, "same"),         # group 3 (hq 1)
+    (4, 2, 128, 100, 300, 200, U32, O.F16, "f32"),      # chunked prefill: queries late in the keys
+    (2, 1, 128, 150, 150, 0, 64, O.BF16, "f32"),        # prefix-causal
+    (2, 1, 128, 150, 150, 0, 77, O.F16, "same"),        # prefix-causal, block inside a tile
+    (16, 2, 64, 130, 130, 0, U32, O.F16, "f32"),        # D 64, group 8
+    (4, 4, 64, 70, 333, 0, 0, O.BF16, "same"),          # D 64, more keys than queries
+    (2, 2, 256, 80, 80, 0, U32, O.BF16, "f32"),         # D 256
+    (4, 1, 256, 65, 129, 64, U32, O.F16, "same"),       # D 256, group 4, offset
+    (2, 2, 128, 1, 1000, 999, U32, O.BF16, "f32"),      # one query (decode through attention())
+    (2, 1, 128, 40, 5, 0, U32, O.F16, "f32"),           # fewer keys than queries: later rows see n_k keys
+]
+
+
+@pytest.mark.parametrize("case", SWEEP, ids=lambda c: "h{}kv{}d{}q{}k{}p{}b{}".format(*c[:6], "c" if c[6] == U32
+                                                                                      else c[6]))
+def test_sweep(case):
+    heads, kv, dim, n_q, n_k, q_pos0, block, dt, out = case
+    rng = np.random.default_rng(hash(case) & 0xFFFF)
+    q_pad, k_pad = (n_q + 63) // 64 * 64, (n_k + 127) // 128 * 128
+    qb = G.randn_bits(rng, (heads, q_pad, dim), dt)
+    kb = G.randn_bits(rng, (kv, k_pad, dim), dt)
+    vb = G.randn_bits(rng, (kv, k_pad, dim), dt)
+    # garbage past n_k: the kernel must mask, not rely on zero padding
+    kb[:, n_k:] = G.bits(np.full((kv, k_pad - n_k, dim), 3e4, np.float32), dt)
+    vb[:, n_k:] = G.bits(np.full((kv, k_pad - n_k, dim), np.nan, np.float32), dt)
+    args = dict(n_q=n_q, q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads, kv_heads=kv, q_pos0=q_pos0, block=block,
+                dim=dim)
+    print(f"sweep {case}", flush=True)
+    o, lse = run_fwd(qb, kb, vb, dt, O.F32 if out == "f32" else dt, o_rows=q_pad, fill=12345.0, **args)
+    want_o, want_l = O.attn_dense(qb, kb, vb, dtype=dt, **args)
+    G.assert_attn_close(o[:n_q], want_o, "output")
+    G.assert_lse_close(lse, want_l, "lse")
+    assert np.all(o[n_q:] == 12345.0), "rows past n_q were written"
+
+
+def _sampled(heads, kv, dim, S, block, dt, n_rows, seed):
+    rng = np.random.default_rng(seed)
+    qb, kb, vb = (G.randn_bits(rng, (h, S, dim), dt) for h in (heads, kv, kv))
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=heads, kv_heads=kv, q_pos0=0, block=block, dim=dim)
+    o, lse = run_fwd(qb, kb, vb, dt, dt, **args)
+    rows = np.concatenate([[0, 1, 31, 32, 63, 64, S - 1], rng.integers(0, S, n_rows)])
+    hr = np.stack([rng.integers(0, heads, len(rows)), rows], 1).astype(np.uint32)
+    want_o, want_l = O.attn_dense_rows(qb, kb, vb, hr, dtype=dt, **args)
+    got_o = np.stack([o[r, h * dim:(h + 1) * dim] for h, r in hr])
+    got_l = np.array([lse[h, r] for h, r in hr])
+    G.assert_attn_close(got_o, want_o, "sampled output")
+    G.assert_rows_l2(got_o, want_o, "sampled output", dim)
+    G.assert_lse_close(got_l, want_l, "sampled lse")
+    return o
+
+
+def test_qwen3_8b_causal_s4096_bf16_sampled():
+    """32 query heads over 8 kv heads, D 128, S 4096, causal, bf16 in and out: sampled rows against the oracle."""
+    print("causal S4096 bf16", flush=True)
+    _sampled(32, 8, 128, 4096, U32, O.BF16, 300, 4096)
+
+
+def test_bidirectional_s16384_bf16_sampled():
+    """24 heads MHA, D 128, S 16384, bidirectional, bf16 in and out: sampled rows against the oracle."""
+    print("bidirectional S16384 bf16", flush=True)
+    _sampled(24, 24, 128, 16384, 0, O.BF16, 60, 16384)
+
+
+def test_deterministic_and_row_independent():
+    """The same call twice gives identical bits; a row computed in a short call equals the same row in a long one
+    (the reference's row-invariance style, tests/gemv_rows_test.cpp:1-2)."""
+    rng = np.random.default_rng(7)
+    heads, kv, dim, S = 8, 2, 128, 640
+    qb, kb, vb = (G.randn_bits(rng, (h, S, dim), O.BF16) for h in (heads, kv, kv))
+    args = dict(q_pad=S, k_pad=S, heads=heads, kv_heads=kv, q_pos0=0, block=0, dim=dim)
+    o1, l1 = run_fwd(qb, kb, vb, O.BF16, O.F32, n_q=S, n_k=S, **args)
+    o2, l2 = run_fwd(qb, kb, vb, O.BF16, O.F32, n_q=S, n_k=S, **args)
+    assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+    o3, _ = run_fwd(qb, kb, vb, O.BF16, O.F32, n_q=33, n_k=S, **args)
+    assert np.array_equal(o3, o1[:33])
