@@ -127,7 +127,7 @@ int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, c
  * with n_q = 1, q_pos0 = ctx - 1 (src/kernels/ops.metal:289), and its split-K primitive attn_pv
  * (src/kernels/gemm.metal:683-730) leaves the softmax and the merge to its caller; this does all three.
  * q [batch][heads][dim]; k, v [batch][kv_heads][cap][dim]; ctx_len u32 [batch] in device memory (sequence b
- * attends keys [0, ctx_len[b]), ctx_len[b] <= max_ctx); o [batch][heads * dim]; lse [batch][heads] (may be
+ * attends keys [0, min(ctx_len[b], max_ctx))); o [batch][heads * dim]; lse [batch][heads] (may be
  * NULL). workspace: at least mako_attn_decode_workspace(a) bytes of device memory.
  */
 size_t mako_attn_decode_workspace(const mako_decode_args* a);

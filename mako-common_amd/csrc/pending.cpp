@@ -17,9 +17,3 @@ extern "C" int mako_attn_sparse(const mako_sparse_args*, mako_dtype, mako_dtype,
 {
     return fail(MAKO_EUNSUPPORTED, "attention_sparse: not in this build");
 }
-extern "C" size_t mako_attn_decode_workspace(const mako_decode_args*) { return 0; }
-extern "C" int mako_attn_decode(const mako_decode_args*, mako_dtype, mako_dtype, const void*, const void*,
-                                const void*, const uint32_t*, void*, float*, void*, size_t, void*)
-{
-    return fail(MAKO_EUNSUPPORTED, "attention_decode: not in this build");
-}
