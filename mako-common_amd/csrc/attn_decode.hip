@@ -3,7 +3,8 @@
 // Semantics: sequence b's one query row sits at position ctx[b] - 1 and sees keys [0, ctx[b]) (the reference's
 // mask rule, src/kernels/ops.metal:289, with n_q = 1 and q_pos0 = ctx - 1); head h reads kv head
 // h / (heads / kv_heads) (:242); the running maximum moves only when a score passes it by 8 (base 2, :303-316);
-// an empty context gives 0 and lse = -inf (:355). The reference splits the P V product over keys
+// an empty context gives 0 and lse = -inf (:355); P and V meet in f16 for the P V product (V converted from
+// bf16 as it is staged). The reference splits the P V product over keys
 // (attn_pv, src/kernels/gemm.metal:688-730) and leaves the softmax and the merge to its caller; here one kernel
 // does the split softmax and products, and a second merges the splits.
 //
@@ -55,20 +56,16 @@ __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 // XOR swizzle of the four 16-byte key chunks in row d of a transposed 32-key V tile.
 __device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return ((d >> 1) ^ (d >> 3)) & 3u; }
 
-__device__ __forceinline__ uint32_t half_of(const u32x4& c, int e)
-{
-    const uint32_t w = c[e >> 1];
-    return (e & 1) ? (w >> 16) : (w & 0xffffu);
-}
-
 template <class T>
 __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p)
 {
     using E = Elem<T>;
     using V8 = typename E::vec8;
+    using H = Elem<_Float16>;
+    using H8 = f16x8;
     constexpr int KS = kD + 8;
     __shared__ __attribute__((aligned(16))) T ks_all[kWaves][kTK * KS];
-    __shared__ __attribute__((aligned(16))) T vt_all[kWaves][kD * kTK];
+    __shared__ __attribute__((aligned(16))) _Float16 vt_all[kWaves][kD * kTK];
 
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t g = lane >> 5, c32 = lane & 31;
@@ -94,7 +91,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
     const uint32_t k_end = min(k_begin + p.split, ctx);
 
     T* ks = ks_all[w];
-    T* vt = vt_all[w];
+    _Float16* vt = vt_all[w];
     // Q: the B operand; column c32 is query head kvh * group + c32 (zero past the group).
     V8 qreg[kD / 16];
     {
@@ -126,8 +123,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
         for (int e = 0; e < 8; ++e) {
             const uint32_t d = cc * 8 + e;
             *reinterpret_cast<u32x4*>(&vt[d * kTK + ((kg ^ vt_swz(d)) * 8)]) =
-                u32x4{half_of(vreg[0], e) | (half_of(vreg[1], e) << 16), half_of(vreg[2], e) | (half_of(vreg[3], e) << 16),
-                      half_of(vreg[4], e) | (half_of(vreg[5], e) << 16), half_of(vreg[6], e) | (half_of(vreg[7], e) << 16)};
+                u32x4{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e),
+                      f16_pair<T>(vreg[4], vreg[5], e), f16_pair<T>(vreg[6], vreg[7], e)};
         }
     };
 
@@ -171,22 +168,22 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
                 for (int r = 0; r < 16; ++r)
                     oacc[db][r] *= f;
         const float mu = m == -INFINITY ? 0.0f : m;
-        V8 pb[2];
+        H8 pb[2];
         for (int a = 0; a < 2; ++a) {
             u32x4 pk;
             for (int jj = 0; jj < 4; ++jj) {
                 const float e0 = exp2f(fmaf(s[8 * a + 2 * jj], c, -mu));
                 const float e1 = exp2f(fmaf(s[8 * a + 2 * jj + 1], c, -mu));
                 l += e0 + e1;
-                pk[jj] = E::pack2(e0, e1);
+                pk[jj] = H::pack2(e0, e1);
             }
-            pb[a] = __builtin_bit_cast(V8, pk);
+            pb[a] = __builtin_bit_cast(H8, pk);
         }
         for (int a = 0; a < 2; ++a)
             for (int db = 0; db < kD / 32; ++db) {
                 const uint32_t d = 32 * db + c32;
-                const T* vr = &vt[d * kTK + (((2 * a + g) ^ vt_swz(d)) * 8)];
-                oacc[db] = E::mfma32(*reinterpret_cast<const V8*>(vr), pb[a], oacc[db]);
+                const _Float16* vr = &vt[d * kTK + (((2 * a + g) ^ vt_swz(d)) * 8)];
+                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[a], oacc[db]);
             }
         asm volatile("" ::: "memory");
     }

@@ -5,8 +5,9 @@
 // to query row r (position pos = q_pos0 + r) when j < n_k && (j <= pos || (pos >= block && j >= block))
 // (ops.metal:289); head h reads kv head h / (heads / kv_heads) (:242); the running maximum moves only when a
 // score passes it by 8 in the base-2 domain (:303-316), so most key blocks leave the output unscaled; P is
-// rounded to the input type for the P V product and the row sum adds the unrounded exponentials (:328-330); a
-// fully masked row gives 0 (:355); rows >= n_q are not stored (:359-362).
+// rounded to f16 for the P V product and the row sum adds the unrounded exponentials (:328-330); a fully masked
+// row gives 0 (:355); rows >= n_q are not stored (:359-362). With bf16 inputs, V is converted to f16 as it is
+// staged, so P keeps f16's 11 significant bits (bf16's 8 would put ~2^-9 |v| of error on rows of few keys).
 //
 // The design is this one's own, for CDNA4:
 // * A workgroup is 4 waves (256 threads). Each wave owns 32 query rows of one head; the workgroup's waves cover
@@ -19,8 +20,8 @@
 // * K rows are stored in LDS with bits 2 and 3 of the row swapped within each 32 (slot_of); that makes the
 //   registers of S^T, once exponentiated and packed, exactly the B operand of O^T = V^T P^T for 16 consecutive
 //   keys, so P never goes through LDS.
-// * V is stored transposed in LDS (one row per head dimension, 64 keys, XOR-swizzled 16-byte chunks), written
-//   with an in-register 4x8 transpose, so the V^T operand is one 16-byte LDS read.
+// * V is stored transposed in LDS as f16 (one row per head dimension, 64 keys, XOR-swizzled 16-byte chunks),
+//   written with an in-register 4x8 transpose, so the V^T operand is one 16-byte LDS read.
 // * K / V tiles of 64 keys are double-buffered in LDS; the next tile's global loads are issued before the
 //   current tile's products, and one barrier per tile orders the buffers.
 // * Workgroups are launched heaviest rows first (causal work grows with the row), and the grid's fastest index
@@ -57,18 +58,13 @@ __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 // XOR swizzle of the 16-byte key chunks in row d of the transposed V tile.
 __device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d ^ (d >> 3)) & 7u; }
 
-// Element e (0..7) of a 16-byte chunk of 16-bit values.
-__device__ __forceinline__ uint32_t half_of(const u32x4& c, int e)
-{
-    const uint32_t w = c[e >> 1];
-    return (e & 1) ? (w >> 16) : (w & 0xffffu);
-}
-
 template <class T, class TO, int D>
 __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const FwdParams p)
 {
     using E = Elem<T>;
     using V8 = typename E::vec8;
+    using H = Elem<_Float16>;
+    using H8 = f16x8;
     constexpr int KS = D + 8;                 // K row stride in LDS (elements): 16 bytes of padding
     constexpr int VS = kKB;                   // V^T row stride (elements)
     constexpr int CPR = D / 8;                // 16-byte chunks a row
@@ -77,7 +73,7 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
     constexpr int NKK = D / 16;               // 16-wide head-dimension steps of Q K^T
     static_assert(NV * kThreads == kKB * CPR && (NV == 2 || NV == 4 || NV == 8), "tile split");
     __shared__ __attribute__((aligned(16))) T ks[2][kKB * KS];
-    __shared__ __attribute__((aligned(16))) T vt[2][D * VS];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * VS];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g = lane >> 5, c32 = lane & 31;
@@ -132,17 +128,16 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
         const uint32_t key0 = NV * v_kg, kc = key0 / 8, off = key0 % 8;
         for (int e = 0; e < 8; ++e) {
             const uint32_t d = v_cc * 8 + e;
-            T* dst = &vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off];
+            _Float16* dst = &vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off];
             if constexpr (NV == 2) {
-                *reinterpret_cast<uint32_t*>(dst) = half_of(vreg[0], e) | (half_of(vreg[1], e) << 16);
+                *reinterpret_cast<uint32_t*>(dst) = f16_pair<T>(vreg[0], vreg[1], e);
             } else if constexpr (NV == 4) {
-                *reinterpret_cast<u32x2*>(dst) = u32x2{half_of(vreg[0], e) | (half_of(vreg[1], e) << 16),
-                                                       half_of(vreg[2], e) | (half_of(vreg[3], e) << 16)};
+                *reinterpret_cast<u32x2*>(dst) =
+                    u32x2{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e)};
             } else {
-                *reinterpret_cast<u32x4*>(dst) = u32x4{half_of(vreg[0], e) | (half_of(vreg[1], e) << 16),
-                                                       half_of(vreg[2], e) | (half_of(vreg[3], e) << 16),
-                                                       half_of(vreg[4], e) | (half_of(vreg[5], e) << 16),
-                                                       half_of(vreg[6], e) | (half_of(vreg[7], e) << 16)};
+                *reinterpret_cast<u32x4*>(dst) =
+                    u32x4{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e),
+                          f16_pair<T>(vreg[4], vreg[5], e), f16_pair<T>(vreg[6], vreg[7], e)};
             }
         }
     };
@@ -199,9 +194,9 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
                     for (int r = 0; r < 16; ++r)
                         oacc[db][r] *= f;
             const float mu = m == -INFINITY ? 0.0f : m;
-            // P in the input type, packed as the B operand of O^T += V^T P^T: chunk 2 t + a holds keys
+            // P in f16, packed as the B operand of O^T += V^T P^T: chunk 2 t + a holds keys
             // j0 + 32 t + 16 a + 8 g + 0..7 of this lane's row.
-            V8 pb[4];
+            H8 pb[4];
             for (int t = 0; t < 2; ++t)
                 for (int a = 0; a < 2; ++a) {
                     u32x4 pk;
@@ -209,15 +204,15 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
                         const float e0 = exp2f(fmaf(s[t][8 * a + 2 * jj], c, -mu));
                         const float e1 = exp2f(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
                         l += e0 + e1;
-                        pk[jj] = E::pack2(e0, e1);
+                        pk[jj] = H::pack2(e0, e1);
                     }
-                    pb[2 * t + a] = __builtin_bit_cast(V8, pk);
+                    pb[2 * t + a] = __builtin_bit_cast(H8, pk);
                 }
             for (int cc = 0; cc < 4; ++cc)
                 for (int db = 0; db < NDB; ++db) {
                     const uint32_t d = 32 * db + c32;
-                    const T* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
-                    oacc[db] = E::mfma32(*reinterpret_cast<const V8*>(vr), pb[cc], oacc[db]);
+                    const _Float16* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
+                    oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[cc], oacc[db]);
                 }
         }
         if (jb + 1 < nb)

@@ -82,6 +82,34 @@ __device__ __forceinline__ float to_float(T x)
     return (float)x;
 }
 
+// Element e (0..7) of a 16-byte chunk of 16-bit values, in the low 16 bits.
+__device__ __forceinline__ uint32_t half_of(const u32x4& c, int e)
+{
+    const uint32_t w = c[e >> 1];
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+// Element e of chunk a and element e of chunk b (inputs of type T) as one dword of two f16 values. The P V
+// product always runs in f16 (P in f16 has 11 significant bits, bf16 only 8); bf16 values convert exactly within
+// f16's normal range, and round toward zero below it and saturate at +-65504 above it.
+template <class T>
+__device__ __forceinline__ uint32_t f16_pair(const u32x4& a, const u32x4& b, int e);
+
+template <>
+__device__ __forceinline__ uint32_t f16_pair<_Float16>(const u32x4& a, const u32x4& b, int e)
+{
+    return half_of(a, e) | (half_of(b, e) << 16);
+}
+
+template <>
+__device__ __forceinline__ uint32_t f16_pair<__bf16>(const u32x4& a, const u32x4& b, int e)
+{
+    const uint32_t wa = a[e >> 1], wb = b[e >> 1];
+    const float fa = __builtin_bit_cast(float, (e & 1) ? (wa & 0xffff0000u) : (wa << 16));
+    const float fb = __builtin_bit_cast(float, (e & 1) ? (wb & 0xffff0000u) : (wb << 16));
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(fa, fb));
+}
+
 // The other half of a 64-lane wave (lane l <-> l ^ 32).
 __device__ __forceinline__ float swap_halves(float x)
 {

@@ -68,8 +68,10 @@ def test_sweep(case):
 
 
 def test_split_invariance_and_dense_agreement():
-    """Splits of 64, 512 and 4096 keys agree to fp32 rounding; each row equals mako_attn_fwd's single query at
-    q_pos0 = ctx - 1 over the same cache (the reference's decode path)."""
+    """Splits of 64, 512 and 4096 keys agree to within P's f16 rounding (where the running maximum moves depends on
+    the split, so P rounds against different maxima); each row equals mako_attn_fwd's single query at
+    q_pos0 = ctx - 1 over the same cache (the reference's decode path). A dropped or doubled split would be off by
+    the output's own size (~3e-2 here)."""
     batch, heads, kv, cap = 3, 16, 4, 5000
     ctx = np.array([4999, 1234, 77], np.uint32)
     gen = torch.Generator(device="cuda").manual_seed(5)
@@ -79,8 +81,8 @@ def test_split_invariance_and_dense_agreement():
     outs = [run_decode(q, k, v, ctx, batch=batch, heads=heads, kv_heads=kv, cap=cap, split=s)
             for s in (64, 512, 4096)]
     for o, lse in outs[1:]:
-        np.testing.assert_allclose(o, outs[0][0], rtol=2e-5, atol=2e-6)
-        np.testing.assert_allclose(lse, outs[0][1], rtol=0, atol=2e-5)
+        np.testing.assert_allclose(o, outs[0][0], rtol=1e-2, atol=3e-4)
+        np.testing.assert_allclose(lse, outs[0][1], rtol=0, atol=1e-4)
     for b in range(batch):
         qt = torch.zeros((heads, 64, 128), dtype=torch.bfloat16, device="cuda")
         qt[:, 0] = q[b]
@@ -89,7 +91,7 @@ def test_split_invariance_and_dense_agreement():
         M.attn_fwd(qt, k[b].contiguous(), v[b].contiguous(), o, n_q=1, q_pad=64, n_k=int(ctx[b]), k_pad=cap,
                    heads=heads, kv_heads=kv, q_pos0=int(ctx[b]) - 1, block=M.U32_MAX, dim=128, lse=lse)
         torch.cuda.synchronize()
-        np.testing.assert_allclose(outs[1][0][b], G.to_host(o)[0], rtol=1e-3, atol=2e-4)
+        np.testing.assert_allclose(outs[1][0][b], G.to_host(o)[0], rtol=1e-2, atol=3e-4)
         np.testing.assert_allclose(outs[1][1][b], lse.cpu().numpy()[:, 0], rtol=0, atol=1e-4)
 
 
