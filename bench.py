@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention path on one MI355X, through the C ABI (mako-common_amd/lib/libmako_attn.so).
+
+Headline (one JSON line): causal GQA prefill at the Qwen3-8B shape (batch 1, 32 query heads over 8 kv heads,
+D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only the unmasked pairs
+(4 * D * S (S + 1) / 2 * 32). Beside it: batch-16 decode against a contiguous f16 KV cache (contexts drawn
+uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
+S16384 24-head case in TFLOP/s. Inputs are synthetic N(0, 1), resident in HBM before the timed region. Each
+figure is the mean launch duration over --steps back-to-back launches (HIP events on the launch stream) after
+--warmup untimed ones. The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
+a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill|decode|bidir|copy]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mako-common_amd"))
+
+PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA
+PEAK_GBPS = 8000.0    # MI355X HBM3E
+U32_MAX = 0xFFFFFFFF
+CPU_SECONDS = 8.0     # wall-clock budget of each CPU-baseline leg
+
+
+def time_launches(torch, fn, steps, warmup):
+    """Mean duration (ms) of one launch of fn over `steps` back-to-back launches, by HIP events on the current
+    stream (the stream the C ABI launches on), after `warmup` untimed launches."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def bits(torch, t):
+    return t.cpu().view(torch.int16).numpy().view("uint16")
+
+
+def cpu_sample(run, n0, budget):
+    """Runs run(n) with n doubling from n0 until one run takes at least budget / 4 seconds; returns (n, seconds)
+    of the last run."""
+    n = n0
+    while True:
+        t0 = time.perf_counter()
+        run(n)
+        dt = time.perf_counter() - t0
+        if dt >= budget / 4 or n >= 1 << 16:
+            return n, dt
+        n = int(n * min(8.0, max(2.0, budget / 2 / max(dt, 1e-3))))
+
+
+def bench_prefill(torch, M, steps, warmup, with_cpu):
+    import numpy as np
+
+    S, H, KV, D = 4096, 32, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    q = torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((H, S), dtype=torch.float32, device="cuda")
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, q_pos0=0, block=U32_MAX, dim=D)
+    ms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
+    flop = 4.0 * D * (S * (S + 1) / 2) * H
+    tflops = flop / (ms * 1e-3) / 1e12
+    out = {"ms": ms, "tflops": tflops, "flop": flop,
+           "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": tflops / PEAK_TFLOPS, "traffic": None, "kernel": "flash_fwd<bf16,bf16,128>"}}
+    if with_cpu:
+        import oracle as O
+
+        qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
+        rng = np.random.default_rng(7)
+        gpu_o = o.float().cpu().numpy()
+        state = {}
+
+        def run(n):
+            hr = np.stack([rng.integers(0, H, n), rng.integers(0, S, n)], 1).astype(np.uint32)
+            want, _ = O.attn_dense_rows(qb, kb, vb, hr, dtype=O.BF16, nthreads=cpu_threads(), **args)
+            state["hr"], state["want"] = hr, want
+
+        n, dt = cpu_sample(run, 64, CPU_SECONDS)
+        hr, want = state["hr"], state["want"]
+        sample_flop = float(sum(4.0 * D * (int(r) + 1) for _, r in hr))
+        got = np.stack([gpu_o[r, h * D:(h + 1) * D] for h, r in hr])
+        err = np.abs(got - want)
+        out["cpu_baseline"] = {"value": sample_flop / dt / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
+                               "kind": "port",
+                               "sample": f"{n} random (head, row) pairs of the S4096 causal prefill, double "
+                                         f"precision, {dt:.2f} s wall; extrapolated by unmasked-pair FLOPs"}
+        out["parity"] = {"rows": n, "max_abs_err": float(err.max()),
+                         "within_tolerance": bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))}
+    return out
+
+
+def bench_decode(torch, M, steps, warmup, with_cpu):
+    import numpy as np
+
+    B, H, KV, D, cap = 16, 32, 8, 128, 32768
+    ctx = np.random.default_rng(2026).integers(1024, 32769, B).astype(np.uint32)
+    gen = torch.Generator(device="cuda").manual_seed(2026)
+    q = torch.randn((B, H, D), generator=gen, device="cuda").half()
+    k = torch.randn((B, KV, cap, D), generator=gen, device="cuda").half()
+    v = torch.randn((B, KV, cap, D), generator=gen, device="cuda").half()
+    ctx_d = torch.from_numpy(ctx.astype(np.int32)).to("cuda")
+    o = torch.empty((B, H * D), dtype=torch.float16, device="cuda")
+    lse = torch.empty((B, H), dtype=torch.float32, device="cuda")
+    a = M.decode_args(batch=B, heads=H, kv_heads=KV, dim=D, cap=cap, max_ctx=cap)
+    ws = torch.empty(M.decode_workspace(a), dtype=torch.uint8, device="cuda")
+    ms = time_launches(torch, lambda: M.attn_decode(a, q, k, v, ctx_d, o, ws, lse=lse), steps, warmup)
+    nbytes = float(4096 * ctx.astype(np.int64).sum())  # K + V: kv_heads * D * 2 bytes * 2 tensors per token
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    out = {"ms": ms, "gbps": gbps, "bytes": nbytes, "sum_ctx": int(ctx.sum()),
+           "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s",
+                        "frac": gbps / PEAK_GBPS, "traffic": None,
+                        "kernel": "decode_split<f16> + decode_merge<f16> (one step)"}}
+    if with_cpu:
+        import oracle as O
+
+        qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
+        rng = np.random.default_rng(11)
+        gpu_o = o.float().cpu().numpy()
+        state = {}
+
+        def run(n):
+            sh = np.stack([rng.integers(0, B, n), rng.integers(0, H, n)], 1).astype(np.uint32)
+            want, _ = O.attn_decode_rows(qb, kb, vb, ctx, sh, batch=B, heads=H, kv_heads=KV, dim=D, cap=cap,
+                                         dtype=O.F16, nthreads=cpu_threads())
+            state["sh"], state["want"] = sh, want
+
+        n, dt = cpu_sample(run, 16, CPU_SECONDS)
+        sh, want = state["sh"], state["want"]
+        # a (sequence, head) pair's share of the K + V bytes: its kv head's rows serve H / KV query heads
+        sample_bytes = float(sum(4096 * int(ctx[b]) / H for b, _ in sh))
+        got = np.stack([gpu_o[b, h * D:(h + 1) * D] for b, h in sh])
+        err = np.abs(got - want)
+        out["cpu_baseline"] = {"value": sample_bytes / dt / 1e9, "unit": "GB/s", "cores": cpu_threads(),
+                               "kind": "port",
+                               "sample": f"{n} random (sequence, head) pairs of the batch-16 decode, double "
+                                         f"precision, {dt:.2f} s wall; each pair credited its share of K + V bytes"}
+        out["parity"] = {"rows": n, "max_abs_err": float(err.max()),
+                         "within_tolerance": bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))}
+    return out
+
+
+def bench_bidir(torch, M, steps, warmup):
+    S, H, D = 16384, 24, 128
+    gen = torch.Generator(device="cuda").manual_seed(16384)
+    q, k, v = (torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(3))
+    o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=H, q_pos0=0, block=0, dim=D)
+    ms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, **args), steps, warmup)
+    flop = 4.0 * D * S * S * H
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tflops, "flop": flop, "frac": tflops / PEAK_TFLOPS}
+
+
+def bench_copy(torch, steps, warmup):
+    """A plain device copy of known size: the reference point that scales the HBM byte counters."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_launches(torch, lambda: dst.copy_(src), steps, warmup)
+    return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbps": 2 * n / (ms * 1e-3) / 1e9}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
+    ap.add_argument("--only", choices=["prefill", "decode", "bidir", "copy"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
+              f"measured on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import mako_attn as M
+
+    M.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    if args.only:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        fn = {"prefill": lambda: bench_prefill(torch, M, args.steps, args.warmup, False),
+              "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, False),
+              "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup),
+              "copy": lambda: bench_copy(torch, args.steps, args.warmup)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return
+    with_cpu = not args.no_cpu
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    pre = bench_prefill(torch, M, args.steps, args.warmup, with_cpu)
+    dec = bench_decode(torch, M, args.steps, args.warmup, with_cpu)
+    bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup))
+    line = {
+        "metric": "attn prefill TFLOP/s (Qwen3-8B shape, seq 4096) + decode KV HBM GB/s, 1 GPU",
+        "value": round(pre["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1), seeded, resident in HBM",
+        "config": {"workload": "causal GQA prefill, batch 1, 32 query heads / 8 kv heads, D 128, S 4096, bf16 "
+                               "in/out, fp32 accumulate, LSE", "global_batch": 1, "seq_len": 4096,
+                   "parallelism": "single GPU"},
+        "roofline": pre["roofline"],
+        "decode": {"value": round(dec["gbps"], 1), "unit": "GB/s", "ms_per_step": round(dec["ms"], 4),
+                   "dtype": "f16", "config": {"workload": "decode, batch 16, 32 query heads / 8 kv heads, D 128, "
+                                                          "contexts U[1024, 32768] seed 2026, f16 cache",
+                                              "sum_ctx": dec["sum_ctx"]},
+                   "roofline": dec["roofline"]},
+        "bidirectional": {"value": round(bid["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(bid["ms"], 4),
+                          "frac": round(bid["frac"], 4),
+                          "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16"}},
+    }
+    if with_cpu:
+        line["cpu_baseline"] = pre["cpu_baseline"]
+        line["parity"] = pre["parity"]
+        line["decode"]["cpu_baseline"] = dec["cpu_baseline"]
+        line["decode"]["parity"] = dec["parity"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
