@@ -96,14 +96,16 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
     // Q: the B operand, lane (c32, g) holds row q0 + c32, head dims 16 kk + 8 g .. + 7.
     V8 qreg[NKK];
     {
-        const uint32_t row = q0 + c32;
-        const T* src = static_cast<const T*>(p.q) + ((size_t)h * p.q_pad + row) * D + 8 * g;
+        // a buffer over this head's n_q rows: rows past n_q load as zeros
+        const auto qrs = buffer_rsrc(static_cast<const T*>(p.q) + (size_t)h * p.q_pad * D, p.n_q * D * sizeof(T));
+        const uint32_t off = ((q0 + c32) * D + 8 * g) * sizeof(T);
         for (int kk = 0; kk < NKK; ++kk)
-            qreg[kk] = row < p.n_q ? *reinterpret_cast<const V8*>(src + 16 * kk) : V8{};
+            qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 16 * kk * sizeof(T)));
     }
 
-    const T* kbase = static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * D;
-    const T* vbase = static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * D;
+    // K / V of this kv head as buffer resources over its n_k valid rows: rows past n_k load as zeros.
+    const auto krs = buffer_rsrc(static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * D, p.n_k * D * sizeof(T));
+    const auto vrs = buffer_rsrc(static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * D, p.n_k * D * sizeof(T));
     // V loads: thread -> head-dim chunk cc and NV consecutive keys from NV * kg (kg XOR-ed by the half row so
     // that the transposed LDS writes of a 16-lane group spread over the banks).
     const uint32_t v_cc = tid % CPR;
@@ -112,13 +114,11 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
 
     auto load_tile = [&](uint32_t j0) {
         for (int i = 0; i < NV; ++i) {
-            const uint32_t c = tid + kThreads * i, row = c / CPR, col = c % CPR, key = j0 + row;
-            kreg[i] = key < p.n_k ? *reinterpret_cast<const u32x4*>(kbase + (size_t)key * D + col * 8) : u32x4{};
+            const uint32_t c = tid + kThreads * i, row = c / CPR, col = c % CPR;
+            kreg[i] = buffer_load16(krs, ((j0 + row) * D + col * 8) * sizeof(T));
         }
-        for (int i = 0; i < NV; ++i) {
-            const uint32_t key = j0 + NV * v_kg + i;
-            vreg[i] = key < p.n_k ? *reinterpret_cast<const u32x4*>(vbase + (size_t)key * D + v_cc * 8) : u32x4{};
-        }
+        for (int i = 0; i < NV; ++i)
+            vreg[i] = buffer_load16(vrs, ((j0 + NV * v_kg + i) * D + v_cc * 8) * sizeof(T));
     };
     auto store_tile = [&](int buf) {
         for (int i = 0; i < NV; ++i) {
@@ -162,30 +162,35 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
         if (j0 < w_keys) {
             // S^T for keys j0 .. j0 + 63: two 32x32 tiles; register r of tile t holds key
             // j0 + 32 t + 16 (r / 8) + 8 g + r % 8 for this lane's row.
-            f32x16 s[2];
-            for (int t = 0; t < 2; ++t) {
-                s[t] = f32x16{};
-                const T* kr = &ks[buf][(32 * t + c32) * KS + 8 * g];
-                for (int kk = 0; kk < NKK; ++kk)
-                    s[t] = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s[t]);
+            f32x16 s[2] = {f32x16{}, f32x16{}};
+            {
+                // the two 32-key tiles' products interleaved: two independent accumulation chains
+                const T* kr0 = &ks[buf][c32 * KS + 8 * g];
+                const T* kr1 = kr0 + 32 * KS;
+                for (int kk = 0; kk < NKK; ++kk) {
+                    s[0] = E::mfma32(*reinterpret_cast<const V8*>(kr0 + 16 * kk), qreg[kk], s[0]);
+                    s[1] = E::mfma32(*reinterpret_cast<const V8*>(kr1 + 16 * kk), qreg[kk], s[1]);
+                }
             }
             const bool plain = j0 + kKB <= p.n_k && (j0 + kKB - 1 <= p0 || (p0 >= p.block && j0 >= p.block));
+            if (!plain) {
+                // the mask rule, branch-free per element
+                const bool lane_open = pos >= p.block;
+                for (int t = 0; t < 2; ++t)
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t j = j0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
+                        const bool seen = (j < p.n_k) & ((j <= pos) | (lane_open & (j >= p.block)));
+                        s[t][r] = seen ? s[t][r] : -INFINITY;
+                    }
+            }
             float mx = -INFINITY;
             for (int t = 0; t < 2; ++t)
-                for (int r = 0; r < 16; ++r) {
-                    float x = s[t][r];
-                    if (!plain) {
-                        const uint32_t j = j0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
-                        if (!(j < p.n_k && (j <= pos || (pos >= p.block && j >= p.block))))
-                            x = -INFINITY;
-                        s[t][r] = x;
-                    }
-                    mx = fmaxf(mx, x);
-                }
+                for (int r = 0; r < 16; ++r)
+                    mx = fmaxf(mx, s[t][r]);
             mx = fmaxf(mx, swap_halves(mx)) * c;  // the row's maximum, base 2 (c > 0)
             float f = 1.0f;
             if (mx > m + kRescale) {
-                f = exp2f(m - mx);  // 0 while nothing was seen
+                f = exp2_fast(m - mx);  // 0 while nothing was seen
                 m = mx;
             }
             l *= f;
@@ -201,8 +206,8 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
                 for (int a = 0; a < 2; ++a) {
                     u32x4 pk;
                     for (int jj = 0; jj < 4; ++jj) {
-                        const float e0 = exp2f(fmaf(s[t][8 * a + 2 * jj], c, -mu));
-                        const float e1 = exp2f(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
+                        const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
+                        const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
                         l += e0 + e1;
                         pk[jj] = H::pack2(e0, e1);
                     }
@@ -280,6 +285,8 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
                     a->width, a->heads, dim);
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return fail(MAKO_EINVAL, "attention: q, k, v and o must be 16-byte aligned");
+    if ((uint64_t)a->k_pad * dim * 2 > 0x7fffffffu)
+        return fail(MAKO_EINVAL, "attention: %u key rows of %u exceed 2 GiB a head", a->k_pad, dim);
     if (a->n_q == 0)
         return ok();
     const uint32_t group = a->heads / a->kv_heads;

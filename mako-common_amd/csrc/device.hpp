@@ -110,6 +110,22 @@ __device__ __forceinline__ uint32_t f16_pair<__bf16>(const u32x4& a, const u32x4
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(fa, fb));
 }
 
+// A raw buffer resource over `bytes` bytes at `base`: loads at offsets past the end return zero (the gfx9
+// range check), which masks rows past a tensor's valid extent without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
+{
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+
+// 2^x by v_exp_f32 alone (no denormal-range fix-up: results below 2^-126 flush to zero, which the softmax
+// sums cannot tell apart).
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // The other half of a 64-lane wave (lane l <-> l ^ 32).
 __device__ __forceinline__ float swap_halves(float x)
 {
