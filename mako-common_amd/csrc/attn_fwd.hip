@@ -75,7 +75,8 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
     __shared__ __attribute__((aligned(16))) T ks[2][kKB * KS];
     __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * VS];
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform over the wave
     const uint32_t g = lane >> 5, c32 = lane & 31;
     const uint32_t hg = blockIdx.x;
     const uint32_t qb = p.n_qblk - 1 - blockIdx.y;  // the latest rows (the most keys) first
@@ -99,8 +100,12 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
         // a buffer over this head's n_q rows: rows past n_q load as zeros
         const auto qrs = buffer_rsrc(static_cast<const T*>(p.q) + (size_t)h * p.q_pad * D, p.n_q * D * sizeof(T));
         const uint32_t off = ((q0 + c32) * D + 8 * g) * sizeof(T);
+        #pragma unroll
         for (int kk = 0; kk < NKK; ++kk)
             qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 16 * kk * sizeof(T)));
+        #pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            settle(qreg[kk]);
     }
 
     // K / V of this kv head as buffer resources over its n_k valid rows: rows past n_k load as zeros.
@@ -113,19 +118,23 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
     u32x4 kreg[NV], vreg[NV];
 
     auto load_tile = [&](uint32_t j0) {
+        #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const uint32_t c = tid + kThreads * i, row = c / CPR, col = c % CPR;
             kreg[i] = buffer_load16(krs, ((j0 + row) * D + col * 8) * sizeof(T));
         }
+        #pragma unroll
         for (int i = 0; i < NV; ++i)
             vreg[i] = buffer_load16(vrs, ((j0 + NV * v_kg + i) * D + v_cc * 8) * sizeof(T));
     };
     auto store_tile = [&](int buf) {
+        #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const uint32_t c = tid + kThreads * i, row = c / CPR, col = c % CPR;
             *reinterpret_cast<u32x4*>(&ks[buf][slot_of(row) * KS + col * 8]) = kreg[i];
         }
         const uint32_t key0 = NV * v_kg, kc = key0 / 8, off = key0 % 8;
+        #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint32_t d = v_cc * 8 + e;
             _Float16* dst = &vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off];
@@ -143,6 +152,7 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
     };
 
     f32x16 oacc[NDB];
+    #pragma unroll
     for (int db = 0; db < NDB; ++db)
         oacc[db] = f32x16{};
     float m = -INFINITY, l = 0.0f;  // running maximum (base-2 domain) and sum of this lane's keys
@@ -167,6 +177,7 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
                 // the two 32-key tiles' products interleaved: two independent accumulation chains
                 const T* kr0 = &ks[buf][c32 * KS + 8 * g];
                 const T* kr1 = kr0 + 32 * KS;
+                #pragma unroll
                 for (int kk = 0; kk < NKK; ++kk) {
                     s[0] = E::mfma32(*reinterpret_cast<const V8*>(kr0 + 16 * kk), qreg[kk], s[0]);
                     s[1] = E::mfma32(*reinterpret_cast<const V8*>(kr1 + 16 * kk), qreg[kk], s[1]);
@@ -176,7 +187,9 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
             if (!plain) {
                 // the mask rule, branch-free per element
                 const bool lane_open = pos >= p.block;
+                #pragma unroll
                 for (int t = 0; t < 2; ++t)
+                    #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const uint32_t j = j0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
                         const bool seen = (j < p.n_k) & ((j <= pos) | (lane_open & (j >= p.block)));
@@ -184,7 +197,9 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
                     }
             }
             float mx = -INFINITY;
+            #pragma unroll
             for (int t = 0; t < 2; ++t)
+                #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     mx = fmaxf(mx, s[t][r]);
             mx = fmaxf(mx, swap_halves(mx)) * c;  // the row's maximum, base 2 (c > 0)
@@ -195,16 +210,21 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
             }
             l *= f;
             if (__any(f != 1.0f))
+                #pragma unroll
                 for (int db = 0; db < NDB; ++db)
+                    #pragma unroll
                     for (int r = 0; r < 16; ++r)
                         oacc[db][r] *= f;
             const float mu = m == -INFINITY ? 0.0f : m;
             // P in f16, packed as the B operand of O^T += V^T P^T: chunk 2 t + a holds keys
             // j0 + 32 t + 16 a + 8 g + 0..7 of this lane's row.
             H8 pb[4];
+            #pragma unroll
             for (int t = 0; t < 2; ++t)
+                #pragma unroll
                 for (int a = 0; a < 2; ++a) {
                     u32x4 pk;
+                    #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
                         const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
                         const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
@@ -213,7 +233,9 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
                     }
                     pb[2 * t + a] = __builtin_bit_cast(H8, pk);
                 }
+            #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
+                #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
                     const uint32_t d = 32 * db + c32;
                     const _Float16* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
@@ -232,7 +254,9 @@ __global__ __launch_bounds__(kThreads, D == 256 ? 1 : 2) void flash_fwd(const Fw
     const uint32_t row = q0 + c32;
     if (live && row < p.n_q) {
         TO* orow = static_cast<TO*>(p.o) + (size_t)row * p.width + (size_t)h * D;
+        #pragma unroll
         for (int db = 0; db < NDB; ++db)
+            #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4)
                 store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
                            oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);

@@ -126,6 +126,16 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 // sums cannot tell apart).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Marks a loaded value as arrived: the compiler waits for its load here, once, instead of treating it as still
+// in flight inside a later loop (where the in-order vmcnt wait would also wait for that loop's prefetches).
+template <class V>
+__device__ __forceinline__ void settle(V& x)
+{
+    u32x4 u = __builtin_bit_cast(u32x4, x);
+    asm volatile("" : "+v"(u));
+    x = __builtin_bit_cast(V, u);
+}
+
 // The other half of a 64-lane wave (lane l <-> l ^ 32).
 __device__ __forceinline__ float swap_halves(float x)
 {
