@@ -1,0 +1,491 @@
+// Block-sparse attention for gfx950 (Video Sparse Attention's training-free form) and its cube selection.
+//
+// Semantics (the reference's, src/kernels/ops.metal:914-1185; host checks src/models/runtime.cpp:286-317):
+// * cube_pool: the mean of a cube's 64 rows of q or k over its cnt[c] valid rows (0 when cnt is 0; the padding
+//   rows are zero by the tiles' construction) (ops.metal:926-939).
+// * cube_scores: sc[h][qc][kc] = qp[h][qc] . kp[h][kc] in fp32 (:941-955).
+// * cube_topk: the `local` cubes {qc, qc - stride, qc + stride} (those in range) first, their scores taken out of
+//   the running, then repeated argmax, the larger score first and the smaller index on ties; nsel = min(topk, n)
+//   (:957-1027).
+// * attention_sparse: query tile t (64 rows) < n_cubes visits the key cubes sel lists for it (64 keys each), then
+//   the dense rows [dense0, dense1); a later tile visits [0, n_k); keys with valid[j] == 0 are masked (:1079-1113);
+//   query row r's output goes to o row map[r], dropped when map[r] < 0 or r >= n_q (:1173-1184). Two fields the
+//   reference does not have: causal (key j is seen by tile row r only when j <= r) and sel_heads (one list per
+//   kv head, shared by the group's query heads, instead of one per query head).
+//
+// Design: the flash tile loop of attn_fwd.hip (S^T = K Q^T on v_mfma_f32_32x32x16, K rows in bit-swapped LDS
+// slots, V transposed to f16 in LDS, P in registers, lazy rescale) driven by a pass list. A workgroup is one
+// 64-row query tile of hs query heads (hs = 2 when a kv head's list is shared by at least two query heads, else
+// 1), two waves a head, so every gathered K / V tile serves 2 hs waves. Each wave builds the tile's validity mask
+// with one byte load a lane and a ballot; a tile whose 64 keys are all valid (and not cut by the causal bound)
+// skips per-element masking.
+#include "device.hpp"
+
+namespace mako {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kKB = 64;  // keys a tile (one cube)
+constexpr int kCube = 64;
+constexpr float kRescale = 8.0f;
+
+__device__ __forceinline__ uint32_t slot_of(uint32_t row)
+{
+    return (row & ~12u) | ((row & 4u) << 1) | ((row & 8u) >> 1);
+}
+__device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d ^ (d >> 3)) & 7u; }
+
+struct SparseParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    const uint16_t* sel;
+    const uint16_t* nsel;
+    const uint8_t* valid;
+    const int32_t* map;
+    uint32_t n_q, q_pad, n_k, k_pad, heads, kv_heads, width;
+    float scale_log2;
+    uint32_t n_cubes, max_sel, dense0, dense1, causal, sel_heads;
+    uint32_t group, hs, n_qt;
+};
+
+template <class T, class TO, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void flash_sparse(const SparseParams p)
+{
+    using E = Elem<T>;
+    using V8 = typename E::vec8;
+    using H = Elem<_Float16>;
+    using H8 = f16x8;
+    constexpr int NT = NW * 64;
+    constexpr int KS = kD + 8;
+    constexpr int CPR = kD / 8;          // 16-byte chunks a row
+    constexpr int NV = kKB * CPR / NT;   // chunks a thread loads per tile, K and V each
+    constexpr int NKK = kD / 16, NDB = kD / 32;
+    __shared__ __attribute__((aligned(16))) T ks[2][kKB * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kD * kKB];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 5, c32 = lane & 31;
+    const uint32_t qt = p.n_qt - 1 - blockIdx.y;  // dense tiles (all keys) and late cubes first
+    const uint32_t h = blockIdx.x * p.hs + (w >> 1);
+    const uint32_t kvh = h / p.group;
+    const uint32_t q0 = qt * kCube + (w & 1) * 32;  // this wave's first row
+    const uint32_t row = q0 + c32;
+
+    // The pass list: a cube tile's selected cubes, then its dense rows; a later tile's all keys.
+    const bool cube = qt < p.n_cubes;
+    const uint32_t sh = p.sel_heads == p.heads ? h : kvh;  // uniform within the workgroup when hs > 1
+    uint32_t ns = 0;
+    const uint16_t* my_sel = p.sel + ((size_t)sh * p.n_cubes + qt) * p.max_sel;
+    if (cube)
+        ns = min((uint32_t)p.nsel[(size_t)sh * p.n_cubes + qt], p.max_sel);
+    const uint32_t dense_lo = cube ? p.dense0 : 0u, dense_hi = cube ? p.dense1 : p.n_k;
+    const uint32_t n_dense = dense_hi > dense_lo ? (dense_hi - dense_lo + kKB - 1) / kKB : 0u;
+    const uint32_t n_pass = ns + n_dense;
+    auto pass_range = [&](uint32_t ps, uint32_t& j0, uint32_t& hi) {
+        if (ps < ns) {
+            j0 = (uint32_t)my_sel[ps] * kCube;
+            hi = j0 + kCube;
+        } else {
+            j0 = dense_lo + (ps - ns) * kKB;
+            hi = min(j0 + kKB, dense_hi);
+        }
+    };
+
+    V8 qreg[NKK];
+    {
+        const auto qrs = buffer_rsrc(static_cast<const T*>(p.q) + (size_t)h * p.q_pad * kD, p.n_q * kD * sizeof(T));
+        const uint32_t off = (row * kD + 8 * g) * sizeof(T);
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 16 * kk * sizeof(T)));
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            settle(qreg[kk]);
+    }
+    // K / V over the kv head's k_pad rows (cube passes may read keys past n_k; valid masks them); the valid
+    // flags over k_pad bytes. Loads past the end return zeros.
+    const auto krs = buffer_rsrc(static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * kD, p.k_pad * kD * sizeof(T));
+    const auto vrs = buffer_rsrc(static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * kD, p.k_pad * kD * sizeof(T));
+    const auto valid_rs = buffer_rsrc(p.valid, p.k_pad);
+    const uint32_t v_cc = tid % CPR;
+    const uint32_t v_kg = (tid / CPR) ^ ((tid / (CPR / 2)) & 1u);
+    u32x4 kreg[NV], vreg[NV];
+    auto load_tile = [&](uint32_t j0) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = tid + NT * i, r = c / CPR, col = c % CPR;
+            kreg[i] = buffer_load16(krs, ((j0 + r) * kD + col * 8) * sizeof(T));
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            vreg[i] = buffer_load16(vrs, ((j0 + NV * v_kg + i) * kD + v_cc * 8) * sizeof(T));
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = tid + NT * i, r = c / CPR, col = c % CPR;
+            *reinterpret_cast<u32x4*>(&ks[buf][slot_of(r) * KS + col * 8]) = kreg[i];
+        }
+        const uint32_t key0 = NV * v_kg, kc = key0 / 8, off = key0 % 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t d = v_cc * 8 + e;
+            _Float16* dst = &vt[buf][d * kKB + ((kc ^ vt_swz(d)) * 8) + off];
+            if constexpr (NV == 4)
+                *reinterpret_cast<u32x2*>(dst) =
+                    u32x2{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e)};
+            else
+                *reinterpret_cast<u32x4*>(dst) =
+                    u32x4{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e),
+                          f16_pair<T>(vreg[4], vreg[5], e), f16_pair<T>(vreg[6], vreg[7], e)};
+        }
+    };
+
+    f32x16 oacc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+        oacc[db] = f32x16{};
+    float m = -INFINITY, l = 0.0f;
+    const float c = p.scale_log2;
+    const bool live = q0 < p.n_q;
+
+    uint32_t j0 = 0, hi = 0;
+    if (n_pass > 0) {
+        pass_range(0, j0, hi);
+        load_tile(j0);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (uint32_t ps = 0; ps < n_pass; ++ps) {
+        const int buf = ps & 1;
+        const uint32_t cj0 = j0, chi = hi;
+        if (ps + 1 < n_pass) {
+            pass_range(ps + 1, j0, hi);
+            load_tile(j0);
+        }
+        // This tile's validity: bit i for key cj0 + i in range and valid.
+        const uint32_t vflag = __builtin_amdgcn_raw_buffer_load_b8(valid_rs, (int)(cj0 + lane), 0, 0);
+        const uint64_t vmask = __ballot(cj0 + lane < chi && vflag != 0);
+        // nothing to do when no key of the tile is valid, or (causal) every key lies past every row of the wave
+        if (live && vmask != 0 && !(p.causal && cj0 > q0 + 31)) {
+            f32x16 s[2] = {f32x16{}, f32x16{}};
+            {
+                const T* kr0 = &ks[buf][c32 * KS + 8 * g];
+                const T* kr1 = kr0 + 32 * KS;
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    s[0] = E::mfma32(*reinterpret_cast<const V8*>(kr0 + 16 * kk), qreg[kk], s[0]);
+                    s[1] = E::mfma32(*reinterpret_cast<const V8*>(kr1 + 16 * kk), qreg[kk], s[1]);
+                }
+            }
+            // Register r of tile t holds key cj0 + 32 t + 16 (r / 8) + 8 g + r % 8.
+            const bool causal_cut = p.causal && cj0 + kKB - 1 > q0;
+            if (vmask != ~0ull || causal_cut) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int a = 0; a < 2; ++a) {
+                        const uint32_t kbase = 32 * t + 16 * a + 8 * g;
+                        const uint32_t bits = (uint32_t)(vmask >> kbase) & 0xffu;
+#pragma unroll
+                        for (int jj = 0; jj < 8; ++jj) {
+                            const bool seen = ((bits >> jj) & 1u) && (!p.causal || cj0 + kbase + jj <= row);
+                            s[t][8 * a + jj] = seen ? s[t][8 * a + jj] : -INFINITY;
+                        }
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    mx = fmaxf(mx, s[t][r]);
+            mx = fmaxf(mx, swap_halves(mx)) * c;
+            float f = 1.0f;
+            if (mx > m + kRescale) {
+                f = exp2_fast(m - mx);
+                m = mx;
+            }
+            l *= f;
+            if (__any(f != 1.0f))
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        oacc[db][r] *= f;
+            const float mu = m == -INFINITY ? 0.0f : m;
+            H8 pb[4];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    u32x4 pk;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
+                        const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
+                        l += e0 + e1;
+                        pk[jj] = H::pack2(e0, e1);
+                    }
+                    pb[2 * t + a] = __builtin_bit_cast(H8, pk);
+                }
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const uint32_t d = 32 * db + c32;
+                    const _Float16* vr = &vt[buf][d * kKB + (((2 * cc + g) ^ vt_swz(d)) * 8)];
+                    oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[cc], oacc[db]);
+                }
+        }
+        if (ps + 1 < n_pass)
+            store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Normalise and store through the row map; the LSE by tile row.
+    const float lt = l + swap_halves(l);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (live && row < p.n_q) {
+        const int32_t dst = p.map[row];
+        if (dst >= 0) {
+            TO* orow = static_cast<TO*>(p.o) + (size_t)dst * p.width + (size_t)h * kD;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
+                               oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
+            if (p.lse && g == 0)
+                p.lse[(size_t)h * p.q_pad + row] = lt > 0.0f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
+        }
+    }
+}
+
+// ---- cube selection ------------------------------------------------------------------------------------------
+
+// out[h][c][d] = (sum of the 64 rows of cube c) / cnt[c], 0 when cnt[c] is 0. Grid (n_cubes, heads, 2): z = 0 pools
+// q (rows q_pad apart per head), z = 1 pools k (k_pad). 128 threads, one per head dimension.
+template <class T>
+__global__ __launch_bounds__(kD) void cube_pool(const T* __restrict__ q, const T* __restrict__ k,
+                                                 const uint32_t* __restrict__ cnt, float* __restrict__ qp,
+                                                 float* __restrict__ kp, uint32_t n_cubes, uint32_t q_pad,
+                                                 uint32_t k_pad)
+{
+    const uint32_t cb = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    const bool is_k = blockIdx.z == 1;
+    const T* x = (is_k ? k + (size_t)h * k_pad * kD : q + (size_t)h * q_pad * kD) + (size_t)cb * kCube * kD + d;
+    float s = 0.0f;
+#pragma unroll 16
+    for (uint32_t r = 0; r < kCube; ++r)
+        s += to_float(x[(size_t)r * kD]);
+    const uint32_t n = cnt[cb];
+    (is_k ? kp : qp)[((size_t)h * n_cubes + cb) * kD + d] = n ? s / (float)n : 0.0f;
+}
+
+// sc[h][qc][kc] = qp[h][qc] . kp[h][kc]: 16 x 16 output tiles through LDS. Grid (ceil(n / 16), ceil(n / 16),
+// heads), 256 threads.
+__global__ __launch_bounds__(256) void cube_scores(const float* __restrict__ qp, const float* __restrict__ kp,
+                                                   float* __restrict__ sc, uint32_t n)
+{
+    __shared__ float qs[16][kD + 1], kt[16][kD + 1];
+    const uint32_t kc0 = blockIdx.x * 16, qc0 = blockIdx.y * 16, h = blockIdx.z, t = threadIdx.x;
+    for (uint32_t i = t; i < 16 * kD; i += 256) {
+        const uint32_t r = i / kD, d = i % kD;
+        qs[r][d] = qc0 + r < n ? qp[((size_t)h * n + qc0 + r) * kD + d] : 0.0f;
+        kt[r][d] = kc0 + r < n ? kp[((size_t)h * n + kc0 + r) * kD + d] : 0.0f;
+    }
+    __syncthreads();
+    const uint32_t qr = t / 16, kr = t % 16;
+    float s = 0.0f;
+#pragma unroll 8
+    for (uint32_t d = 0; d < kD; ++d)
+        s = fmaf(qs[qr][d], kt[kr][d], s);
+    if (qc0 + qr < n && kc0 + kr < n)
+        sc[((size_t)h * n + qc0 + qr) * n + kc0 + kr] = s;
+}
+
+// sel[h][qc][0 .. kk) (kk = min(topk, n)): the local cubes first, then repeated argmax (the larger score, the
+// smaller index on ties); nsel[h][qc] = kk. One workgroup of 256 threads per (qc, h); n <= 4096.
+__global__ __launch_bounds__(256) void cube_topk(const float* __restrict__ sc, uint16_t* __restrict__ sel,
+                                                 uint16_t* __restrict__ nsel, uint32_t n, uint32_t kk,
+                                                 uint32_t local, uint32_t stride)
+{
+    __shared__ float scores[4096];
+    __shared__ float best_v[4];
+    __shared__ uint32_t best_i[4];
+    __shared__ uint32_t n_local;
+    const uint32_t qc = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const float* rowp = sc + ((size_t)h * n + qc) * n;
+    for (uint32_t i = tid; i < n; i += 256)
+        scores[i] = rowp[i];
+    uint16_t* out = sel + ((size_t)h * n + qc) * kk;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t it = 0;
+        if (local) {
+            const uint32_t picks[3] = {qc, qc >= stride ? qc - stride : n, qc + stride < n ? qc + stride : n};
+            for (uint32_t j = 0; j < local && it < kk; ++j)
+                if (picks[j] < n) {
+                    out[it++] = (uint16_t)picks[j];
+                    scores[picks[j]] = -INFINITY;
+                }
+        }
+        n_local = it;
+    }
+    __syncthreads();
+    for (uint32_t it = n_local; it < kk; ++it) {
+        float v = -INFINITY;
+        uint32_t idx = 0;
+        for (uint32_t i = tid; i < n; i += 256)
+            if (scores[i] > v) {
+                v = scores[i];
+                idx = i;
+            }
+#pragma unroll
+        for (uint32_t o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(v, o);
+            const uint32_t oi = __shfl_xor(idx, o);
+            if (ov > v || (ov == v && oi < idx)) {
+                v = ov;
+                idx = oi;
+            }
+        }
+        if (lane == 0) {
+            best_v[wv] = v;
+            best_i[wv] = idx;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float bv = best_v[0];
+            uint32_t bi = best_i[0];
+            for (uint32_t j = 1; j < 4; ++j)
+                if (best_v[j] > bv || (best_v[j] == bv && best_i[j] < bi)) {
+                    bv = best_v[j];
+                    bi = best_i[j];
+                }
+            out[it] = (uint16_t)bi;
+            scores[bi] = -INFINITY;
+        }
+        __syncthreads();
+    }
+    if (tid == 0)
+        nsel[(size_t)h * n + qc] = (uint16_t)kk;
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+size_t pooled_bytes(uint32_t heads, uint32_t n) { return ((size_t)heads * n * kD * sizeof(float) + 255) / 256 * 256; }
+
+template <class T, class TO>
+void launch_sparse(const SparseParams& p, hipStream_t s)
+{
+    const dim3 grid(p.heads / p.hs, p.n_qt);
+    if (p.hs == 2)
+        hipLaunchKernelGGL((flash_sparse<T, TO, 4>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((flash_sparse<T, TO, 2>), grid, dim3(128), 0, s, p);
+}
+
+}  // namespace
+}  // namespace mako
+
+using namespace mako;
+
+extern "C" size_t mako_cube_select_workspace(uint32_t heads, uint32_t n_cubes)
+{
+    return 2 * pooled_bytes(heads, n_cubes) + (size_t)heads * n_cubes * n_cubes * sizeof(float);
+}
+
+extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_cubes, uint32_t topk,
+                                uint32_t local, uint32_t stride, mako_dtype in, const void* q, const void* k,
+                                const uint32_t* cnt, uint16_t* sel, uint16_t* nsel, void* workspace,
+                                size_t workspace_bytes, void* stream)
+{
+    if (n_cubes > 4096 || !topk || (local != 0 && local != 1 && local != 3))
+        return fail(MAKO_EINVAL, "cube_select: %u cubes, top %u, local %u", n_cubes, topk, local);
+    if (!q || !k || !cnt || !sel || !nsel)
+        return fail(MAKO_EINVAL, "cube_select: a null argument");
+    if (in != MAKO_F16 && in != MAKO_BF16)
+        return fail(MAKO_EUNSUPPORTED, "cube_select: input type %d (f16 or bf16)", (int)in);
+    if ((uint64_t)n_cubes * kCube > q_pad || (uint64_t)n_cubes * kCube > k_pad)
+        return fail(MAKO_EINVAL, "cube_select: %u cubes of 64 rows exceed the tiles' %u / %u rows", n_cubes, q_pad,
+                    k_pad);
+    if (!workspace || workspace_bytes < mako_cube_select_workspace(heads, n_cubes) || !aligned16(workspace))
+        return fail(MAKO_EWORKSPACE, "cube_select: workspace of %zu bytes, %zu needed (16-byte aligned)",
+                    workspace_bytes, mako_cube_select_workspace(heads, n_cubes));
+    if (!heads || !n_cubes)
+        return ok();
+    float* qp = static_cast<float*>(workspace);
+    float* kp = reinterpret_cast<float*>(static_cast<char*>(workspace) + pooled_bytes(heads, n_cubes));
+    float* sc = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * pooled_bytes(heads, n_cubes));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 pgrid(n_cubes, heads, 2), sgrid((n_cubes + 15) / 16, (n_cubes + 15) / 16, heads), tgrid(n_cubes, heads);
+    if (in == MAKO_BF16)
+        hipLaunchKernelGGL(cube_pool<__bf16>, pgrid, dim3(kD), 0, s, static_cast<const __bf16*>(q),
+                           static_cast<const __bf16*>(k), cnt, qp, kp, n_cubes, q_pad, k_pad);
+    else
+        hipLaunchKernelGGL(cube_pool<_Float16>, pgrid, dim3(kD), 0, s, static_cast<const _Float16*>(q),
+                           static_cast<const _Float16*>(k), cnt, qp, kp, n_cubes, q_pad, k_pad);
+    hipLaunchKernelGGL(cube_scores, sgrid, dim3(256), 0, s, qp, kp, sc, n_cubes);
+    hipLaunchKernelGGL(cube_topk, tgrid, dim3(256), 0, s, sc, sel, nsel, n_cubes, std::min(topk, n_cubes), local,
+                       stride);
+    return check_launch("cube_select");
+}
+
+extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q,
+                                const void* k, const void* v, void* o, const uint16_t* sel, const uint16_t* nsel,
+                                const uint8_t* valid, const int32_t* map, float* lse, void* stream)
+{
+    if (!a || !q || !k || !v || !o || !valid || !map || ((!sel || !nsel) && a->n_cubes))
+        return fail(MAKO_EINVAL, "attention_sparse: a null argument");
+    if (a->q_pad % 64 || a->k_pad % 128 || a->dense0 % 32)
+        return fail(MAKO_EINVAL,
+                    "attention_sparse: q_pad a multiple of 64, k_pad of 128, the dense rows from a multiple of 32");
+    if (in != MAKO_F16 && in != MAKO_BF16)
+        return fail(MAKO_EUNSUPPORTED, "attention_sparse: input type %d (f16 or bf16)", (int)in);
+    if (out != MAKO_F32 && out != in)
+        return fail(MAKO_EUNSUPPORTED, "attention_sparse: output type %d (f32 or the input's)", (int)out);
+    if (!a->heads || !a->kv_heads || a->heads % a->kv_heads)
+        return fail(MAKO_EINVAL, "attention_sparse: %u heads over %u kv heads", a->heads, a->kv_heads);
+    if (a->sel_heads != a->heads && a->sel_heads != a->kv_heads)
+        return fail(MAKO_EINVAL, "attention_sparse: sel rows for %u heads (heads %u or kv heads %u)", a->sel_heads,
+                    a->heads, a->kv_heads);
+    if (a->n_q > a->q_pad || a->n_k > a->k_pad || a->dense0 > a->dense1 || a->dense1 > a->k_pad ||
+        (uint64_t)a->n_cubes * kCube > a->k_pad || (a->n_cubes && !a->max_sel))
+        return fail(MAKO_EINVAL, "attention_sparse: %u queries in %u rows, %u keys in %u, dense rows [%u, %u), %u "
+                    "cubes of %u selections", a->n_q, a->q_pad, a->n_k, a->k_pad, a->dense0, a->dense1, a->n_cubes,
+                    a->max_sel);
+    if ((uint64_t)a->heads * kD > a->width || a->width % 4)
+        return fail(MAKO_EINVAL, "attention_sparse: o rows of %u for %u heads of 128", a->width, a->heads);
+    if ((uint64_t)a->k_pad * kD * 2 > 0x7fffffffu)
+        return fail(MAKO_EINVAL, "attention_sparse: %u key rows exceed 2 GiB a head", a->k_pad);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return fail(MAKO_EINVAL, "attention_sparse: q, k, v and o must be 16-byte aligned");
+    if (a->n_q == 0)
+        return ok();
+    const uint32_t group = a->heads / a->kv_heads;
+    const uint32_t hs = (a->sel_heads == a->kv_heads && group % 2 == 0) ? 2 : 1;
+    const SparseParams p{q, k, v, o, lse, sel, nsel, valid, map, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads,
+                         a->kv_heads, a->width, a->scale * kLog2e, a->n_cubes, a->max_sel, a->dense0, a->dense1,
+                         a->causal ? 1u : 0u, a->sel_heads, group, hs, (a->n_q + kCube - 1) / kCube};
+    if (p.n_qt > 65535)
+        return fail(MAKO_EINVAL, "attention_sparse: %u query tiles exceed the grid", p.n_qt);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (in == MAKO_BF16) {
+        if (out == MAKO_F32)
+            launch_sparse<__bf16, float>(p, s);
+        else
+            launch_sparse<__bf16, __bf16>(p, s);
+    } else {
+        if (out == MAKO_F32)
+            launch_sparse<_Float16, float>(p, s);
+        else
+            launch_sparse<_Float16, _Float16>(p, s);
+    }
+    return check_launch("attention_sparse");
+}

@@ -136,3 +136,25 @@ def attn_decode(a, q, k, v, ctx_len, o, workspace, *, lse=None, stream=None):
                                   _ptr(ctx_len), _ptr(o), _ptr(lse), _ptr(workspace),
                                   0 if workspace is None else workspace.numel() * workspace.element_size(),
                                   _stream(stream)))
+
+
+def window_random_blocks(n_blocks, lists, window=8, n_random=8, seed=0):
+    """Block lists for causal block-sparse attention over n_blocks 64-row blocks: block qb attends itself (the
+    diagonal, causally masked inside), the `window` blocks before it, and `n_random` distinct blocks drawn
+    uniformly from the earlier ones (fewer when fewer exist), for each of `lists` lists (one per kv head).
+    Returns (sel u16 [lists][n_blocks][1 + window + n_random], nsel u16 [lists][n_blocks]) as numpy arrays."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    width = 1 + window + n_random
+    sel = np.zeros((lists, n_blocks, width), np.uint16)
+    nsel = np.zeros((lists, n_blocks), np.uint16)
+    for li in range(lists):
+        for qb in range(n_blocks):
+            picks = [qb] + list(range(qb - 1, max(qb - 1 - window, -1), -1))
+            early = qb - window
+            if early > 0:
+                picks += sorted(rng.choice(early, size=min(n_random, early), replace=False).tolist())
+            sel[li, qb, :len(picks)] = picks
+            nsel[li, qb] = len(picks)
+    return sel, nsel
