@@ -1,0 +1,97 @@
+// The launch side of the attention path on HIP: what src/gpu/runtime.hpp gives the reference's engines, for the
+// parts the attention path uses (named scratch buffers, one in-order launch queue, finish() raising device errors,
+// per-kernel telemetry, the step statistics). Kernels are reached through the C ABI of include/mako_attn.h, not
+// by name: the typed entry points replace the pipeline lookup (src/gpu/runtime.cpp:127-135).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <chrono>
+#include <cstdint>
+#include <map>
+#include <optional>
+#include <string>
+#include <string_view>
+#include <vector>
+
+namespace mako::gpu {
+
+// How much a step measures (src/gpu/runtime.hpp:21-26): at the kernels level every launch is bracketed by a pair
+// of HIP events and labelled.
+enum class Telemetry { off, summary, steps, layers, kernels };
+std::optional<Telemetry> parse_telemetry(std::string_view s);
+
+struct KernelTime {
+    std::string kernel;
+    double ms = 0;
+    uint32_t count = 0;
+};
+
+// Device memory (what an MTL::Buffer at offset 0 was): a hipMalloc'd pointer and its size.
+struct Buffer {
+    void* ptr = nullptr;
+    uint64_t bytes = 0;
+};
+
+// The launch queue a step records into (what the compute command encoder was): one HIP stream at the default
+// priority, launches in order, results visible after Runtime::finish.
+struct Encoder {
+    hipStream_t stream = nullptr;
+};
+
+class Runtime {
+public:
+    struct Stats {
+        double gpu_wait_ms = 0, gpu_exec_ms = 0;  // wait: finish() blocked; exec: timed launches, summed
+        double encode_ms = 0, step_ms = 0;        // encode: step start to finish()
+    };
+    const Stats& stats() const { return stats_; }
+    // Bytes of all scratch buffers allocated so far.
+    uint64_t scratch_bytes() const;
+    // At the kernels level: the launches' GPU times since the last call, summed per kernel.
+    std::vector<KernelTime> kernel_times();
+
+    Runtime(const Runtime&) = delete;
+    Runtime& operator=(const Runtime&) = delete;
+
+protected:
+    explicit Runtime(Telemetry telemetry, int device = 0);
+    virtual ~Runtime();
+
+    // A named device buffer of at least `bytes`, reallocated (after the queue drains) when too small
+    // (src/gpu/runtime.cpp:117-125). Its contents survive until then.
+    Buffer* scratch(const std::string& name, uint64_t bytes);
+    void drop_scratch(const std::string& name);
+    // The step's launch queue; `enc` stays valid for the Runtime's life.
+    Encoder* encoder();
+    // Before / after a launch: at the kernels level, events around it, labelled `kernel` (the reference closed
+    // and reopened the encoder, src/gpu/runtime.cpp:362-370).
+    void before(Encoder* enc);
+    void after(Encoder*& enc, std::string_view kernel);
+    // Waits for every launch of the queue and raises std::runtime_error if one failed
+    // (src/gpu/runtime.cpp:453-475).
+    void finish(Encoder* enc);
+    // Turns a nonzero C ABI status into std::runtime_error carrying the library's message.
+    static void check(int status);
+
+    int device_ = 0;
+    Telemetry tel_ = Telemetry::off;
+    Encoder enc_;
+    std::map<std::string, Buffer> scratch_;
+    Stats stats_;
+
+private:
+    struct Timed {
+        hipEvent_t start = nullptr, end = nullptr;
+        std::string kernel;
+    };
+    std::vector<Timed> timed_;
+    std::vector<hipEvent_t> spare_events_;
+    std::vector<KernelTime> kernels_;
+    std::chrono::steady_clock::time_point step_start_;
+    bool encoding_ = false;
+    hipEvent_t event();
+    void resolve_times();
+};
+
+}  // namespace mako::gpu

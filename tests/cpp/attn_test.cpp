@@ -1,0 +1,199 @@
+// Dense and decode attention through TransformerRuntime against the CPU oracle:
+// * attention() with the reference's own arguments and defaults (f16 tiles in, f32 rows out): causal GQA at
+//   batch 1, 16 query heads over 8 kv heads, D 128, S 512 (the call QwenText::encode makes,
+//   src/models/qwen_text.cpp:311), every row;
+// * the same call with AttnOptions: bf16 in and out and an LSE, bidirectional (block 0, the call H3::block makes,
+//   src/models/h3.cpp:364);
+// * attention_decode: 4 sequences of different contexts, GQA 4;
+// * the refusal of a head width the reference refuses (src/models/runtime.cpp:266-267).
+// Tolerance: every element within 2e-3 + 1e-2 |ref|; LSE within 1e-3.
+//   attn_test
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "attn_oracle.h"
+#include "transformer_runtime.hpp"
+
+namespace {
+
+class Harness final : public mako::models::TransformerRuntime {
+public:
+    Harness() : TransformerRuntime(mako::gpu::Telemetry::kernels) {}
+    using TransformerRuntime::attention;
+    using TransformerRuntime::attention_decode;
+    using TransformerRuntime::encoder;
+    using TransformerRuntime::finish;
+    using TransformerRuntime::scratch;
+};
+
+int failures = 0;
+void check(bool ok, const std::string& what)
+{
+    std::printf("  %s  %s\n", ok ? "ok  " : "FAIL", what.c_str());
+    failures += !ok;
+}
+
+uint64_t rng_state = 12345;
+double normal()
+{
+    auto next = [] {
+        uint64_t z = (rng_state += 0x9e3779b97f4a7c15ull);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        return z ^ (z >> 31);
+    };
+    const double u1 = ((next() >> 11) + 0.5) * 0x1.0p-53, u2 = (next() >> 11) * 0x1.0p-53;
+    return std::sqrt(-2.0 * std::log(u1)) * std::cos(2 * M_PI * u2);
+}
+
+std::vector<uint16_t> random_tile(size_t n, int dtype)
+{
+    std::vector<uint16_t> v(n);
+    for (auto& x : v)
+        x = dtype == ORACLE_F16 ? oracle_f32_to_f16(float(normal())) : oracle_f32_to_bf16(float(normal()));
+    return v;
+}
+
+template <class T>
+mako::gpu::Buffer* put(Harness& h, const std::string& name, const std::vector<T>& v)
+{
+    auto* b = h.scratch(name, v.size() * sizeof(T));
+    if (hipMemcpy(b->ptr, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+        throw std::runtime_error("hipMemcpy");
+    return b;
+}
+
+template <class T>
+std::vector<T> get(const mako::gpu::Buffer* b, size_t n)
+{
+    std::vector<T> v(n);
+    if (hipMemcpy(v.data(), b->ptr, n * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+        throw std::runtime_error("hipMemcpy");
+    return v;
+}
+
+float widen(uint16_t b, bool bf16)
+{
+    if (!bf16)
+        return oracle_f16_to_f32(b);
+    const uint32_t u = uint32_t(b) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Elements past 2e-3 + 1e-2 |ref| and the largest LSE error.
+uint64_t bad_elems(const std::vector<float>& got, const std::vector<double>& want)
+{
+    uint64_t bad = 0;
+    for (size_t i = 0; i < want.size(); ++i)
+        bad += !(std::fabs(got[i] - want[i]) <= 2e-3 + 1e-2 * std::fabs(want[i]));
+    return bad;
+}
+
+double lse_err(const std::vector<float>& got, const std::vector<double>& want)
+{
+    double e = 0;
+    for (size_t i = 0; i < want.size(); ++i)
+        e = std::max(e, std::isinf(want[i]) ? (got[i] == want[i] ? 0.0 : 1.0) : std::fabs(got[i] - want[i]));
+    return e;
+}
+
+}  // namespace
+
+int main()
+{
+    std::setvbuf(stdout, nullptr, _IOLBF, 0);
+    Harness h;
+    // Causal GQA, f16 in, f32 out: the reference's call and defaults.
+    {
+        const uint32_t heads = 16, kv = 8, D = 128, S = 512;
+        const auto q = random_tile(size_t(heads) * S * D, ORACLE_F16), k = random_tile(size_t(kv) * S * D, ORACLE_F16),
+                   v = random_tile(size_t(kv) * S * D, ORACLE_F16);
+        auto qb = put(h, "q", q), kb = put(h, "k", k), vb = put(h, "v", v);
+        auto ob = h.scratch("o", size_t(S) * heads * D * 4);
+        auto* enc = h.encoder();
+        h.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX);
+        h.finish(enc);
+        const oracle_attn_args a{S, S, S, S, heads, kv, 0, UINT32_MAX, heads * D, 1.0f / std::sqrt(float(D))};
+        std::vector<double> want(size_t(S) * heads * D);
+        oracle_attn_dense(&a, D, ORACLE_F16, q.data(), k.data(), v.data(), want.data(), nullptr, 0);
+        const uint64_t bad = bad_elems(get<float>(ob, want.size()), want);
+        check(bad == 0, "attention, causal GQA S512 f16 -> f32: " + std::to_string(bad) + " elements out of tolerance");
+    }
+    // Bidirectional, bf16 in and out, with the LSE.
+    {
+        const uint32_t heads = 4, kv = 4, D = 128, S = 300, q_pad = 320, k_pad = 384;
+        const auto q = random_tile(size_t(heads) * q_pad * D, ORACLE_BF16),
+                   k = random_tile(size_t(kv) * k_pad * D, ORACLE_BF16),
+                   v = random_tile(size_t(kv) * k_pad * D, ORACLE_BF16);
+        auto qb = put(h, "q", q), kb = put(h, "k", k), vb = put(h, "v", v);
+        auto ob = h.scratch("o", size_t(S) * heads * D * 2);
+        auto lb = h.scratch("lse", size_t(heads) * S * 4);
+        mako::models::AttnOptions opt;
+        opt.in = MAKO_BF16;
+        opt.out = MAKO_BF16;
+        opt.lse = lb;
+        auto* enc = h.encoder();
+        h.attention(enc, qb, kb, vb, ob, S, q_pad, S, k_pad, heads, kv, 0, 0, D, opt);
+        h.finish(enc);
+        const oracle_attn_args a{S, q_pad, S, k_pad, heads, kv, 0, 0, heads * D, 1.0f / std::sqrt(float(D))};
+        std::vector<double> want(size_t(S) * heads * D), want_l(size_t(heads) * S);
+        oracle_attn_dense(&a, D, ORACLE_BF16, q.data(), k.data(), v.data(), want.data(), want_l.data(), 0);
+        const auto ob16 = get<uint16_t>(ob, want.size());
+        std::vector<float> got(ob16.size());
+        for (size_t i = 0; i < got.size(); ++i)
+            got[i] = widen(ob16[i], true);
+        const uint64_t bad = bad_elems(got, want);
+        const double le = lse_err(get<float>(lb, want_l.size()), want_l);
+        check(bad == 0 && le <= 1e-3, "attention, bidirectional S300 bf16 -> bf16 + LSE: " + std::to_string(bad) +
+                                          " elements out of tolerance, LSE error " + std::to_string(le));
+    }
+    // Decode: 4 sequences, 32 query heads over 8 kv heads.
+    {
+        const uint32_t batch = 4, heads = 32, kv = 8, D = 128, cap = 3000;
+        const std::vector<uint32_t> ctx{1, 700, 2048, 3000};
+        const auto q = random_tile(size_t(batch) * heads * D, ORACLE_F16),
+                   k = random_tile(size_t(batch) * kv * cap * D, ORACLE_F16),
+                   v = random_tile(size_t(batch) * kv * cap * D, ORACLE_F16);
+        auto qb = put(h, "q", q), kb = put(h, "k", k), vb = put(h, "v", v), cb = put(h, "ctx", ctx);
+        auto ob = h.scratch("o", size_t(batch) * heads * D * 4);
+        auto lb = h.scratch("lse", size_t(batch) * heads * 4);
+        mako::models::AttnOptions opt;
+        opt.lse = lb;
+        auto* enc = h.encoder();
+        h.attention_decode(enc, qb, kb, vb, cb, ob, batch, heads, kv, cap, cap, opt);
+        h.finish(enc);
+        std::vector<double> want(size_t(batch) * heads * D), want_l(size_t(batch) * heads);
+        oracle_attn_decode(batch, heads, kv, D, cap, 1.0f / std::sqrt(float(D)), ORACLE_F16, q.data(), k.data(),
+                           v.data(), ctx.data(), want.data(), want_l.data(), 0);
+        const uint64_t bad = bad_elems(get<float>(ob, want.size()), want);
+        const double le = lse_err(get<float>(lb, want_l.size()), want_l);
+        check(bad == 0 && le <= 1e-3, "attention_decode, 4 sequences: " + std::to_string(bad) +
+                                          " elements out of tolerance, LSE error " + std::to_string(le));
+    }
+    // A head width the reference refuses.
+    {
+        auto* enc = h.encoder();
+        auto* b = h.scratch("q", 16);
+        bool threw = false;
+        try {
+            h.attention(enc, b, b, b, b, 1, 64, 1, 128, 1, 1, 0, 0, 96);
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()) == "attention: heads of 96";
+        }
+        check(threw, "attention refuses heads of 96");
+        h.finish(enc);
+    }
+    for (const auto& kt : h.kernel_times())
+        std::printf("  %-20s %3u launches %8.3f ms\n", kt.kernel.c_str(), kt.count, kt.ms);
+    std::printf("%s\n", failures ? "FAILED" : "all passed");
+    return failures ? 1 : 0;
+}

@@ -29,6 +29,13 @@ def test_library_exports_every_declared_symbol():
     assert L.mako_attn_abi_version() == 1
 
 
+def test_host_library_loads():
+    """The C++ host side (libmako_host.so) loads and resolves against libmako_attn.so."""
+    path = os.path.join(ROOT, "mako-common_amd", "lib", "libmako_host.so")
+    assert os.path.exists(path)
+    ctypes.CDLL(path)
+
+
 FAKE = ctypes.c_void_p(0x10000)  # aligned, never dereferenced: every call below fails validation first
 
 
