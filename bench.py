@@ -169,6 +169,36 @@ def bench_bidir(torch, M, steps, warmup):
     return {"ms": ms, "tflops": tflops, "flop": flop, "frac": tflops / PEAK_TFLOPS}
 
 
+def bench_sparse(torch, M, steps, warmup):
+    """Block-sparse causal attention, S16384, 32 query heads over 8 kv heads, 64x64 blocks: each block attends
+    itself (causal), the 8 before it and 8 random earlier ones (seed 16384, one list per kv head)."""
+    import numpy as np
+
+    S, H, KV, D = 16384, 32, 8, 128
+    nb = S // 64
+    sel, nsel = M.window_random_blocks(nb, KV, seed=16384)
+    gen = torch.Generator(device="cuda").manual_seed(16384)
+    q = torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
+    sel_d = torch.from_numpy(sel.view(np.int16)).to("cuda")
+    nsel_d = torch.from_numpy(nsel.view(np.int16)).to("cuda")
+    valid = torch.ones(S, dtype=torch.uint8, device="cuda")
+    map_ = torch.arange(S, dtype=torch.int32, device="cuda")
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, n_cubes=nb, max_sel=sel.shape[2], dense0=S,
+                dense1=S, causal=1, sel_heads=KV)
+    ms = time_launches(torch, lambda: M.attn_sparse(q, k, v, o, sel_d, nsel_d, valid, map_, **args), steps, warmup)
+    blocks = int(nsel[0].astype(np.int64).sum())          # blocks a head attends (the same count for every list)
+    pairs = (blocks - nb) * 64 * 64 + nb * (64 * 65 // 2)  # full blocks, plus the causal diagonal ones
+    flop = 4.0 * D * pairs * H
+    gathered = float(blocks) * KV * 64 * D * 2 * 2        # K + V of each block once per (query block, kv head)
+    tflops, gbps = flop / (ms * 1e-3) / 1e12, gathered / (ms * 1e-3) / 1e9
+    t_mfma, t_hbm = flop / (PEAK_TFLOPS * 1e12), gathered / (PEAK_GBPS * 1e9)
+    return {"ms": ms, "tflops": tflops, "gbps": gbps, "flop": flop, "gathered_bytes": gathered, "blocks": blocks,
+            "bound": "mfma" if t_mfma >= t_hbm else "hbm", "frac": max(t_mfma, t_hbm) / (ms * 1e-3)}
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the reference point that scales the HBM byte counters."""
     n = 256 << 20
@@ -184,7 +214,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
-    ap.add_argument("--only", choices=["prefill", "decode", "bidir", "copy"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "bidir", "sparse", "copy"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -203,6 +233,7 @@ def main():
         fn = {"prefill": lambda: bench_prefill(torch, M, args.steps, args.warmup, False),
               "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, False),
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup),
+              "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps, args.warmup)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
@@ -212,6 +243,7 @@ def main():
     pre = bench_prefill(torch, M, args.steps, args.warmup, with_cpu)
     dec = bench_decode(torch, M, args.steps, args.warmup, with_cpu)
     bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup))
+    spa = bench_sparse(torch, M, args.steps, args.warmup)
     line = {
         "metric": "attn prefill TFLOP/s (Qwen3-8B shape, seq 4096) + decode KV HBM GB/s, 1 GPU",
         "value": round(pre["tflops"], 2),
@@ -237,6 +269,11 @@ def main():
         "bidirectional": {"value": round(bid["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(bid["ms"], 4),
                           "frac": round(bid["frac"], 4),
                           "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16"}},
+        "block_sparse": {"value": round(spa["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(spa["ms"], 4),
+                         "gathered_gbps": round(spa["gbps"], 1), "bound": spa["bound"], "frac": round(spa["frac"], 4),
+                         "config": {"workload": "causal block-sparse, 32 query heads / 8 kv heads, D 128, S 16384, "
+                                                "64x64 blocks: diagonal + 8 preceding + 8 random earlier (seed "
+                                                "16384, per kv head), bf16", "blocks_per_head": spa["blocks"]}},
     }
     if with_cpu:
         line["cpu_baseline"] = pre["cpu_baseline"]
