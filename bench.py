@@ -5,12 +5,13 @@ Headline (one JSON line): causal GQA prefill at the Qwen3-8B shape (batch 1, 32 
 D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only the unmasked pairs
 (4 * D * S (S + 1) / 2 * 32). Beside it: batch-16 decode against a contiguous f16 KV cache (contexts drawn
 uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
-S16384 24-head case in TFLOP/s. Inputs are synthetic N(0, 1), resident in HBM before the timed region. Each
-figure is the mean launch duration over --steps back-to-back launches (HIP events on the launch stream) after
---warmup untimed ones. The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
+S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s. Inputs are synthetic N(0, 1), resident in
+HBM before the timed region. `value` and ms_per_step come from --steps back-to-back launches bracketed by HIP
+events on the launch stream, after --warmup untimed ones; the roofline's `achieved` divides by the mean of each
+launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
 a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill|decode|bidir|copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill|decode|bidir|sparse|copy]
 """
 import argparse
 import json
@@ -28,18 +29,34 @@ CPU_SECONDS = 8.0     # wall-clock budget of each CPU-baseline leg
 
 
 def time_launches(torch, fn, steps, warmup):
-    """Mean duration (ms) of one launch of fn over `steps` back-to-back launches, by HIP events on the current
-    stream (the stream the C ABI launches on), after `warmup` untimed launches."""
+    """Times `steps` back-to-back launches of fn after `warmup` untimed ones, by HIP events on the current stream
+    (the stream the C ABI launches on). Returns (ms a step over the whole timed region, the mean of each launch's
+    own event pair): the first is the step time, the second the kernel duration the roofline divides."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(steps):
+    for a, b in ev:
+        a.record()
         fn()
+        b.record()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return start.elapsed_time(end) / steps, sum(a.elapsed_time(b) for a, b in ev) / steps
+
+
+def traffic(kernel):
+    """HBM bytes a launch of `kernel` moves, from the committed counter summary (profiles/traffic.json: two
+    rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a copy of known size);
+    None when the summary does not cover the kernel."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get("kernels", {}).get(kernel)
+    return None if entry is None else entry["bytes_per_launch"]
 
 
 def cpu_threads():
@@ -74,12 +91,13 @@ def bench_prefill(torch, M, steps, warmup, with_cpu):
     o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
     lse = torch.empty((H, S), dtype=torch.float32, device="cuda")
     args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, q_pos0=0, block=U32_MAX, dim=D)
-    ms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
+    ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
     flop = 4.0 * D * (S * (S + 1) / 2) * H
-    tflops = flop / (ms * 1e-3) / 1e12
-    out = {"ms": ms, "tflops": tflops, "flop": flop,
-           "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": tflops / PEAK_TFLOPS, "traffic": None, "kernel": "flash_fwd<bf16,bf16,128>"}}
+    tflops, ktflops = flop / (ms * 1e-3) / 1e12, flop / (kms * 1e-3) / 1e12
+    out = {"ms": ms, "kernel_ms": kms, "tflops": tflops, "flop": flop,
+           "roofline": {"bound": "mfma", "achieved": ktflops, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": ktflops / PEAK_TFLOPS, "traffic": traffic("flash_fwd_causal_s4096"),
+                        "kernel": "flash_fwd<bf16,bf16,128>", "kernel_ms": kms}}
     if with_cpu:
         import oracle as O
 
@@ -121,13 +139,14 @@ def bench_decode(torch, M, steps, warmup, with_cpu):
     lse = torch.empty((B, H), dtype=torch.float32, device="cuda")
     a = M.decode_args(batch=B, heads=H, kv_heads=KV, dim=D, cap=cap, max_ctx=cap)
     ws = torch.empty(M.decode_workspace(a), dtype=torch.uint8, device="cuda")
-    ms = time_launches(torch, lambda: M.attn_decode(a, q, k, v, ctx_d, o, ws, lse=lse), steps, warmup)
+    ms, kms = time_launches(torch, lambda: M.attn_decode(a, q, k, v, ctx_d, o, ws, lse=lse), steps, warmup)
     nbytes = float(4096 * ctx.astype(np.int64).sum())  # K + V: kv_heads * D * 2 bytes * 2 tensors per token
-    gbps = nbytes / (ms * 1e-3) / 1e9
-    out = {"ms": ms, "gbps": gbps, "bytes": nbytes, "sum_ctx": int(ctx.sum()),
-           "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s",
-                        "frac": gbps / PEAK_GBPS, "traffic": None,
-                        "kernel": "decode_split<f16> + decode_merge<f16> (one step)"}}
+    gbps, kgbps = nbytes / (ms * 1e-3) / 1e9, nbytes / (kms * 1e-3) / 1e9
+    out = {"ms": ms, "kernel_ms": kms, "gbps": gbps, "bytes": nbytes, "sum_ctx": int(ctx.sum()),
+           "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_GBPS, "unit": "GB/s",
+                        "frac": kgbps / PEAK_GBPS, "traffic": traffic("decode_batch16"),
+                        "kernel": "decode_split<f16> + decode_merge<f16> (one step, both kernels)",
+                        "kernel_ms": kms}}
     if with_cpu:
         import oracle as O
 
@@ -163,10 +182,10 @@ def bench_bidir(torch, M, steps, warmup):
     q, k, v = (torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(3))
     o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
     args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=H, q_pos0=0, block=0, dim=D)
-    ms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, **args), steps, warmup)
+    ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, **args), steps, warmup)
     flop = 4.0 * D * S * S * H
     tflops = flop / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "flop": flop, "frac": tflops / PEAK_TFLOPS}
+    return {"ms": ms, "kernel_ms": kms, "tflops": tflops, "flop": flop, "frac": flop / (kms * 1e-3) / 1e12 / PEAK_TFLOPS}
 
 
 def bench_sparse(torch, M, steps, warmup):
@@ -188,15 +207,16 @@ def bench_sparse(torch, M, steps, warmup):
     map_ = torch.arange(S, dtype=torch.int32, device="cuda")
     args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, n_cubes=nb, max_sel=sel.shape[2], dense0=S,
                 dense1=S, causal=1, sel_heads=KV)
-    ms = time_launches(torch, lambda: M.attn_sparse(q, k, v, o, sel_d, nsel_d, valid, map_, **args), steps, warmup)
+    ms, kms = time_launches(torch, lambda: M.attn_sparse(q, k, v, o, sel_d, nsel_d, valid, map_, **args), steps,
+                            warmup)
     blocks = int(nsel[0].astype(np.int64).sum())          # blocks a head attends (the same count for every list)
     pairs = (blocks - nb) * 64 * 64 + nb * (64 * 65 // 2)  # full blocks, plus the causal diagonal ones
     flop = 4.0 * D * pairs * H
     gathered = float(blocks) * KV * 64 * D * 2 * 2        # K + V of each block once per (query block, kv head)
     tflops, gbps = flop / (ms * 1e-3) / 1e12, gathered / (ms * 1e-3) / 1e9
     t_mfma, t_hbm = flop / (PEAK_TFLOPS * 1e12), gathered / (PEAK_GBPS * 1e9)
-    return {"ms": ms, "tflops": tflops, "gbps": gbps, "flop": flop, "gathered_bytes": gathered, "blocks": blocks,
-            "bound": "mfma" if t_mfma >= t_hbm else "hbm", "frac": max(t_mfma, t_hbm) / (ms * 1e-3)}
+    return {"ms": ms, "kernel_ms": kms, "tflops": tflops, "gbps": gbps, "flop": flop, "gathered_bytes": gathered,
+            "blocks": blocks, "bound": "mfma" if t_mfma >= t_hbm else "hbm", "frac": max(t_mfma, t_hbm) / (kms * 1e-3)}
 
 
 def bench_copy(torch, steps, warmup):
@@ -204,8 +224,8 @@ def bench_copy(torch, steps, warmup):
     n = 256 << 20
     src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
-    ms = time_launches(torch, lambda: dst.copy_(src), steps, warmup)
-    return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbps": 2 * n / (ms * 1e-3) / 1e9}
+    ms, kms = time_launches(torch, lambda: dst.copy_(src), steps, warmup)
+    return {"bytes_read": n, "bytes_written": n, "ms": ms, "kernel_ms": kms, "gbps": 2 * n / (kms * 1e-3) / 1e9}
 
 
 def main():
@@ -267,9 +287,11 @@ def main():
                                               "sum_ctx": dec["sum_ctx"]},
                    "roofline": dec["roofline"]},
         "bidirectional": {"value": round(bid["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(bid["ms"], 4),
+                          "kernel_ms": round(bid["kernel_ms"], 4),
                           "frac": round(bid["frac"], 4),
                           "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16"}},
         "block_sparse": {"value": round(spa["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(spa["ms"], 4),
+                         "kernel_ms": round(spa["kernel_ms"], 4),
                          "gathered_gbps": round(spa["gbps"], 1), "bound": spa["bound"], "frac": round(spa["frac"], 4),
                          "config": {"workload": "causal block-sparse, 32 query heads / 8 kv heads, D 128, S 16384, "
                                                 "64x64 blocks: diagonal + 8 preceding + 8 random earlier (seed "
