@@ -11,7 +11,7 @@ events on the launch stream, after --warmup untimed ones; the roofline's `achiev
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
 a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill|decode|bidir|sparse|copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,copy]
 """
 import argparse
 import json
@@ -26,15 +26,22 @@ PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA
 PEAK_GBPS = 8000.0    # MI355X HBM3E
 U32_MAX = 0xFFFFFFFF
 CPU_SECONDS = 8.0     # wall-clock budget of each CPU-baseline leg
+WARM_SECONDS = 0.3    # least untimed GPU work before each timed region
 
 
 def time_launches(torch, fn, steps, warmup):
     """Times `steps` back-to-back launches of fn after `warmup` untimed ones, by HIP events on the current stream
     (the stream the C ABI launches on). Returns (ms a step over the whole timed region, the mean of each launch's
-    own event pair): the first is the step time, the second the kernel duration the roofline divides."""
+    own event pair): the first is the step time, the second the kernel duration the roofline divides. The untimed
+    warmup also runs for at least WARM_SECONDS, so the GPU's clocks have settled before the timed region."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARM_SECONDS:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -234,7 +241,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
-    ap.add_argument("--only", choices=["prefill", "decode", "bidir", "sparse", "copy"], default=None)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -254,8 +262,11 @@ def main():
               "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, False),
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup),
-              "copy": lambda: bench_copy(torch, args.steps, args.warmup)}[args.only]
-        print(json.dumps({args.only: fn()}), flush=True)
+              "copy": lambda: bench_copy(torch, args.steps, args.warmup)}
+        for leg in args.only.split(","):
+            if leg not in fn:
+                ap.error(f"--only: unknown leg {leg!r}")
+            print(json.dumps({leg: fn[leg]()}), flush=True)
         return
     with_cpu = not args.no_cpu
     if with_cpu:

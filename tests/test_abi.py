@@ -61,6 +61,8 @@ def fwd_rc(**kw):
     (dict(args=dict(width=256)), M.EINVAL, "o rows"),
     (dict(q=None), M.EINVAL, "null"),
     (dict(k=ctypes.c_void_p(0x10002)), M.EINVAL, "aligned"),
+    (dict(args=dict(scale=0.0)), M.EINVAL, "scale"),
+    (dict(args=dict(scale=-0.088)), M.EINVAL, "scale"),
 ])
 def test_fwd_refuses(kw, code, msg):
     rc, err = fwd_rc(**kw)
