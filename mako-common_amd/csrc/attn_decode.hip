@@ -399,6 +399,8 @@ extern "C" int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_d
         return fail(MAKO_EINVAL, "attention_decode: %u keys a split (a multiple of 64, or 0)", a->split);
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return fail(MAKO_EINVAL, "attention_decode: q, k, v and o must be 16-byte aligned");
+    if (!(a->scale > 0.0f) || a->scale == INFINITY)
+        return fail(MAKO_EINVAL, "attention_decode: scale %g (positive and finite)", (double)a->scale);
     const uint32_t resident = resident_waves();
     if (!resident)
         return fail(MAKO_EHIP, "attention_decode: no device to size the split for");

@@ -466,6 +466,8 @@ extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_d
         return fail(MAKO_EINVAL, "attention_sparse: %u key rows exceed 2 GiB a head", a->k_pad);
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return fail(MAKO_EINVAL, "attention_sparse: q, k, v and o must be 16-byte aligned");
+    if (!(a->scale > 0.0f) || a->scale == INFINITY)
+        return fail(MAKO_EINVAL, "attention_sparse: scale %g (positive and finite)", (double)a->scale);
     if (a->n_q == 0)
         return ok();
     const uint32_t group = a->heads / a->kv_heads;

@@ -67,3 +67,45 @@ def fwd_rc(**kw):
 def test_fwd_refuses(kw, code, msg):
     rc, err = fwd_rc(**kw)
     assert rc == code and msg in err, (rc, err)
+
+
+def sparse_rc(**kw):
+    a = dict(n_q=64, q_pad=64, n_k=128, k_pad=128, heads=4, kv_heads=2, width=512, scale=0.088, n_cubes=1, max_sel=1,
+             dense0=0, dense1=0, causal=1, sel_heads=4)
+    a.update(kw)
+    args = M.SparseArgs(*[a[f] for f, _ in M.SparseArgs._fields_])
+    rc = M.lib().mako_attn_sparse(ctypes.byref(args), M.BF16, M.BF16, *([FAKE] * 8), None, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(q_pad=65), M.EINVAL, "multiple of 64"),
+    (dict(heads=3), M.EINVAL, "heads over"),
+    (dict(sel_heads=3), M.EINVAL, "sel rows"),
+    (dict(n_cubes=3), M.EINVAL, "cubes of"),
+    (dict(width=100), M.EINVAL, "o rows"),
+    (dict(scale=0.0), M.EINVAL, "scale"),
+])
+def test_sparse_refuses(kw, code, msg):
+    rc, err = sparse_rc(**kw)
+    assert rc == code and msg in err, (rc, err)
+
+
+def decode_rc(**kw):
+    a = dict(batch=2, heads=8, kv_heads=2, dim=128, cap=256, max_ctx=256, split=0, scale=0.088)
+    a.update(kw)
+    args = M.DecodeArgs(*[a[f] for f, _ in M.DecodeArgs._fields_])
+    rc = M.lib().mako_attn_decode(ctypes.byref(args), M.BF16, M.BF16, *([FAKE] * 6), FAKE, 1 << 20, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dim=64), M.EUNSUPPORTED, "heads of 64"),
+    (dict(heads=7), M.EINVAL, "kv heads"),
+    (dict(max_ctx=512), M.EINVAL, "max_ctx"),
+    (dict(split=100), M.EINVAL, "a split"),
+    (dict(scale=float("inf")), M.EINVAL, "scale"),
+])
+def test_decode_refuses(kw, code, msg):
+    rc, err = decode_rc(**kw)
+    assert rc == code and msg in err, (rc, err)
