@@ -321,9 +321,7 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
         #pragma unroll
         for (int kk = 0; kk < NKK; ++kk)
             qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 16 * kk * sizeof(T)));
-        #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
-            settle(qreg[kk]);
+        // (settled after the first tiles' loads are in flight too: one round trip for both)
     }
 
     // Staging: group grp stages keys 32 grp .. 32 grp + 31 of a tile, global -> registers (a buffer resource
@@ -480,6 +478,9 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
     }
     if (grp == 1 && 3 < nt)
         load_half(3, st);
+    #pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+        settle(qreg[kk]);
     __syncthreads();
     if (nt_w > 0) {
         qk(s, 0);
