@@ -151,10 +151,10 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
         auto load_tile = [&](uint32_t j0) {
             #pragma unroll
             for (int i = 0; i < 8; ++i)
-                kreg[i] = buffer_load16(krs, ((j0 + 4 * i + kg) * kD + cc * 8) * sizeof(T));
+                kreg[i] = buffer_load16_nt(krs, ((j0 + 4 * i + kg) * kD + cc * 8) * sizeof(T));
             #pragma unroll
             for (int i = 0; i < 8; ++i)
-                vreg[i] = buffer_load16(vrs, ((j0 + 8 * kg + i) * kD + cc * 8) * sizeof(T));
+                vreg[i] = buffer_load16_nt(vrs, ((j0 + 8 * kg + i) * kD + cc * 8) * sizeof(T));
         };
         auto store_tile = [&]() {
             #pragma unroll
