@@ -381,9 +381,289 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 size_t pooled_bytes(uint32_t heads, uint32_t n) { return ((size_t)heads * n * kD * sizeof(float) + 255) / 256 * 256; }
 
+constexpr int kWaves8 = 8;
+
+// Lists shared by a kv head's query heads, in groups of 4: the ping-pong structure of attn_fwd.hip's flash_fwd
+// driven by the pass list. A workgroup is one 64-row query tile of 4 query heads: 8 waves, wave w holding head
+// w % 4's rows 32 (w / 4) .. + 31, so every gathered K / V tile serves all eight. Waves 0-3 and 4-7 alternate a
+// matrix phase (Q K^T of the next pass's tile, P V of the current one) and a vector phase (that tile's masks,
+// softmax and the staging of later tiles), one phase apart; tiles rotate through three LDS buffers. A tile's
+// validity (valid flags and the pass's end) is one byte load a lane and a ballot, issued a phase ahead.
+template <class T, class TO>
+__global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams p)
+{
+    using E = Elem<T>;
+    using V8 = typename E::vec8;
+    using H = Elem<_Float16>;
+    using H8 = f16x8;
+    constexpr int NBUF = 3;
+    constexpr int KS = kD + 8;
+    constexpr int VS = kKB;
+    constexpr int CPR = kD / 8;
+    constexpr int GRPI = 256 / CPR;  // K rows one group-wide staging instruction covers
+    constexpr int NKG = 32 / GRPI;   // K chunks a thread stages per half tile
+    constexpr int NKK = kD / 16, NDB = kD / 32;
+    __shared__ __attribute__((aligned(16))) T ks[NBUF][kKB * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[NBUF][kD * VS];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t grp = w >> 2;
+    const uint32_t g = lane >> 5, c32 = lane & 31;
+    const uint32_t qt = p.n_qt - 1 - blockIdx.y;  // dense tiles (all keys) and late cubes first
+    const uint32_t h = blockIdx.x * 4 + (w & 3);
+    const uint32_t kvh = h / p.group;  // the same for the workgroup's 4 heads
+    const uint32_t q0 = qt * kCube + 32 * (w >> 2);
+    const uint32_t row = q0 + c32;
+    const bool live = q0 < p.n_q;
+
+    // The pass list: a cube tile's selected cubes, then its dense rows; a later tile's all keys. A pass past the
+    // list is empty (its keys start at k_pad: loads fetch nothing and every key is masked).
+    const bool cube = qt < p.n_cubes;
+    const uint16_t* my_sel = p.sel + ((size_t)kvh * p.n_cubes + qt) * p.max_sel;
+    const uint32_t ns = cube ? min((uint32_t)p.nsel[(size_t)kvh * p.n_cubes + qt], p.max_sel) : 0u;
+    const uint32_t dense_lo = cube ? p.dense0 : 0u, dense_hi = cube ? p.dense1 : p.n_k;
+    const uint32_t n_dense = dense_hi > dense_lo ? (dense_hi - dense_lo + kKB - 1) / kKB : 0u;
+    const uint32_t nt = ns + n_dense;
+    auto pass_range = [&](uint32_t ps, uint32_t& j0, uint32_t& hi) {
+        if (ps < ns) {
+            j0 = (uint32_t)my_sel[ps] * kCube;
+            hi = j0 + kCube;
+        } else if (ps < nt) {
+            j0 = dense_lo + (ps - ns) * kKB;
+            hi = min(j0 + kKB, dense_hi);
+        } else {
+            j0 = p.k_pad;
+            hi = j0;
+        }
+    };
+
+    V8 qreg[NKK];
+    {
+        const auto qrs = buffer_rsrc(static_cast<const T*>(p.q) + (size_t)h * p.q_pad * kD, p.n_q * kD * sizeof(T));
+        const uint32_t off = (row * kD + 8 * g) * sizeof(T);
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 16 * kk * sizeof(T)));
+    }
+
+    // Staging (as in flash_fwd): group grp stages keys 32 grp .. 32 grp + 31 of a pass's tile, K row-major in slot
+    // order, V transposed to f16. The K / V resources span the kv head's k_pad rows (a cube may hold rows past n_k,
+    // which valid masks); loads past k_pad return zeros.
+    const T* kbase = static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * kD;
+    const T* vbase = static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * kD;
+    const uint32_t gt = tid & 255, hk = 32 * grp;
+    const uint32_t k_row = gt / CPR, k_col = gt % CPR;
+    const uint32_t v_cc = gt % CPR;
+    const uint32_t v_kp = ((gt / CPR) & ~3u) | (((gt / CPR) ^ (2 * (v_cc >> 3))) & 3u);  // key pair 0 .. 15
+    struct Half {
+        u32x4 k[NKG], v[2];
+    };
+    auto load_half = [&](uint32_t ps, Half& st) {
+        uint32_t j0, hi;
+        pass_range(ps, j0, hi);
+        j0 += hk;
+        const uint32_t left = j0 < p.k_pad ? (p.k_pad - j0) * kD * (uint32_t)sizeof(T) : 0u;
+        const auto krs = buffer_rsrc(kbase + (size_t)min(j0, p.k_pad) * kD, left);
+        const auto vrs = buffer_rsrc(vbase + (size_t)min(j0, p.k_pad) * kD, left);
+#pragma unroll
+        for (int i = 0; i < NKG; ++i)
+            st.k[i] = buffer_load16(krs, ((k_row + GRPI * i) * kD + k_col * 8) * sizeof(T));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            st.v[i] = buffer_load16(vrs, ((2 * v_kp + i) * kD + v_cc * 8) * sizeof(T));
+    };
+    auto store_half = [&](uint32_t buf, const Half& st) {
+#pragma unroll
+        for (int i = 0; i < NKG; ++i)
+            *reinterpret_cast<u32x4*>(&ks[buf][(hk + slot_of(k_row + GRPI * i)) * KS + k_col * 8]) = st.k[i];
+        const uint32_t key = hk + 2 * v_kp, kc = key / 8, off = key % 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t d = v_cc * 8 + e;
+            *reinterpret_cast<uint32_t*>(&vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off]) =
+                f16_pair<T>(st.v[0], st.v[1], e);
+        }
+    };
+    // A pass's validity flag for key j0 + lane (loaded a phase before its ballot).
+    const auto valid_rs = buffer_rsrc(p.valid, p.k_pad);
+    auto valid_flag = [&](uint32_t ps) {
+        uint32_t j0, hi;
+        pass_range(ps, j0, hi);
+        const uint32_t f = __builtin_amdgcn_raw_buffer_load_b8(valid_rs, (int)(j0 + lane), 0, 0);
+        return (j0 + lane < hi && f != 0) ? 1u : 0u;
+    };
+
+    const float c = p.scale_log2;
+    auto qk = [&](f32x16 (&s)[2], uint32_t buf) {
+        const T* kr = &ks[buf][c32 * KS + 8 * g];
+        s[0] = f32x16{};
+        s[1] = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            s[0] = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s[0]);
+            s[1] = E::mfma32(*reinterpret_cast<const V8*>(kr + 32 * KS + 16 * kk), qreg[kk], s[1]);
+        }
+    };
+
+    f32x16 oacc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+        oacc[db] = f32x16{};
+    float m = -INFINITY, l = 0.0f, thr = -INFINITY;
+    f32x16 s[2];
+    H8 pb[4];
+
+    // The vector work on pass ps's scores (register r of s[t] holds key j0 + 32 t + 16 (r / 8) + 8 g + r % 8):
+    // masks from the validity ballot and the causal bound, the rescale decision, exponentials and the row sum.
+    auto softmax = [&](uint32_t ps, uint64_t vmask) {
+        uint32_t j0, hi;
+        pass_range(ps, j0, hi);
+        const bool cut = p.causal && j0 + kKB - 1 > q0;
+        if (vmask != ~0ull || cut) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    const uint32_t kb = 32 * t + 16 * a + 8 * g;
+                    const uint32_t bits = (uint32_t)(vmask >> kb) & 0xffu;
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const bool seen = ((bits >> jj) & 1u) && (!p.causal || j0 + kb + jj <= row);
+                        s[t][8 * a + jj] = seen ? s[t][8 * a + jj] : -INFINITY;
+                    }
+                }
+        }
+        float lmx = s[0][0];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                lmx = fmaxf(lmx, s[t][r]);
+        if (__any(lmx > thr)) {
+            const float mx = fmaxf(lmx, swap_halves(lmx)) * c;
+            const bool up = mx > m + kRescale;
+            const float f = up ? exp2_fast(m - mx) : 1.0f;
+            m = up ? mx : m;
+            thr = up ? (m + kRescale) / c : thr;
+            l *= f;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[db][r] *= f;
+        }
+        const float mu = m == -INFINITY ? 0.0f : m;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                u32x4 pk;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
+                    const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
+                    l += e0 + e1;
+                    pk[jj] = H::pack2(e0, e1);
+                }
+                pb[2 * t + a] = __builtin_bit_cast(H8, pk);
+            }
+    };
+    auto pv = [&](uint32_t buf) {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const uint32_t d = 32 * db + c32;
+                const _Float16* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
+                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[cc], oacc[db]);
+            }
+    };
+
+    // Prologue: passes 0 .. 2 by both groups (loads in flight together with Q's), group 1's half of pass 3.
+    Half st;
+    {
+        Half st1, st2;
+        load_half(0, st);
+        load_half(1, st1);
+        load_half(2, st2);
+        store_half(0, st);
+        store_half(1, st1);
+        store_half(2, st2);
+    }
+    if (grp == 1)
+        load_half(3, st);
+    uint32_t vflag = valid_flag(0);
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+        settle(qreg[kk]);
+    __syncthreads();
+    if (nt > 0) {
+        qk(s, 0);
+        softmax(0, __ballot(vflag != 0));
+    }
+    if (grp == 1)
+        __syncthreads();  // group 1 runs one phase behind group 0
+
+    uint32_t b0 = 0, b1 = 1, b2 = 2;
+    for (uint32_t j = 0; j < nt; ++j) {
+        // matrix phase: scores of pass j + 1, P V of pass j; pass j + 1's validity flags in flight
+        vflag = valid_flag(j + 1);
+        __builtin_amdgcn_s_setprio(1);
+        if (j + 1 < nt)
+            qk(s, b1);
+        pv(b0);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        // vector phase: softmax of pass j + 1, and the staging as in flash_fwd
+        if (j + 1 < nt)
+            softmax(j + 1, __ballot(vflag != 0));
+        if (grp == 0) {
+            if (j >= 1 && j + 2 < nt)
+                store_half(b2, st);
+            if (j + 3 < nt)
+                load_half(j + 3, st);
+        } else {
+            if (j + 3 < nt)
+                store_half(b0, st);
+            if (j + 4 < nt)
+                load_half(j + 4, st);
+        }
+        __syncthreads();
+        const uint32_t t = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = t;
+    }
+    if (grp == 0)
+        __syncthreads();  // the barrier count of group 1's offset
+
+    // Normalise and store through the row map; the LSE by tile row.
+    const float lt = l + swap_halves(l);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (live && row < p.n_q) {
+        const int32_t dst = p.map[row];
+        if (dst >= 0) {
+            TO* orow = static_cast<TO*>(p.o) + (size_t)dst * p.width + (size_t)h * kD;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
+                               oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
+            if (p.lse && g == 0)
+                p.lse[(size_t)h * p.q_pad + row] = lt > 0.0f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
+        }
+    }
+}
+
 template <class T, class TO>
 void launch_sparse(const SparseParams& p, hipStream_t s)
 {
+    if (p.sel_heads == p.kv_heads && p.group % 4 == 0) {
+        hipLaunchKernelGGL((flash_sparse8<T, TO>), dim3(p.heads / 4, p.n_qt), dim3(kWaves8 * 64), 0, s, p);
+        return;
+    }
     const dim3 grid(p.heads / p.hs, p.n_qt);
     if (p.hs == 2)
         hipLaunchKernelGGL((flash_sparse<T, TO, 4>), grid, dim3(256), 0, s, p);

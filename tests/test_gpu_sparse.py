@@ -224,3 +224,47 @@ def test_window_random_s16384_sampled():
     G.assert_attn_close(got, want_o, "sampled output")
     G.assert_rows_l2(got, want_o, "sampled output", 128)
     G.assert_lse_close(np.array([lse[h, r] for h, r in hr]), want_l, "sampled lse")
+
+
+@pytest.mark.parametrize("heads,kv,causal,dt", [(8, 2, 0, O.BF16), (8, 2, 1, O.F16), (16, 2, 1, O.BF16),
+                                                 (8, 1, 0, O.F16)])
+def test_shared_lists_grouped(heads, kv, causal, dt):
+    """Lists shared by a kv head's query heads in groups of 4 (the 8-wave path): random lists in random order,
+    dense rows, a cube with invalid rows, rows past n_q, and a map that drops rows, against the oracle."""
+    cubes, dense, topk = 5, 40, 3
+    cnt = np.array([64, 64, 37, 64, 64], np.uint32)
+    n = cubes * 64 + dense
+    q_pad, k_pad = (n + 63) // 64 * 64, (n + 127) // 128 * 128
+    n_q = n - 10
+    valid = np.zeros(k_pad, np.uint8)
+    for c in range(cubes):
+        valid[c * 64:c * 64 + cnt[c]] = 1
+    valid[cubes * 64:n] = 1
+    map_ = np.full(q_pad, -1, np.int32)
+    keep = np.nonzero(valid[:n_q])[0]
+    map_[keep] = np.arange(len(keep), dtype=np.int32)
+    map_[keep[::7]] = -1  # dropped rows stay untouched
+    rng = np.random.default_rng(40 + heads + causal)
+    sel = np.zeros((kv, cubes, topk), np.uint16)
+    nsel = np.zeros((kv, cubes), np.uint16)
+    for h in range(kv):
+        for c in range(cubes):
+            pool = np.arange(c + 1) if causal else np.arange(cubes)
+            ch = rng.permutation(pool)[:topk]
+            sel[h, c, :len(ch)] = ch
+            nsel[h, c] = len(ch)
+    qb, kb, vb = (G.randn_bits(rng, (hh, pad, 128), dt) for hh, pad in ((heads, q_pad), (kv, k_pad), (kv, k_pad)))
+    args = dict(n_q=n_q, q_pad=q_pad, n_k=n, k_pad=k_pad, heads=heads, kv_heads=kv, n_cubes=cubes, max_sel=topk,
+                dense0=cubes * 64, dense1=n, causal=causal, sel_heads=kv)
+    print(f"shared lists heads {heads} kv {kv} causal {causal}", flush=True)
+    want_o, want_l = O.attn_sparse(qb, kb, vb, sel, nsel, valid, map_, dtype=dt, o_fill=np.full((q_pad, heads * 128),
+                                   SENTINEL), **args)
+    for out in (torch.float32, G.TORCH[dt]):
+        o, lse = run_sparse(G.to_dev(qb, dt), G.to_dev(kb, dt), G.to_dev(vb, dt), dev_u16(sel), dev_u16(nsel),
+                            dev(valid), dev(map_), out=out, **args)
+        written = np.zeros(q_pad, bool)
+        written[map_[map_ >= 0]] = True
+        G.assert_attn_close(o[written], want_o[written], "output")
+        assert np.all(o[~written] == SENTINEL), "rows outside the map were written"
+        rows = np.nonzero(map_ >= 0)[0]
+        G.assert_lse_close(lse[:, rows], want_l[:, rows], "lse")
