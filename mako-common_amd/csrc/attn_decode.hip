@@ -319,22 +319,7 @@ __global__ __launch_bounds__(kD) void decode_merge(const DecParams p, TO* __rest
 }
 
 // Resident waves: kWgPerCu workgroups of kWaves waves on every CU of the current device (0: no device).
-uint32_t resident_waves()
-{
-    static thread_local int dev_cached = -1;
-    static thread_local uint32_t waves = 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess)
-        return 0;
-    if (dev != dev_cached) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            return 0;
-        waves = (uint32_t)cus * kWgPerCu * kWaves;
-        dev_cached = dev;
-    }
-    return waves;
-}
+uint32_t resident_waves() { return device_cus() * kWgPerCu * kWaves; }
 
 // Waves a call launches: the resident ones, or fewer when split asks for at most `split` keys a wave.
 uint32_t waves_for(const mako_decode_args* a, uint32_t resident)

@@ -163,5 +163,7 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();
 // MAKO_OK, or MAKO_EHIP with the launch error recorded (hipGetLastError after a launch).
 int check_launch(const char* what);
+// Compute units of the current device (cached per device and thread); 0 when there is none.
+uint32_t device_cus();
 
 }  // namespace mako

@@ -38,6 +38,23 @@ int check_launch(const char* what)
     return ok();
 }
 
+uint32_t device_cus()
+{
+    static thread_local int dev_cached = -1;
+    static thread_local uint32_t cus_cached = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return 0;
+    if (dev != dev_cached) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return 0;
+        cus_cached = (uint32_t)cus;
+        dev_cached = dev;
+    }
+    return cus_cached;
+}
+
 }  // namespace mako
 
 extern "C" int mako_attn_abi_version(void) { return MAKO_ATTN_ABI_VERSION; }
