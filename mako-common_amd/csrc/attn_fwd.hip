@@ -26,7 +26,7 @@
 // flash_fwd (heads of 64 and 128) runs 8 waves in two groups that alternate matrix and vector phases; the
 // running maximum's exchange between the two halves of a wave happens only when some lane's maximum passes its
 // threshold. flash_fwd_wide (heads of 256) runs 4 waves with double-buffered tiles.
-#include "pingpong.hpp"
+#include "device.hpp"
 
 namespace mako {
 namespace {
@@ -46,10 +46,7 @@ struct FwdParams {
     uint32_t group;    // heads / kv_heads
     uint32_t hq;       // query heads a workgroup (4, 2 or 1; divides group)
     uint32_t rows_wg;  // query rows a workgroup (32 x waves / hq)
-    uint32_t n_qblk;   // blocks of rows_wg rows
-    uint32_t n_hg;     // head groups (heads / hq)
-    uint32_t n_items;  // n_hg x n_qblk: the persistent kernel's work items
-    uint32_t n_wg;     // its workgroups
+    uint32_t n_qblk;   // workgroups along the rows
 };
 
 // LDS slot of K row `row` of a tile: bits 2 and 3 swapped within each 32 rows.
@@ -268,98 +265,295 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide(const FwdParams p)
     }
 }
 
-// Heads of 64 and 128: the persistent ping-pong loop of pingpong.hpp. An item is one block of rows_wg query rows of
-// hq heads of one GQA group (wave w: head hq * a + w % hq, rows 32 (w / hq) ..); items sorted heaviest rows first
-// (causal work grows with the row; the head group is the fastest index, so with 8 kv heads the XCDs' L2s each
-// serve one kv head) and dealt to the workgroups in snake order.
-struct DenseSched {
-    static constexpr bool kValid = false;
-    FwdParams p;
-    PPDeal deal;
-    uint32_t wr, wh;  // this wave's row block (w / hq) and head within the group (w % hq)
+constexpr int kWaves8 = 8;  // waves a workgroup of the ping-pong kernel
 
-    __device__ uint32_t n_items() const { return deal.count(); }
-    __device__ float scale_log2() const { return p.scale_log2; }
-    // a = head group, b = query block, x = keys the block visits (its causal bound)
-    __device__ void item(uint32_t i, PPItem& it) const
-    {
-        uint32_t hg, rank;
-        deal.at(i, hg, rank);
-        const uint32_t qb = p.n_qblk - 1 - rank;
-        const uint32_t last = p.q_pos0 + min(qb * p.rows_wg + p.rows_wg, p.n_q) - 1;
-        const uint32_t n_keys = last >= p.block ? p.n_k : min(p.n_k, last + 1);
-        it = PPItem{hg, qb, max(1u, (n_keys + kPPKeys - 1) / kPPKeys), n_keys, hg * p.hq / p.group};
-    }
-    __device__ PPWave wave(const PPItem& it, uint32_t) const
-    {
-        const uint32_t q0 = it.b * p.rows_wg + wr * 32;
-        const uint32_t last = p.q_pos0 + min(q0 + 32, p.n_q) - 1;
-        const uint32_t w_keys = q0 >= p.n_q ? 0u : (last >= p.block ? p.n_k : min(p.n_k, last + 1));
-        return PPWave{it.a * p.hq + wh, it.kv, q0, (w_keys + kPPKeys - 1) / kPPKeys};
-    }
-    __device__ void keys(const PPItem& it, uint32_t t, uint32_t& j0, uint32_t& hi) const
-    {
-        j0 = t * kPPKeys;
-        hi = it.x;
-    }
-    __device__ uint32_t extent() const { return p.n_k; }
-    __device__ size_t kv_row0(const PPItem& it) const { return (size_t)it.kv * p.k_pad; }
-    __device__ size_t q_row0(const PPWave& wv) const { return (size_t)wv.h * p.q_pad; }
-    __device__ uint32_t q_rows() const { return p.n_q; }
-    __device__ uint32_t valid_flag(uint32_t, uint32_t) const { return 1u; }
-    __device__ bool plain(const PPItem&, const PPWave& wv, uint32_t t, uint64_t) const
-    {
-        const uint32_t j0 = t * kPPKeys, p0 = p.q_pos0 + wv.q0;
-        return j0 + kPPKeys <= p.n_k && (j0 + kPPKeys - 1 <= p0 || (p0 >= p.block && j0 >= p.block));
-    }
-    __device__ uint32_t pos_of(const PPWave&, uint32_t row) const { return p.q_pos0 + row; }
-    __device__ bool open_of(uint32_t pos) const { return pos >= p.block; }
-    __device__ bool seen(uint32_t j, uint32_t, uint32_t, uint32_t pos, bool open, uint64_t) const
-    {
-        return (j < p.n_k) & ((j <= pos) | (open & (j >= p.block)));
-    }
-    // Normalise and store: register r of output block db holds head dim 32 db + 8 (r / 4) + 4 g + r % 4.
-    template <class TO, int D, int NDB>
-    __device__ void finish(const PPItem&, const PPWave& wv, const f32x16 (&oacc)[NDB], float l, float m,
-                           uint32_t c32, uint32_t g) const
-    {
-        const float lt = l + swap_halves(l);
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        const uint32_t row = wv.q0 + c32;
-        if (row < p.n_q) {
-            TO* orow = static_cast<TO*>(p.o) + (size_t)row * p.width + (size_t)wv.h * D;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4)
-                    store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
-                               oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
-            if (p.lse && g == 0)
-                p.lse[(size_t)wv.h * p.n_q + row] = lt > 0.0f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
-        }
-    }
-};
-
+// Heads of 64 and 128. A workgroup is 8 waves, each owning 32 query rows; waves 0-3 and 4-7 form two groups with
+// one wave of each on every SIMD. A wave alternates a matrix phase (Q K^T of the next 64-key tile and P V of the
+// current one: MFMAs fed from LDS) and a vector phase (the softmax of the next tile's scores, and staging half of
+// a later K / V tile into LDS). The groups run one phase apart, separated by workgroup barriers, so on every SIMD
+// one wave issues matrix work while the other does vector work. Tiles rotate through three LDS buffers.
 template <class T, class TO, int D>
-__global__ __launch_bounds__(kPPWaves * 64) void flash_fwd(const FwdParams p)
+__global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
 {
-    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    pingpong<T, TO, D>(DenseSched{p, PPDeal{p.n_hg, p.n_qblk, p.n_wg, blockIdx.x}, w / p.hq, w % p.hq}, p.q, p.k,
-                       p.v);
+    using E = Elem<T>;
+    using V8 = typename E::vec8;
+    using H = Elem<_Float16>;
+    using H8 = f16x8;
+    constexpr int NBUF = 3;            // LDS tile buffers
+    constexpr int KS = D + 8;          // K row stride in LDS (elements)
+    constexpr int VS = kKB;            // V^T row stride (elements)
+    constexpr int CPR = D / 8;         // 16-byte chunks a row
+    constexpr int GRPI = 256 / CPR;    // K rows one group-wide staging instruction covers
+    constexpr int NKG = 32 / GRPI;     // K chunks a thread stages per half tile (2 or 1)
+    constexpr int NVP = 16 * CPR;      // (key pair, chunk) units of V in a half tile (threads staging V)
+    constexpr int NDB = D / 32;
+    constexpr int NKK = D / 16;
+    static_assert(D == 64 || D == 128, "ping-pong path: heads of 64 or 128");
+    static_assert(NKG * GRPI == 32 && NVP <= 256, "half-tile split");
+    __shared__ __attribute__((aligned(16))) T ks[NBUF][kKB * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[NBUF][D * VS];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform over the wave
+    const uint32_t grp = w >> 2;                                  // 0: waves 0-3, 1: waves 4-7
+    const uint32_t g = lane >> 5, c32 = lane & 31;
+    const uint32_t hg = blockIdx.x;
+    const uint32_t qb = p.n_qblk - 1 - blockIdx.y;  // the latest rows (the most keys) first
+    const uint32_t h = hg * p.hq + w % p.hq;
+    const uint32_t kvh = hg * p.hq / p.group;
+    const uint32_t wg_q0 = qb * p.rows_wg;
+    const uint32_t q0 = wg_q0 + (w / p.hq) * 32;  // this wave's first row
+
+    // Keys the workgroup visits (the causal bound), and this wave's own bound.
+    const uint32_t wg_last = p.q_pos0 + min(wg_q0 + p.rows_wg, p.n_q) - 1;
+    const uint32_t n_keys = wg_last >= p.block ? p.n_k : min(p.n_k, wg_last + 1);
+    const bool live = q0 < p.n_q;
+    const uint32_t w_last = p.q_pos0 + min(q0 + 32, p.n_q) - 1;
+    const uint32_t w_keys = !live ? 0u : (w_last >= p.block ? p.n_k : min(p.n_k, w_last + 1));
+    const uint32_t p0 = p.q_pos0 + q0;  // the wave's first position
+    const uint32_t pos = p0 + c32;      // this lane's row's position
+
+    // Q: the B operand, lane (c32, g) holds row q0 + c32, head dims 16 kk + 8 g .. + 7 (rows past n_q load as 0).
+    V8 qreg[NKK];
+    {
+        const auto qrs = buffer_rsrc(static_cast<const T*>(p.q) + (size_t)h * p.q_pad * D, p.n_q * D * sizeof(T));
+        const uint32_t off = ((q0 + c32) * D + 8 * g) * sizeof(T);
+        #pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 16 * kk * sizeof(T)));
+        // (settled after the first tiles' loads are in flight too: one round trip for both)
+    }
+
+    // Staging: group grp stages keys 32 grp .. 32 grp + 31 of a tile, global -> registers (a buffer resource
+    // that starts at the tile, so rows past n_k load as zeros) -> LDS: K row-major in slot order, V transposed to
+    // f16. A V thread holds two consecutive keys of one 8-wide head-dimension chunk; the pair's place within its
+    // 16-byte chunk is XOR-ed with twice bit 3 of the chunk index so that the 32 lanes of a write cover 32
+    // distinct banks.
+    const T* kbase = static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * D;
+    const T* vbase = static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * D;
+    const uint32_t gt = tid & 255, hk = 32 * grp;
+    const uint32_t k_row = gt / CPR, k_col = gt % CPR;
+    const bool v_on = gt < (uint32_t)NVP;
+    const uint32_t v_cc = gt % CPR;
+    const uint32_t v_kp = ((gt / CPR) & ~3u) | (((gt / CPR) ^ (2 * (v_cc >> 3))) & 3u);  // key pair 0 .. 15
+    struct Half {
+        u32x4 k[NKG], v[2];
+    };
+    auto load_half = [&](uint32_t tile, Half& st) {
+        const uint32_t j0 = tile * kKB + hk;
+        const uint32_t left = j0 < p.n_k ? (p.n_k - j0) * D * (uint32_t)sizeof(T) : 0u;
+        const auto krs = buffer_rsrc(kbase + (size_t)j0 * D, left);
+        #pragma unroll
+        for (int i = 0; i < NKG; ++i)
+            st.k[i] = buffer_load16(krs, ((k_row + GRPI * i) * D + k_col * 8) * sizeof(T));
+        if (v_on) {
+            const auto vrs = buffer_rsrc(vbase + (size_t)j0 * D, left);
+            #pragma unroll
+            for (int i = 0; i < 2; ++i)
+                st.v[i] = buffer_load16(vrs, ((2 * v_kp + i) * D + v_cc * 8) * sizeof(T));
+        }
+    };
+    auto store_half = [&](uint32_t buf, const Half& st) {
+        #pragma unroll
+        for (int i = 0; i < NKG; ++i)
+            *reinterpret_cast<u32x4*>(&ks[buf][(hk + slot_of(k_row + GRPI * i)) * KS + k_col * 8]) = st.k[i];
+        if (v_on) {
+            const uint32_t key = hk + 2 * v_kp, kc = key / 8, off = key % 8;
+            #pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t d = v_cc * 8 + e;
+                *reinterpret_cast<uint32_t*>(&vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off]) =
+                    f16_pair<T>(st.v[0], st.v[1], e);
+            }
+        }
+    };
+
+    const float c = p.scale_log2;
+    // Tile tt's keys all visible to all of this wave's rows.
+    auto plain = [&](uint32_t tt) {
+        const uint32_t j0 = tt * kKB;
+        return j0 + kKB <= p.n_k && (j0 + kKB - 1 <= p0 || (p0 >= p.block && j0 >= p.block));
+    };
+    // Scores of a tile: s[t] register r holds key 64 tt + 32 t + 16 (r / 8) + 8 g + r % 8 of this lane's row.
+    auto qk = [&](f32x16 (&s)[2], uint32_t buf) {
+        const T* kr = &ks[buf][c32 * KS + 8 * g];
+        s[0] = f32x16{};
+        s[1] = f32x16{};
+        #pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            s[0] = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s[0]);
+            s[1] = E::mfma32(*reinterpret_cast<const V8*>(kr + 32 * KS + 16 * kk), qreg[kk], s[1]);
+        }
+    };
+
+    f32x16 oacc[NDB];
+    #pragma unroll
+    for (int db = 0; db < NDB; ++db)
+        oacc[db] = f32x16{};
+    // Running maximum m (base 2) and sum l of the row; the running maximum moves when a tile's maximum passes
+    // m + kRescale, i.e. when a raw score passes thr = (m + kRescale) / c (c > 0).
+    float m = -INFINITY, l = 0.0f, thr = -INFINITY;
+    f32x16 s[2];  // scores of the next tile
+    H8 pb[4];     // P of the current tile in f16: pb[cc] holds keys 16 cc + 8 g + 0 .. 7 of this lane's row
+
+    // The vector work on a tile's scores: mask, the rescale decision (the row's maximum is formed only when some
+    // lane passes its threshold), exponentials and the row sum.
+    auto softmax = [&](uint32_t tt) {
+        if (!plain(tt)) {
+            const bool open = pos >= p.block;
+            #pragma unroll
+            for (int t = 0; t < 2; ++t)
+                #pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t j = tt * kKB + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
+                    const bool seen = (j < p.n_k) & ((j <= pos) | (open & (j >= p.block)));
+                    s[t][r] = seen ? s[t][r] : -INFINITY;
+                }
+        }
+        float lmx = s[0][0];
+        #pragma unroll
+        for (int t = 0; t < 2; ++t)
+            #pragma unroll
+            for (int r = 0; r < 16; ++r)
+                lmx = fmaxf(lmx, s[t][r]);
+        if (__any(lmx > thr)) {
+            const float mx = fmaxf(lmx, swap_halves(lmx)) * c;
+            const bool up = mx > m + kRescale;
+            const float f = up ? exp2_fast(m - mx) : 1.0f;  // 0 while nothing was seen
+            m = up ? mx : m;
+            thr = up ? (m + kRescale) / c : thr;
+            l *= f;
+            #pragma unroll
+            for (int db = 0; db < NDB; ++db)
+                #pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[db][r] *= f;
+        }
+        const float mu = m == -INFINITY ? 0.0f : m;
+        #pragma unroll
+        for (int t = 0; t < 2; ++t)
+            #pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                u32x4 pk;
+                #pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
+                    const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
+                    l += e0 + e1;
+                    pk[jj] = H::pack2(e0, e1);
+                }
+                pb[2 * t + a] = __builtin_bit_cast(H8, pk);
+            }
+    };
+    // O^T += V^T P^T for the current tile (V^T in buffer buf).
+    auto pv = [&](uint32_t buf) {
+        #pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+            #pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const uint32_t d = 32 * db + c32;
+                const _Float16* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
+                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[cc], oacc[db]);
+            }
+    };
+
+    const uint32_t nt = (n_keys + kKB - 1) / kKB;
+    const uint32_t nt_w = (w_keys + kKB - 1) / kKB;
+    // Tiles 0 .. 2 by both groups (their loads in flight together); group 1's half of tile 3 into registers.
+    Half st;
+    {
+        Half st1, st2;
+        if (0 < nt)
+            load_half(0, st);
+        if (1 < nt)
+            load_half(1, st1);
+        if (2 < nt)
+            load_half(2, st2);
+        if (0 < nt)
+            store_half(0, st);
+        if (1 < nt)
+            store_half(1, st1);
+        if (2 < nt)
+            store_half(2, st2);
+    }
+    if (grp == 1 && 3 < nt)
+        load_half(3, st);
+    #pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+        settle(qreg[kk]);
+    __syncthreads();
+    if (nt_w > 0) {
+        qk(s, 0);
+        softmax(0);
+    }
+    if (grp == 1)
+        __syncthreads();  // group 1 runs one phase behind group 0
+
+    uint32_t b0 = 0, b1 = 1, b2 = 2;  // buffers of tiles j, j + 1, j + 2
+    for (uint32_t j = 0; j < nt; ++j) {
+        // matrix phase: scores of tile j + 1, P V of tile j
+        if (j < nt_w) {
+            __builtin_amdgcn_s_setprio(1);
+            if (j + 1 < nt_w)
+                qk(s, b1);
+            pv(b0);
+            __builtin_amdgcn_s_setprio(0);
+        }
+        __syncthreads();
+        // vector phase: softmax of tile j + 1; group 0 stores its half of tile j + 2 and loads tile j + 3,
+        // group 1 stores its half of tile j + 3 and loads tile j + 4
+        if (j + 1 < nt_w)
+            softmax(j + 1);
+        if (grp == 0) {
+            if (j >= 1 && j + 2 < nt)
+                store_half(b2, st);
+            if (j + 3 < nt)
+                load_half(j + 3, st);
+        } else {
+            if (j + 3 < nt)
+                store_half(b0, st);
+            if (j + 4 < nt)
+                load_half(j + 4, st);
+        }
+        __syncthreads();
+        const uint32_t t = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = t;
+    }
+    if (grp == 0)
+        __syncthreads();  // the barrier count of group 1's offset
+
+    // The row's sum over both halves of the wave; normalise and store. Register r of output block db holds head
+    // dim 32 db + 8 (r / 4) + 4 g + r % 4.
+    const float lt = l + swap_halves(l);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const uint32_t row = q0 + c32;
+    if (live && row < p.n_q) {
+        TO* orow = static_cast<TO*>(p.o) + (size_t)row * p.width + (size_t)h * D;
+        #pragma unroll
+        for (int db = 0; db < NDB; ++db)
+            #pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
+                           oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
+        if (p.lse && g == 0)
+            p.lse[(size_t)h * p.n_q + row] = lt > 0.0f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
+    }
 }
 
 // Query rows a workgroup covers for heads of `dim` with hq heads a workgroup.
-uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uint32_t)kPPWaves) * 32u / hq; }
+uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uint32_t)kWaves8) * 32u / hq; }
 
 template <class T, class TO>
 void launch_d(uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
 {
     switch (dim) {
     case 64:
-        hipLaunchKernelGGL((flash_fwd<T, TO, 64>), grid, dim3(kPPWaves * 64), 0, s, p);
+        hipLaunchKernelGGL((flash_fwd<T, TO, 64>), grid, dim3(kWaves8 * 64), 0, s, p);
         break;
     case 128:
-        hipLaunchKernelGGL((flash_fwd<T, TO, 128>), grid, dim3(kPPWaves * 64), 0, s, p);
+        hipLaunchKernelGGL((flash_fwd<T, TO, 128>), grid, dim3(kWaves8 * 64), 0, s, p);
         break;
     default:
         hipLaunchKernelGGL((flash_fwd_wide<T, TO, 256>), grid, dim3(kThreads), 0, s, p);
@@ -405,24 +599,11 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
     const uint32_t group = a->heads / a->kv_heads;
     const uint32_t hq = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
     FwdParams p{q, k, v, o, lse, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads, a->kv_heads, a->q_pos0, a->block,
-                a->width, a->scale * kLog2e, group, hq, rows_per_wg(dim, hq), 0, 0, 0, 0};
+                a->width, a->scale * kLog2e, group, hq, rows_per_wg(dim, hq), 0};
     p.n_qblk = (a->n_q + p.rows_wg - 1) / p.rows_wg;
-    p.n_hg = a->heads / hq;
-    dim3 grid(p.n_hg, p.n_qblk);
-    if (dim == 256) {
-        if (p.n_qblk > 65535)
-            return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
-    } else {
-        // persistent: one workgroup a CU, each walking its share of the (head group, row block) items
-        const uint32_t cus = device_cus();
-        if (!cus)
-            return fail(MAKO_EHIP, "attention: no device to size the grid for");
-        if ((uint64_t)p.n_hg * p.n_qblk > 0xffffffffu)
-            return fail(MAKO_EINVAL, "attention: %u queries x %u head groups exceed the work list", a->n_q, p.n_hg);
-        p.n_items = p.n_hg * p.n_qblk;
-        p.n_wg = min(cus, p.n_items);
-        grid = dim3(p.n_wg);
-    }
+    if (p.n_qblk > 65535)
+        return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
+    const dim3 grid(a->heads / hq, p.n_qblk);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (in == MAKO_BF16) {
         if (out == MAKO_F32)

@@ -81,13 +81,13 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_sparse(const SparseParams p)
     uint32_t ns = 0;
     const uint16_t* my_sel = p.sel + ((size_t)sh * p.n_cubes + qt) * p.max_sel;
     if (cube)
-        ns = min((uint32_t)p.nsel[(size_t)sh * p.n_cubes + qt], p.max_sel);
+        ns = min(uniform_u16(p.nsel, (size_t)sh * p.n_cubes + qt), p.max_sel);
     const uint32_t dense_lo = cube ? p.dense0 : 0u, dense_hi = cube ? p.dense1 : p.n_k;
     const uint32_t n_dense = dense_hi > dense_lo ? (dense_hi - dense_lo + kKB - 1) / kKB : 0u;
     const uint32_t n_pass = ns + n_dense;
     auto pass_range = [&](uint32_t ps, uint32_t& j0, uint32_t& hi) {
         if (ps < ns) {
-            j0 = (uint32_t)my_sel[ps] * kCube;
+            j0 = uniform_u16(my_sel, ps) * kCube;
             hi = j0 + kCube;
         } else {
             j0 = dense_lo + (ps - ns) * kKB;
@@ -421,13 +421,13 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
     // list is empty (its keys start at k_pad: loads fetch nothing and every key is masked).
     const bool cube = qt < p.n_cubes;
     const uint16_t* my_sel = p.sel + ((size_t)kvh * p.n_cubes + qt) * p.max_sel;
-    const uint32_t ns = cube ? min((uint32_t)p.nsel[(size_t)kvh * p.n_cubes + qt], p.max_sel) : 0u;
+    const uint32_t ns = cube ? min(uniform_u16(p.nsel, (size_t)kvh * p.n_cubes + qt), p.max_sel) : 0u;
     const uint32_t dense_lo = cube ? p.dense0 : 0u, dense_hi = cube ? p.dense1 : p.n_k;
     const uint32_t n_dense = dense_hi > dense_lo ? (dense_hi - dense_lo + kKB - 1) / kKB : 0u;
     const uint32_t nt = ns + n_dense;
     auto pass_range = [&](uint32_t ps, uint32_t& j0, uint32_t& hi) {
         if (ps < ns) {
-            j0 = (uint32_t)my_sel[ps] * kCube;
+            j0 = uniform_u16(my_sel, ps) * kCube;
             hi = j0 + kCube;
         } else if (ps < nt) {
             j0 = dense_lo + (ps - ns) * kKB;

@@ -129,6 +129,17 @@ __device__ __forceinline__ u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 2));
 }
 
+// A 16-bit entry of a read-only device array at a wave-uniform index, read through the scalar cache (a dword
+// load of the aligned dword holding it: that dword lies in the same page as the entry, so it is always mapped).
+// Unlike a vector load, it does not wait behind the wave's outstanding vector-memory loads.
+__device__ __forceinline__ uint32_t uniform_u16(const uint16_t* base, size_t i)
+{
+    typedef const __attribute__((address_space(4))) uint32_t const_u32;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(base + i);
+    const uint32_t w = *reinterpret_cast<const_u32*>(a & ~(uintptr_t)3);
+    return (a & 2) ? w >> 16 : w & 0xffffu;
+}
+
 // 2^x by v_exp_f32 alone (no denormal-range fix-up: results below 2^-126 flush to zero, which the softmax
 // sums cannot tell apart).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
