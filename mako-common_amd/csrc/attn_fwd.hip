@@ -339,9 +339,11 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
     struct Half {
         u32x4 k[NKG], v[2];
     };
-    auto load_half = [&](uint32_t tile, Half& st) {
-        const uint32_t j0 = tile * kKB + hk;
-        const uint32_t left = j0 < p.n_k ? (p.n_k - j0) * D * (uint32_t)sizeof(T) : 0u;
+    // (Keys at or past n_keys are masked for every row of the workgroup, so they load as zeros; a tile past the
+    // last fetches nothing.)
+    auto load_half = [&](uint32_t tile, Half& st) __attribute__((always_inline)) {
+        const uint32_t j0 = min(tile * kKB + hk, n_keys);
+        const uint32_t left = (n_keys - j0) * D * (uint32_t)sizeof(T);
         const auto krs = buffer_rsrc(kbase + (size_t)j0 * D, left);
         #pragma unroll
         for (int i = 0; i < NKG; ++i)
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
                 st.v[i] = buffer_load16(vrs, ((2 * v_kp + i) * D + v_cc * 8) * sizeof(T));
         }
     };
-    auto store_half = [&](uint32_t buf, const Half& st) {
+    auto store_half = [&](uint32_t buf, const Half& st) __attribute__((always_inline)) {
         #pragma unroll
         for (int i = 0; i < NKG; ++i)
             *reinterpret_cast<u32x4*>(&ks[buf][(hk + slot_of(k_row + GRPI * i)) * KS + k_col * 8]) = st.k[i];
@@ -370,12 +372,12 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
 
     const float c = p.scale_log2;
     // Tile tt's keys all visible to all of this wave's rows.
-    auto plain = [&](uint32_t tt) {
+    auto plain = [&](uint32_t tt) __attribute__((always_inline)) {
         const uint32_t j0 = tt * kKB;
         return j0 + kKB <= p.n_k && (j0 + kKB - 1 <= p0 || (p0 >= p.block && j0 >= p.block));
     };
     // Scores of a tile: s[t] register r holds key 64 tt + 32 t + 16 (r / 8) + 8 g + r % 8 of this lane's row.
-    auto qk = [&](f32x16 (&s)[2], uint32_t buf) {
+    auto qk = [&](f32x16 (&s)[2], uint32_t buf) __attribute__((always_inline)) {
         const T* kr = &ks[buf][c32 * KS + 8 * g];
         s[0] = f32x16{};
         s[1] = f32x16{};
@@ -394,11 +396,17 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
     // m + kRescale, i.e. when a raw score passes thr = (m + kRescale) / c (c > 0).
     float m = -INFINITY, l = 0.0f, thr = -INFINITY;
     f32x16 s[2];  // scores of the next tile
-    H8 pb[4];     // P of the current tile in f16: pb[cc] holds keys 16 cc + 8 g + 0 .. 7 of this lane's row
+    // P of the current tile, f16 pairs: pw[4 cc .. 4 cc + 3] hold keys 16 cc + 8 g + 0 .. 7 of this lane's row (kept
+    // as dwords, not f16 vectors, so that the row sum reads them as whole registers)
+    uint32_t pw[16];
+    auto pb = [&](int cc) __attribute__((always_inline)) {
+        return __builtin_bit_cast(H8, u32x4{pw[4 * cc], pw[4 * cc + 1], pw[4 * cc + 2], pw[4 * cc + 3]});
+    };
 
     // The vector work on a tile's scores: mask, the rescale decision (the row's maximum is formed only when some
-    // lane passes its threshold), exponentials and the row sum.
-    auto softmax = [&](uint32_t tt) {
+    // lane passes its threshold), exponentials, and the row sum of the f16 values the P V product multiplies.
+    // Maxima and sums run as four independent chains.
+    auto softmax = [&](uint32_t tt) __attribute__((always_inline)) {
         if (!plain(tt)) {
             const bool open = pos >= p.block;
             #pragma unroll
@@ -410,12 +418,16 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
                     s[t][r] = seen ? s[t][r] : -INFINITY;
                 }
         }
-        float lmx = s[0][0];
+        float mx4[4];
         #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int q = 0; q < 4; ++q)
+            mx4[q] = fmaxf(s[q >> 1][8 * (q & 1)], s[q >> 1][8 * (q & 1) + 1]);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
             #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                lmx = fmaxf(lmx, s[t][r]);
+            for (int r = 2; r < 8; ++r)
+                mx4[q] = fmaxf(mx4[q], s[q >> 1][8 * (q & 1) + r]);
+        const float lmx = fmaxf(fmaxf(mx4[0], mx4[1]), fmaxf(mx4[2], mx4[3]));
         if (__any(lmx > thr)) {
             const float mx = fmaxf(lmx, swap_halves(lmx)) * c;
             const bool up = mx > m + kRescale;
@@ -431,29 +443,24 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
         }
         const float mu = m == -INFINITY ? 0.0f : m;
         #pragma unroll
-        for (int t = 0; t < 2; ++t)
-            #pragma unroll
-            for (int a = 0; a < 2; ++a) {
-                u32x4 pk;
-                #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
-                    const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
-                    l += e0 + e1;
-                    pk[jj] = H::pack2(e0, e1);
-                }
-                pb[2 * t + a] = __builtin_bit_cast(H8, pk);
-            }
+        for (int q = 0; q < 16; ++q)
+            pw[q] = H::pack2(exp2_fast(fmaf(s[q >> 3][2 * (q & 7)], c, -mu)),
+                             exp2_fast(fmaf(s[q >> 3][2 * (q & 7) + 1], c, -mu)));
+        float l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        #pragma unroll
+        for (int q = 0; q < 16; ++q)
+            l4[q & 3] = sum_f16x2(pw[q], l4[q & 3]);
+        l += (l4[0] + l4[1]) + (l4[2] + l4[3]);
     };
     // O^T += V^T P^T for the current tile (V^T in buffer buf).
-    auto pv = [&](uint32_t buf) {
+    auto pv = [&](uint32_t buf) __attribute__((always_inline)) {
         #pragma unroll
         for (int cc = 0; cc < 4; ++cc)
             #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const uint32_t d = 32 * db + c32;
                 const _Float16* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
-                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[cc], oacc[db]);
+                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb(cc), oacc[db]);
             }
     };
 
@@ -463,20 +470,14 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
     Half st;
     {
         Half st1, st2;
-        if (0 < nt)
-            load_half(0, st);
-        if (1 < nt)
-            load_half(1, st1);
-        if (2 < nt)
-            load_half(2, st2);
-        if (0 < nt)
-            store_half(0, st);
-        if (1 < nt)
-            store_half(1, st1);
-        if (2 < nt)
-            store_half(2, st2);
+        load_half(0, st);
+        load_half(1, st1);
+        load_half(2, st2);
+        store_half(0, st);
+        store_half(1, st1);
+        store_half(2, st2);
     }
-    if (grp == 1 && 3 < nt)
+    if (grp == 1)
         load_half(3, st);
     #pragma unroll
     for (int kk = 0; kk < NKK; ++kk)
@@ -489,37 +490,54 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
     if (grp == 1)
         __syncthreads();  // group 1 runs one phase behind group 0
 
+    // Vector phase j's staging: group 0 stores its half of tile j + 2 (j >= 1; tile 2 came with the prologue) and
+    // loads tile j + 3, group 1 stores its half of tile j + 3 and loads tile j + 4. Loads past the last tile fetch
+    // nothing; one code path for both groups.
     uint32_t b0 = 0, b1 = 1, b2 = 2;  // buffers of tiles j, j + 1, j + 2
-    for (uint32_t j = 0; j < nt; ++j) {
-        // matrix phase: scores of tile j + 1, P V of tile j
-        if (j < nt_w) {
-            __builtin_amdgcn_s_setprio(1);
-            if (j + 1 < nt_w)
-                qk(s, b1);
-            pv(b0);
-            __builtin_amdgcn_s_setprio(0);
-        }
-        __syncthreads();
-        // vector phase: softmax of tile j + 1; group 0 stores its half of tile j + 2 and loads tile j + 3,
-        // group 1 stores its half of tile j + 3 and loads tile j + 4
-        if (j + 1 < nt_w)
-            softmax(j + 1);
-        if (grp == 0) {
-            if (j >= 1 && j + 2 < nt)
-                store_half(b2, st);
-            if (j + 3 < nt)
-                load_half(j + 3, st);
-        } else {
-            if (j + 3 < nt)
-                store_half(b0, st);
-            if (j + 4 < nt)
-                load_half(j + 4, st);
-        }
-        __syncthreads();
+    auto stage = [&](uint32_t j) __attribute__((always_inline)) {
+        const bool put = grp ? j + 3 < nt : j >= 1 && j + 2 < nt;
+        if (put)
+            store_half(grp ? b0 : b2, st);
+        load_half(j + 3 + grp, st);
+    };
+    auto rotate = [&]() __attribute__((always_inline)) {
         const uint32_t t = b0;
         b0 = b1;
         b1 = b2;
         b2 = t;
+    };
+    // Three loops with one barrier pattern (two a tile), so that the matrix work of the steady state has no branch
+    // around it: tiles this wave computes that have a next one, this wave's last tile, then tiles only the
+    // workgroup's other waves compute.
+    uint32_t j = 0;
+    for (; j + 1 < nt_w; ++j) {
+        // matrix phase: scores of tile j + 1, P V of tile j
+        __builtin_amdgcn_s_setprio(1);
+        qk(s, b1);
+        pv(b0);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        // vector phase: softmax of tile j + 1 and the staging
+        softmax(j + 1);
+        stage(j);
+        __syncthreads();
+        rotate();
+    }
+    if (j < nt_w) {
+        __builtin_amdgcn_s_setprio(1);
+        pv(b0);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        stage(j);
+        __syncthreads();
+        rotate();
+        ++j;
+    }
+    for (; j < nt; ++j) {
+        __syncthreads();
+        stage(j);
+        __syncthreads();
+        rotate();
     }
     if (grp == 0)
         __syncthreads();  // the barrier count of group 1's offset

@@ -144,6 +144,14 @@ __device__ __forceinline__ uint32_t uniform_u16(const uint16_t* base, size_t i)
 // sums cannot tell apart).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// acc + lo(x) + hi(x) for the two f16 halves of x, summed in f32 (v_dot2_f32_f16 against (1, 1)). Pass a whole
+// register: when the operand was a dword extracted from a wider f16 vector, this compiler selected the vector's
+// first dword instead (the half pair's offset lost).
+__device__ __forceinline__ float sum_f16x2(uint32_t x, float acc)
+{
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), f16x2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+
 // Marks a loaded value as arrived: the compiler waits for its load here, once, instead of treating it as still
 // in flight inside a later loop (where the in-order vmcnt wait would also wait for that loop's prefetches).
 template <class V>
