@@ -459,7 +459,7 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
     struct Half {
         u32x4 k[NKG], v[2];
     };
-    auto load_half = [&](uint32_t ps, Half& st) {
+    auto load_half = [&](uint32_t ps, Half& st) __attribute__((always_inline)) {
         uint32_t j0, hi;
         pass_range(ps, j0, hi);
         j0 += hk;
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
         for (int i = 0; i < 2; ++i)
             st.v[i] = buffer_load16(vrs, ((2 * v_kp + i) * kD + v_cc * 8) * sizeof(T));
     };
-    auto store_half = [&](uint32_t buf, const Half& st) {
+    auto store_half = [&](uint32_t buf, const Half& st) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NKG; ++i)
             *reinterpret_cast<u32x4*>(&ks[buf][(hk + slot_of(k_row + GRPI * i)) * KS + k_col * 8]) = st.k[i];
@@ -512,11 +512,15 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
         oacc[db] = f32x16{};
     float m = -INFINITY, l = 0.0f, thr = -INFINITY;
     f32x16 s[2];
-    H8 pb[4];
+    // P of the current pass as f16 pairs (dwords, so that the row sum reads whole registers)
+    uint32_t pw[16];
+    auto pb = [&](int cc) __attribute__((always_inline)) {
+        return __builtin_bit_cast(H8, u32x4{pw[4 * cc], pw[4 * cc + 1], pw[4 * cc + 2], pw[4 * cc + 3]});
+    };
 
     // The vector work on pass ps's scores (register r of s[t] holds key j0 + 32 t + 16 (r / 8) + 8 g + r % 8):
     // masks from the validity ballot and the causal bound, the rescale decision, exponentials and the row sum.
-    auto softmax = [&](uint32_t ps, uint64_t vmask) {
+    auto softmax = [&](uint32_t ps, uint64_t vmask) __attribute__((always_inline)) {
         uint32_t j0, hi;
         pass_range(ps, j0, hi);
         const bool cut = p.causal && j0 + kKB - 1 > q0;
@@ -534,12 +538,16 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
                     }
                 }
         }
-        float lmx = s[0][0];
+        float mx4[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int q = 0; q < 4; ++q)
+            mx4[q] = fmaxf(s[q >> 1][8 * (q & 1)], s[q >> 1][8 * (q & 1) + 1]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                lmx = fmaxf(lmx, s[t][r]);
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int r = 2; r < 8; ++r)
+                mx4[q] = fmaxf(mx4[q], s[q >> 1][8 * (q & 1) + r]);
+        const float lmx = fmaxf(fmaxf(mx4[0], mx4[1]), fmaxf(mx4[2], mx4[3]));
         if (__any(lmx > thr)) {
             const float mx = fmaxf(lmx, swap_halves(lmx)) * c;
             const bool up = mx > m + kRescale;
@@ -555,19 +563,14 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
         }
         const float mu = m == -INFINITY ? 0.0f : m;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int q = 0; q < 16; ++q)
+            pw[q] = H::pack2(exp2_fast(fmaf(s[q >> 3][2 * (q & 7)], c, -mu)),
+                             exp2_fast(fmaf(s[q >> 3][2 * (q & 7) + 1], c, -mu)));
+        float l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // the row sum of the f16 values P V multiplies
 #pragma unroll
-            for (int a = 0; a < 2; ++a) {
-                u32x4 pk;
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const float e0 = exp2_fast(fmaf(s[t][8 * a + 2 * jj], c, -mu));
-                    const float e1 = exp2_fast(fmaf(s[t][8 * a + 2 * jj + 1], c, -mu));
-                    l += e0 + e1;
-                    pk[jj] = H::pack2(e0, e1);
-                }
-                pb[2 * t + a] = __builtin_bit_cast(H8, pk);
-            }
+        for (int q = 0; q < 16; ++q)
+            l4[q & 3] = sum_f16x2(pw[q], l4[q & 3]);
+        l += (l4[0] + l4[1]) + (l4[2] + l4[3]);
     };
     auto pv = [&](uint32_t buf) {
 #pragma unroll
@@ -576,7 +579,7 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
             for (int db = 0; db < NDB; ++db) {
                 const uint32_t d = 32 * db + c32;
                 const _Float16* vr = &vt[buf][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)];
-                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[cc], oacc[db]);
+                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb(cc), oacc[db]);
             }
     };
 
@@ -606,34 +609,42 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
         __syncthreads();  // group 1 runs one phase behind group 0
 
     uint32_t b0 = 0, b1 = 1, b2 = 2;
-    for (uint32_t j = 0; j < nt; ++j) {
-        // matrix phase: scores of pass j + 1, P V of pass j; pass j + 1's validity flags in flight
-        vflag = valid_flag(j + 1);
-        __builtin_amdgcn_s_setprio(1);
-        if (j + 1 < nt)
-            qk(s, b1);
-        pv(b0);
-        __builtin_amdgcn_s_setprio(0);
-        __syncthreads();
-        // vector phase: softmax of pass j + 1, and the staging as in flash_fwd
-        if (j + 1 < nt)
-            softmax(j + 1, __ballot(vflag != 0));
-        if (grp == 0) {
-            if (j >= 1 && j + 2 < nt)
-                store_half(b2, st);
-            if (j + 3 < nt)
-                load_half(j + 3, st);
-        } else {
-            if (j + 3 < nt)
-                store_half(b0, st);
-            if (j + 4 < nt)
-                load_half(j + 4, st);
-        }
-        __syncthreads();
+    // The staging as in flash_fwd (loads past the list fetch nothing), and the buffer rotation.
+    auto stage = [&](uint32_t j) __attribute__((always_inline)) {
+        const bool put = grp ? j + 3 < nt : j >= 1 && j + 2 < nt;
+        if (put)
+            store_half(grp ? b0 : b2, st);
+        load_half(j + 3 + grp, st);
+    };
+    auto rotate = [&]() __attribute__((always_inline)) {
         const uint32_t t = b0;
         b0 = b1;
         b1 = b2;
         b2 = t;
+    };
+    // Passes with a next one, then the last: no branch around the matrix work of the steady state.
+    uint32_t j = 0;
+    for (; j + 1 < nt; ++j) {
+        // matrix phase: scores of pass j + 1, P V of pass j; pass j + 1's validity flags in flight
+        vflag = valid_flag(j + 1);
+        __builtin_amdgcn_s_setprio(1);
+        qk(s, b1);
+        pv(b0);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        // vector phase: softmax of pass j + 1, and the staging
+        softmax(j + 1, __ballot(vflag != 0));
+        stage(j);
+        __syncthreads();
+        rotate();
+    }
+    if (j < nt) {
+        __builtin_amdgcn_s_setprio(1);
+        pv(b0);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        stage(j);
+        __syncthreads();
     }
     if (grp == 0)
         __syncthreads();  // the barrier count of group 1's offset
