@@ -5,8 +5,9 @@
 // to query row r (position pos = q_pos0 + r) when j < n_k && (j <= pos || (pos >= block && j >= block))
 // (ops.metal:289); head h reads kv head h / (heads / kv_heads) (:242); the running maximum moves only when a
 // score passes it by 8 in the base-2 domain (:303-316), so most key blocks leave the output unscaled; P is
-// rounded to f16 for the P V product and the row sum adds the unrounded exponentials (:328-330); a fully masked
-// row gives 0 (:355); rows >= n_q are not stored (:359-362). With bf16 inputs, V is converted to f16 as it is
+// rounded to f16 for the P V product (:329); a fully masked row gives 0 (:355); rows >= n_q are not stored
+// (:359-362). One difference: the reference's row sum adds the unrounded exponentials (:330), the ping-pong kernel's
+// adds the f16 values P V multiplies (v_dot2, half the instructions; the two differ by under 2^-12 relative). With bf16 inputs, V is converted to f16 as it is
 // staged, so P keeps f16's 11 significant bits (bf16's 8 would put ~2^-9 |v| of error on rows of few keys).
 //
 // The design is this one's own, for CDNA4. Shared by both kernels below:
