@@ -135,6 +135,42 @@ int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_dtype out, c
                      const void* v, const uint32_t* ctx_len, void* o, float* lse, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/*
+ * Head tiles from fp32 rows: head h of token t, x[t][col0 + h * stride .. + dim), written as y row
+ * [h][row0 + t][dim] in f16 (the reference's half tiles) or bf16, optionally RMS-normed (times w) and then rotated by
+ * the angle table cs. One call stands for each of the reference's tile producers (src/kernels/ops.metal:11-52,
+ * 371-408, 576-620):
+ *   TransformerRuntime::heads (src/models/runtime.cpp:215-226; heads_half + heads_clear): stride = dim = 128,
+ *     eps = 0, rope 0 / 1 / 2 over rot = dim, clear = 1;
+ *   TransformerRuntime::heads_norm (runtime.cpp:228-241; heads_norm_half): as heads with eps > 0 and w, any row0,
+ *     clear = 0 (the rows past T are left as they are);
+ *   TransformerRuntime::heads_partial (runtime.cpp:243-260; heads_partial): any stride, dim a multiple of 32 up to
+ *     256, rope 1 over the first rot values, eps 0 (no norm) or > 0 with w, row0 = 0, clear = 0, and map: y row t
+ *     takes x row map[t] (and its angles), a zero row where map[t] < 0.
+ * Rotation: a pair (u, v) becomes (u c - v s, v c + u s) with (c, s) = cs[t][p] (float pairs, rot / 2 a row):
+ * rope 1 pairs value i with i + rot / 2 (p = i), rope 2 pairs 2p with 2p + 1. The norm is
+ * x * w / sqrt(mean(x^2) + eps) over the head's dim values, before the rotation. cs, w and map may be NULL when
+ * unused. Refuses (MAKO_EINVAL) what the reference refuses (heads_partial: dim > 256, dim % 32, odd rot) and
+ * shapes it cannot address.
+ */
+typedef struct mako_heads_args {
+    uint32_t rows;   /* tokens T */
+    uint32_t ld;     /* x row stride in elements */
+    uint32_t col0;   /* the first head's column in x */
+    uint32_t stride; /* columns from one head to the next in x */
+    uint32_t dim;    /* values a head: a multiple of 32, at most 256 */
+    uint32_t heads;  /* heads produced */
+    uint32_t n_pad;  /* rows of a head in y (>= row0 + rows) */
+    uint32_t row0;   /* y row of token 0 */
+    uint32_t rope;   /* 0 none; 1 value i with i + rot / 2; 2 value 2i with 2i + 1 */
+    uint32_t rot;    /* leading values rotated (even, at most dim) */
+    float eps;       /* 0: no norm */
+    uint32_t clear;  /* 1: zero y rows [row0 + rows, n_pad) of every head */
+} mako_heads_args;
+
+int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const float* cs, const float* w,
+               const int32_t* map, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

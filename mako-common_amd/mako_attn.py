@@ -15,7 +15,7 @@ U32_MAX = 0xFFFFFFFF
 
 # Every symbol include/mako_attn.h declares.
 EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
-           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode")
+           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode", "mako_heads")
 
 
 class AttnArgs(ctypes.Structure):
@@ -32,6 +32,11 @@ class SparseArgs(ctypes.Structure):
 class DecodeArgs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("batch", "heads", "kv_heads", "dim", "cap", "max_ctx", "split")] + \
         [("scale", ctypes.c_float)]
+
+
+class HeadsArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("rows", "ld", "col0", "stride", "dim", "heads", "n_pad", "row0",
+                                               "rope", "rot")] + [("eps", ctypes.c_float), ("clear", ctypes.c_uint32)]
 
 
 class MakoError(RuntimeError):
@@ -61,7 +66,8 @@ def lib():
         L.mako_attn_decode_workspace.argtypes = [ctypes.POINTER(DecodeArgs)]
         L.mako_attn_decode_workspace.restype = SZ
         L.mako_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P, SZ, P]
-        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode"):
+        L.mako_heads.argtypes = [ctypes.POINTER(HeadsArgs), I, P, P, P, P, P, P]
+        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode", "mako_heads"):
             getattr(L, name).restype = I
         _lib = L
     return _lib
@@ -158,3 +164,12 @@ def window_random_blocks(n_blocks, lists, window=8, n_random=8, seed=0):
             sel[li, qb, :len(picks)] = picks
             nsel[li, qb] = len(picks)
     return sel, nsel
+
+
+def heads(x, y, *, rows, ld, col0, stride, dim, heads, n_pad, row0=0, rope=0, rot=0, eps=0.0, clear=0, cs=None,
+          w=None, map_=None, stream=None):
+    """mako_heads on torch tensors: x float32 rows, y [heads][n_pad][dim] f16 or bf16, cs float32 [*][rot / 2][2],
+    w float32 [dim], map_ int32 [rows]."""
+    a = HeadsArgs(rows, ld, col0, stride, dim, heads, n_pad, row0, rope, rot, eps, clear)
+    _check(lib().mako_heads(ctypes.byref(a), dtype_code(y), _ptr(x), _ptr(cs), _ptr(w), _ptr(map_), _ptr(y),
+                            _stream(stream)))

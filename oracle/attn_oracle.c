@@ -6,6 +6,7 @@
  * show that their checks catch it:
  *   1 mask off by one (j < pos)          2 GQA map h % kv_heads           3 lse without the maximum
  *   4 k and v swapped in the scores      5 cube_topk ties to the larger   6 sparse dense rows ignore valid
+ *   7 heads: the second value of a rotated pair takes v c - u s          8 heads: the norm divides by the sum
  */
 #include "attn_oracle.h"
 
@@ -574,4 +575,68 @@ void oracle_lse_merge(uint32_t n, uint32_t dim, const double* o_i, const double*
             o[d] += w * o_i[(size_t)i * dim + d];
     }
     *lse = mx + log(sum);
+}
+
+/* ---- head tiles ------------------------------------------------------------------------------------------- */
+
+static uint16_t round_to(int out_dtype, double v)
+{
+    return out_dtype == ORACLE_BF16 ? oracle_f32_to_bf16((float)v) : oracle_f32_to_f16((float)v);
+}
+
+int oracle_heads(const oracle_heads_args* a, int out_dtype, const float* x, const float* cs, const float* w,
+                 const int32_t* map, uint16_t* y)
+{
+    if (a->dim == 0 || a->dim > 256 || a->rot % 2 || a->rot > a->dim || a->row0 + a->rows > a->n_pad)
+        return 1;
+    double v[256], r[256];
+    const uint32_t half = a->rot / 2;
+    for (uint32_t h = 0; h < a->heads; ++h) {
+        for (uint32_t t = 0; t < a->rows; ++t) {
+            uint16_t* yr = y + ((size_t)h * a->n_pad + a->row0 + t) * a->dim;
+            const int32_t src = map ? map[t] : (int32_t)t;
+            if (src < 0) { /* heads_partial: a zero row (ops.metal:598-601) */
+                for (uint32_t i = 0; i < a->dim; ++i)
+                    yr[i] = 0;
+                continue;
+            }
+            const float* xr = x + (size_t)src * a->ld + a->col0 + (size_t)h * a->stride;
+            for (uint32_t i = 0; i < a->dim; ++i)
+                v[i] = xr[i];
+            if (a->eps > 0.0f) { /* ops.metal:389-396, 602-611 */
+                double ss = 0.0;
+                for (uint32_t i = 0; i < a->dim; ++i)
+                    ss += v[i] * v[i];
+#if ORACLE_MUTANT == 8
+                const double inv = 1.0 / sqrt(ss + a->eps);
+#else
+                const double inv = 1.0 / sqrt(ss / a->dim + a->eps);
+#endif
+                for (uint32_t i = 0; i < a->dim; ++i)
+                    v[i] *= inv * w[i];
+            }
+            for (uint32_t i = 0; i < a->dim; ++i)
+                r[i] = v[i];
+            if (a->rope) { /* ops.metal:33-38, 398-403, 614-617 */
+                for (uint32_t i = 0; i < a->rot; ++i) {
+                    const int first = a->rope == 1 ? i < half : (i % 2) == 0;
+                    const uint32_t j = a->rope == 1 ? (first ? i + half : i - half) : (i ^ 1u);
+                    const uint32_t p = a->rope == 1 ? (first ? i : i - half) : i / 2;
+                    const double c = cs[((size_t)src * half + p) * 2], s = cs[((size_t)src * half + p) * 2 + 1];
+#if ORACLE_MUTANT == 7
+                    r[i] = first ? v[i] * c - v[j] * s : v[i] * c - v[j] * s;
+#else
+                    r[i] = first ? v[i] * c - v[j] * s : v[i] * c + v[j] * s;
+#endif
+                }
+            }
+            for (uint32_t i = 0; i < a->dim; ++i)
+                yr[i] = round_to(out_dtype, r[i]);
+        }
+        if (a->clear) /* heads_clear (ops.metal:44-52) */
+            for (uint32_t t = a->row0 + a->rows; t < a->n_pad; ++t)
+                for (uint32_t i = 0; i < a->dim; ++i)
+                    y[((size_t)h * a->n_pad + t) * a->dim + i] = 0;
+    }
+    return 0;
 }

@@ -20,6 +20,10 @@
  *   oracle_attn_decode  - one query row per sequence at position ctx - 1 against keys [0, ctx): the dense rule
  *                         with n_q = 1, q_pos0 = ctx - 1 (ops.metal:289), batched.
  *   oracle_lse_merge    - the split-K merge: o = sum_i exp(lse_i - lse) o_i, lse = log sum_i exp(lse_i).
+ *   oracle_heads        - the tile producers heads_half, heads_clear, heads_norm_half and heads_partial
+ *                         (src/kernels/ops.metal:21-52, 376-407, 587-620): slice, RMS norm times w
+ *                         (x / sqrt(mean(x^2) + eps)), rotation of pairs (u, v) -> (u c - v s, v c + u s),
+ *                         row map (a zero row where map[t] < 0), padding rows zeroed.
  *
  * Inputs are raw element arrays of a stated type (f32, f16 or bf16 bits), widened exactly to double.
  */
@@ -111,6 +115,20 @@ int oracle_attn_decode_rows(uint32_t batch, uint32_t heads, uint32_t kv_heads, u
                             double* lse_rows, int nthreads);
 
 /* Merges n partial results of one row: o_i [n][dim] (each normalised), lse_i [n] -> o [dim], *lse. */
+/* HeadsArgs, HeadsNormArgs and HeadsPartialArgs (src/kernels/ops.metal:11-19, 371-374, 577-585) in one struct:
+ * rope 1 pairs value i with i + rot / 2, rope 2 pairs 2p with 2p + 1; cs holds rot / 2 (cos, sin) pairs a row;
+ * eps 0: no norm; clear: zero rows [row0 + rows, n_pad) of every head. */
+typedef struct oracle_heads_args {
+    uint32_t rows, ld, col0, stride, dim, heads, n_pad, row0, rope, rot;
+    float eps;
+    uint32_t clear;
+} oracle_heads_args;
+
+/* y [heads][n_pad][dim] as f16 or bf16 bits (out_dtype); y row row0 + t from x row t, or from x row map[t] (and
+ * its angles) when map is not NULL, a zero row where map[t] < 0. Rows it does not write are left as they are. */
+int oracle_heads(const oracle_heads_args* a, int out_dtype, const float* x, const float* cs, const float* w,
+                 const int32_t* map, uint16_t* y);
+
 void oracle_lse_merge(uint32_t n, uint32_t dim, const double* o_i, const double* lse_i, double* o, double* lse);
 
 #ifdef __cplusplus

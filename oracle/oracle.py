@@ -29,6 +29,13 @@ class SparseArgs(ctypes.Structure):
         [(n, ctypes.c_uint32) for n in ("n_cubes", "max_sel", "dense0", "dense1", "causal", "sel_heads")]
 
 
+class HeadsArgs(ctypes.Structure):
+    """HeadsArgs / HeadsNormArgs / HeadsPartialArgs (src/kernels/ops.metal:11-19, 371-374, 577-585) in one."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in ("rows", "ld", "col0", "stride", "dim", "heads", "n_pad", "row0",
+                                               "rope", "rot")] + [("eps", ctypes.c_float), ("clear", ctypes.c_uint32)]
+
+
 def build(name="liboracle.so", mutant=None):
     """Builds the oracle library (or a mutant with one planted mistake) and returns its path."""
     target = name if mutant is None else f"liboracle_mutant{mutant}.so"
@@ -54,6 +61,7 @@ def lib(mutant=None):
         L.oracle_cube_select.argtypes = [U32, U32, I, P, U32, P, U32, U32, P, U32, U32, U32, P, P, P, P, P]
         L.oracle_attn_decode.argtypes = [U32, U32, U32, U32, U32, F, I, P, P, P, P, P, P, I]
         L.oracle_attn_decode_rows.argtypes = [U32, U32, U32, U32, U32, F, I, P, P, P, P, P, SZ, P, P, I]
+        L.oracle_heads.argtypes = [ctypes.POINTER(HeadsArgs), I, P, P, P, P, P]
         L.oracle_lse_merge.argtypes = [U32, U32, P, P, P, P]
         L.oracle_lse_merge.restype = None
         L.oracle_f32_to_f16.argtypes = [F]
@@ -231,6 +239,24 @@ def lse_merge(o_i, lse_i, mutant=None):
     lse = np.zeros(1, np.float64)
     lib(mutant).oracle_lse_merge(n, dim, _p(o_i), _p(lse_i), _p(o), _p(lse))
     return o, float(lse[0])
+
+
+def heads(x, cs=None, w=None, map_=None, *, rows, ld, col0, stride, dim, heads, n_pad, row0=0, rope=0, rot=0,
+          eps=0.0, clear=0, out=F16, y=None, mutant=None):
+    """Head tiles: x float32 [*][ld] rows, cs float32 [*][rot / 2][2], w float32 [dim], map_ int32 [rows].
+    Returns y [heads][n_pad][dim] as uint16 bits of `out` (f16 or bf16); pass y to see which rows stay untouched."""
+    x = np.ascontiguousarray(x, np.float32)
+    cs = None if cs is None else np.ascontiguousarray(cs, np.float32)
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    map_ = None if map_ is None else np.ascontiguousarray(map_, np.int32)
+    if y is None:
+        y = np.zeros((heads, n_pad, dim), np.uint16)
+    assert y.dtype == np.uint16 and y.flags.c_contiguous and y.shape == (heads, n_pad, dim)
+    a = HeadsArgs(rows, ld, col0, stride, dim, heads, n_pad, row0, rope, rot, eps, clear)
+    rc = lib(mutant).oracle_heads(ctypes.byref(a), out, _p(x), _p(cs), _p(w), _p(map_), _p(y))
+    if rc:
+        raise ValueError("oracle_heads: bad arguments")
+    return y
 
 
 def to_f16_bits(x):

@@ -10,6 +10,11 @@ planted mistake), so the same checks both pass on the oracle and are shown to fa
   sparse         - all cubes selected equals dense over the valid keys; rows with map < 0 stay untouched
   cube_select    - the order numpy's stable argsort of (-score) gives; local cubes lead without duplicates
   decode, merge  - decode equals the dense rule at q_pos0 = ctx - 1; merging splits equals the whole row
+  heads          - the plain slice is numpy's f16 / bf16 rounding of x; padding rows zeroed, others untouched;
+                   angle 0 is the identity and angle pi / 2 maps (u, v) to (-v, u); a rotation is the complex
+                   product (u + i v)(c + i s); rope 2 pairs adjacent values; values past rot pass through; with w = 1
+                   the normed head has unit mean square and is invariant to scaling x; a mapped row is the
+                   unmapped row of its source, a negative map gives a zero row
 """
 import glob
 import os
@@ -281,5 +286,69 @@ def check_decode_and_merge(mutant=None):
     return not msgs, "; ".join(msgs)
 
 
+def check_heads(mutant=None):
+    msgs = []
+    rng = _rng(31)
+    T, H, D, ld = 6, 3, 128, 3 * 128 + 16
+    x = rng.standard_normal((T, ld)).astype(np.float32)
+    args = dict(rows=T, ld=ld, col0=8, stride=D, dim=D, heads=H, n_pad=9, mutant=mutant)
+    heads3 = x[:, 8:8 + H * D].reshape(T, H, D).transpose(1, 0, 2)
+    # the plain slice, rounded by numpy; padding zeroed with clear, left alone without
+    for out, conv in ((O.F16, O.to_f16_bits), (O.BF16, O.to_bf16_bits)):
+        y = O.heads(x, clear=1, out=out, y=np.full((H, 9, D), 0x7777, np.uint16), **args)
+        if not (np.array_equal(y[:, :T], conv(heads3)) and (y[:, T:] == 0).all()):
+            msgs.append(f"plain slice ({'f16' if out == O.F16 else 'bf16'}) is not numpy's rounding of x")
+    y = O.heads(x, row0=2, y=np.full((H, 9, D), 0x7777, np.uint16), **args)
+    if not ((y[:, :2] == 0x7777).all() and (y[:, 2 + T:] == 0x7777).all()):
+        msgs.append("rows outside [row0, row0 + rows) were written without clear")
+
+    def rot(rope, rr, ang, src=None):
+        cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+        return O.bits_to_f32(O.heads(x, cs, rope=rope, rot=rr, **args), O.F16).astype(np.float64)[:, :T], cs
+    ident, _ = rot(1, D, np.zeros((T, D // 2)))
+    if not np.array_equal(ident, O.bits_to_f32(O.to_f16_bits(heads3), O.F16)):
+        msgs.append("angle 0 is not the identity")
+    q90, _ = rot(1, D, np.full((T, D // 2), np.pi / 2))
+    if not (np.allclose(q90[..., :D // 2], -heads3[..., D // 2:], atol=2e-3, rtol=2e-3) and
+            np.allclose(q90[..., D // 2:], heads3[..., :D // 2], atol=2e-3, rtol=2e-3)):
+        msgs.append("angle pi / 2 does not map (u, v) to (-v, u)")
+    for rope, rr in ((1, D), (1, 96), (2, D), (2, 64)):
+        ang = rng.uniform(-np.pi, np.pi, (T, rr // 2))
+        got, cs = rot(rope, rr, ang)
+        c = cs[..., 0].astype(np.float64) + 1j * cs[..., 1].astype(np.float64)  # [T][rr / 2]
+        xs = heads3.astype(np.float64)
+        if rope == 1:
+            z = (xs[..., :rr // 2] + 1j * xs[..., rr // 2:rr]) * c[None]
+            want = np.concatenate([z.real, z.imag, xs[..., rr:]], -1)
+        else:
+            z = (xs[..., 0:rr:2] + 1j * xs[..., 1:rr:2]) * c[None]
+            want = xs.copy()
+            want[..., 0:rr:2], want[..., 1:rr:2] = z.real, z.imag
+        if not np.allclose(got, want, atol=1e-3, rtol=2 ** -10):
+            msgs.append(f"rope {rope} over {rr} is not the complex product (u + i v)(c + i s)")
+    # the norm: unit mean square with w = 1, invariant to scaling x, the weight multiplies value-wise
+    ones = np.ones(D, np.float32)
+    yn = O.bits_to_f32(O.heads(x, w=ones, eps=1e-6, **args), O.F16).astype(np.float64)[:, :T]
+    if not np.allclose((yn ** 2).mean(-1), 1.0, rtol=2e-3):
+        msgs.append("a normed head with w = 1 does not have unit mean square")
+    ys = O.bits_to_f32(O.heads(x * 8.0, w=ones, eps=1e-6, **args), O.F16).astype(np.float64)[:, :T]
+    if not np.allclose(ys, yn, atol=2e-3, rtol=2e-3):
+        msgs.append("the norm is not invariant to scaling x")
+    wv = rng.uniform(0.5, 2.0, D).astype(np.float32)
+    yw = O.bits_to_f32(O.heads(x, w=wv, eps=1e-6, **args), O.F16).astype(np.float64)[:, :T]
+    if not np.allclose(yw, yn * wv, atol=2e-3, rtol=2e-3):
+        msgs.append("the weight does not multiply the normed values")
+    # the row map: row t from x row map[t] with that row's angles; a negative entry gives a zero row
+    ang = rng.uniform(-np.pi, np.pi, (T, 48))
+    cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+    mp = np.array([3, -1, 0, 5, 5, 2], np.int32)
+    full = O.heads(x, cs, w=wv, eps=1e-5, rope=1, rot=96, **args)
+    mapped = O.heads(x, cs, wv, mp, eps=1e-5, rope=1, rot=96, **args)
+    if not all(np.array_equal(mapped[:, t], full[:, mp[t]]) if mp[t] >= 0 else (mapped[:, t] == 0).all()
+               for t in range(T)):
+        msgs.append("a mapped row is not its source row's result (or a negative map is not a zero row)")
+    return not msgs, "; ".join(msgs)
+
+
 ALL_CHECKS = [check_goldens, check_closed_forms, check_invariants, check_sparse, check_cube_select,
-              check_decode_and_merge]
+              check_decode_and_merge, check_heads]

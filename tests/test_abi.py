@@ -109,3 +109,33 @@ def decode_rc(**kw):
 def test_decode_refuses(kw, code, msg):
     rc, err = decode_rc(**kw)
     assert rc == code and msg in err, (rc, err)
+
+
+def heads_rc(**kw):
+    a = dict(rows=64, ld=4096, col0=0, stride=128, dim=128, heads=32, n_pad=64, row0=0, rope=1, rot=128, eps=1e-6,
+             clear=0)
+    a.update(kw.pop("args", {}))
+    args = M.HeadsArgs(*[a[f] for f, _ in M.HeadsArgs._fields_])
+    out = kw.pop("out", M.BF16)
+    ptrs = [kw.pop(n, FAKE) for n in ("x", "cs", "w")]
+    rc = M.lib().mako_heads(ctypes.byref(args), out, *ptrs, None, FAKE, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(out=M.F32), M.EUNSUPPORTED, "output type"),
+    (dict(args=dict(dim=288, ld=1 << 16)), M.EINVAL, "heads of 288"),   # the reference: dim > 256
+    (dict(args=dict(dim=100)), M.EINVAL, "heads of 100"),               # the reference: dim % 32
+    (dict(args=dict(rot=95)), M.EINVAL, "95 rotated"),                  # the reference: odd rot
+    (dict(args=dict(rope=3)), M.EINVAL, "rope 3"),
+    (dict(args=dict(rot=160)), M.EINVAL, "over 160"),
+    (dict(cs=None), M.EINVAL, "angle table"),
+    (dict(w=None), M.EINVAL, "without a weight"),
+    (dict(args=dict(eps=-1.0)), M.EINVAL, "eps"),
+    (dict(args=dict(row0=8)), M.EINVAL, "exceed 64"),
+    (dict(args=dict(col0=1)), M.EINVAL, "exceed rows of 4096"),
+    (dict(x=None), M.EINVAL, "null"),
+])
+def test_heads_refuses(kw, code, msg):
+    rc, err = heads_rc(**kw)
+    assert rc == code and msg in err, (rc, err)

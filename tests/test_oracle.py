@@ -45,7 +45,8 @@ def test_oracle_passes(check, oracle):
 
 MUTANTS = {1: "mask off by one", 2: "GQA map h % kv_heads", 3: "lse without the maximum",
            4: "k and v swapped in the scores", 5: "cube_topk ties to the larger index",
-           6: "sparse dense rows ignore valid"}
+           6: "sparse dense rows ignore valid", 7: "heads rotation sign of the second value",
+           8: "heads norm divides by the sum"}
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS), ids=lambda m: MUTANTS[m].replace(" ", "_"))
