@@ -5,13 +5,14 @@ Headline (one JSON line): causal GQA prefill at the Qwen3-8B shape (batch 1, 32 
 D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only the unmasked pairs
 (4 * D * S (S + 1) / 2 * 32). Beside it: batch-16 decode against a contiguous f16 KV cache (contexts drawn
 uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
-S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s. Inputs are synthetic N(0, 1), resident in
+S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s, and the head tiles of the prefill step
+(fp32 rows to normed, rotated bf16 tiles) in GB/s. Inputs are synthetic N(0, 1), resident in
 HBM before the timed region. `value` and ms_per_step come from --steps back-to-back launches bracketed by HIP
 events on the launch stream, after --warmup untimed ones; the roofline's `achieved` divides by the mean of each
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
 a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,copy]
 """
 import argparse
 import json
@@ -226,6 +227,32 @@ def bench_sparse(torch, M, steps, warmup):
             "blocks": blocks, "bound": "mfma" if t_mfma >= t_hbm else "hbm", "frac": max(t_mfma, t_hbm) / (kms * 1e-3)}
 
 
+def bench_heads(torch, M, steps, warmup):
+    """The head tiles of a Qwen3-8B prefill step (src/models/qwen_text.cpp:415-417): 4096 tokens, q 32 heads and
+    k 8 heads of 128 RMS-normed and rotated over the whole head, v 8 heads sliced, from fp32 rows into bf16 tiles;
+    one step is the three calls. Bytes: the fp32 rows read, the angle table read once, the tiles written."""
+    T, D = 4096, 128
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    xq = torch.randn((T, 32 * D), generator=gen, device="cuda")
+    xk = torch.randn((T, 8 * D), generator=gen, device="cuda")
+    xv = torch.randn((T, 8 * D), generator=gen, device="cuda")
+    ang = torch.rand((T, D // 2), generator=gen, device="cuda") * 6.283
+    cs = torch.stack([ang.cos(), ang.sin()], -1).contiguous()
+    wq, wk = (torch.rand(D, generator=gen, device="cuda") + 0.5 for _ in range(2))
+    yq = torch.empty((32, T, D), dtype=torch.bfloat16, device="cuda")
+    yk, yv = (torch.empty((8, T, D), dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    base = dict(rows=T, col0=0, stride=D, dim=D, n_pad=T)
+
+    def step():
+        M.heads(xq, yq, ld=32 * D, heads=32, rope=1, rot=D, eps=1e-6, cs=cs, w=wq, **base)
+        M.heads(xk, yk, ld=8 * D, heads=8, rope=1, rot=D, eps=1e-6, cs=cs, w=wk, **base)
+        M.heads(xv, yv, ld=8 * D, heads=8, **base)
+    ms, kms = time_launches(torch, step, steps, warmup)
+    nbytes = 48.0 * T * D * (4 + 2) + T * D // 2 * 8
+    gbps = nbytes / (kms * 1e-3) / 1e9
+    return {"ms": ms, "kernel_ms": kms, "gbps": gbps, "bytes": nbytes, "frac": gbps / PEAK_GBPS}
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the reference point that scales the HBM byte counters."""
     n = 256 << 20
@@ -242,7 +269,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, copy")
+                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -262,6 +289,7 @@ def main():
               "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, False),
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup),
+              "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps, args.warmup)}
         for leg in args.only.split(","):
             if leg not in fn:
@@ -275,6 +303,7 @@ def main():
     dec = bench_decode(torch, M, args.steps, args.warmup, with_cpu)
     bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup))
     spa = bench_sparse(torch, M, args.steps, args.warmup)
+    hds = bench_heads(torch, M, args.steps, args.warmup)
     line = {
         "metric": "attn prefill TFLOP/s (Qwen3-8B shape, seq 4096) + decode KV HBM GB/s, 1 GPU",
         "value": round(pre["tflops"], 2),
@@ -307,6 +336,11 @@ def main():
                          "config": {"workload": "causal block-sparse, 32 query heads / 8 kv heads, D 128, S 16384, "
                                                 "64x64 blocks: diagonal + 8 preceding + 8 random earlier (seed "
                                                 "16384, per kv head), bf16", "blocks_per_head": spa["blocks"]}},
+        "head_tiles": {"value": round(hds["gbps"], 1), "unit": "GB/s", "ms_per_step": round(hds["ms"], 4),
+                       "kernel_ms": round(hds["kernel_ms"], 4), "bound": "hbm", "frac": round(hds["frac"], 4),
+                       "config": {"workload": "Qwen3-8B prefill head tiles: 4096 tokens, q 32 and k 8 heads of 128 "
+                                              "RMS-normed and rotated, v 8 heads sliced, fp32 rows to bf16 tiles",
+                                  "bytes": hds["bytes"]}},
     }
     if with_cpu:
         line["cpu_baseline"] = pre["cpu_baseline"]

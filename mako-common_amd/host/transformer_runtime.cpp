@@ -20,6 +20,46 @@ std::string fmt(const char* f, A... a)
 
 }  // namespace
 
+void TransformerRuntime::heads(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, uint32_t col0, uint32_t n_heads,
+                               uint32_t T, uint32_t n_pad, gpu::Buffer* cs, uint32_t rope, gpu::Buffer* y,
+                               mako_dtype out)
+{
+    const mako_heads_args a{T, ld, col0, kHeadDim, kHeadDim, n_heads, n_pad, 0, rope, rope ? kHeadDim : 0u, 0.0f,
+                            1};
+    before(enc);
+    check(mako_heads(&a, out, static_cast<const float*>(x->ptr), cs ? static_cast<const float*>(cs->ptr) : nullptr,
+                     nullptr, nullptr, y->ptr, enc->stream));
+    after(enc, "heads");
+}
+
+void TransformerRuntime::heads_norm(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, uint32_t col0, uint32_t n_heads,
+                                    uint32_t T, uint32_t n_pad, gpu::Buffer* cs, uint64_t cs_off, uint32_t rope,
+                                    gpu::Buffer* w, float eps, uint32_t row0, gpu::Buffer* y, mako_dtype out)
+{
+    const mako_heads_args a{T, ld, col0, kHeadDim, kHeadDim, n_heads, n_pad, row0, rope, rope ? kHeadDim : 0u, eps,
+                            0};
+    const float* c = cs ? reinterpret_cast<const float*>(static_cast<const char*>(cs->ptr) + cs_off) : nullptr;
+    before(enc);
+    check(mako_heads(&a, out, static_cast<const float*>(x->ptr), c, static_cast<const float*>(w->ptr), nullptr,
+                     y->ptr, enc->stream));
+    after(enc, "heads_norm");
+}
+
+void TransformerRuntime::heads_partial(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, uint32_t col0,
+                                       uint32_t stride, uint32_t dim, uint32_t rot, uint32_t n_heads, uint32_t T,
+                                       uint32_t n_pad, gpu::Buffer* cs, gpu::Buffer* w, float eps, gpu::Buffer* y,
+                                       gpu::Buffer* map, mako_dtype out)
+{
+    if (dim > 256 || dim % 32 || rot % 2)
+        throw std::runtime_error(fmt("heads_partial: heads of %u with %u rotated", dim, rot));
+    const mako_heads_args a{T, ld, col0, stride, dim, n_heads, n_pad, 0, rot ? 1u : 0u, rot, w ? eps : 0.0f, 0};
+    before(enc);
+    check(mako_heads(&a, out, static_cast<const float*>(x->ptr), cs ? static_cast<const float*>(cs->ptr) : nullptr,
+                     w ? static_cast<const float*>(w->ptr) : nullptr,
+                     map ? static_cast<const int32_t*>(map->ptr) : nullptr, y->ptr, enc->stream));
+    after(enc, "heads_partial");
+}
+
 void TransformerRuntime::attention(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, gpu::Buffer* v, gpu::Buffer* o,
                                    uint32_t n_q, uint32_t q_pad, uint32_t n_k, uint32_t k_pad, uint32_t n_heads,
                                    uint32_t kv_heads, uint32_t q_pos0, uint32_t block, uint32_t dim,

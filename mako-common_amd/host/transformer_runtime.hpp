@@ -35,6 +35,21 @@ protected:
     static constexpr uint32_t kAttnRows = 64;  // query rows of a tile: q_pad is a multiple of it
     static uint32_t round_up(uint32_t x, uint32_t m) { return (x + m - 1) / m * m; }
 
+    // Head tiles from fp32 rows (src/models/runtime.hpp:78-89): head h of token t, x[t][col0 + h * dim ..], into
+    // y [heads][n_pad][dim] (f16, as the reference's half tiles, or bf16 by `out`). heads(): dim 128, rotated by
+    // cs [T][64] (cos, sin) pairs when rope is 1 (value i with i + 64) or 2 (2i with 2i + 1), rows [T, n_pad)
+    // zeroed. heads_norm(): each head RMS-normed first (times w [128]), written from y row row0, the rows past T
+    // left as they are; cs_off is a byte offset into cs. heads_partial(): heads of dim (a multiple of 32, at most
+    // 256) `stride` apart, the first rot values rotated (i with i + rot / 2, cs [T][rot / 2]), the norm when w is
+    // given, and through the row map when given (y row t from x row map[t], a zero row where map[t] < 0).
+    void heads(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, uint32_t col0, uint32_t heads, uint32_t T,
+               uint32_t n_pad, gpu::Buffer* cs, uint32_t rope, gpu::Buffer* y, mako_dtype out = MAKO_F16);
+    void heads_norm(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, uint32_t col0, uint32_t heads, uint32_t T,
+                    uint32_t n_pad, gpu::Buffer* cs, uint64_t cs_off, uint32_t rope, gpu::Buffer* w, float eps,
+                    uint32_t row0, gpu::Buffer* y, mako_dtype out = MAKO_F16);
+    void heads_partial(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, uint32_t col0, uint32_t stride, uint32_t dim,
+                       uint32_t rot, uint32_t heads, uint32_t T, uint32_t n_pad, gpu::Buffer* cs, gpu::Buffer* w,
+                       float eps, gpu::Buffer* y, gpu::Buffer* map = nullptr, mako_dtype out = MAKO_F16);
     // Flash attention over tiles q [heads][q_pad][dim], k and v [kv_heads][k_pad][dim] into o [n_q][heads * dim].
     // block: positions from here on see each other both ways; below it, causal (0: all both ways). dim 64, 128
     // or 256.

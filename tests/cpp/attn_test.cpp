@@ -5,8 +5,11 @@
 // * the same call with AttnOptions: bf16 in and out and an LSE, bidirectional (block 0, the call H3::block makes,
 //   src/models/h3.cpp:364);
 // * attention_decode: 4 sequences of different contexts, GQA 4;
-// * the refusal of a head width the reference refuses (src/models/runtime.cpp:266-267).
-// Tolerance: every element within 2e-3 + 1e-2 |ref|; LSE within 1e-3.
+// * the refusal of a head width the reference refuses (src/models/runtime.cpp:266-267);
+// * heads_partial with the call H3::block makes (src/models/h3.cpp:348: heads of 128, the first 96 values
+//   rotated, RMS norm, the cube row map), heads() with rotation and the padding cleared
+//   (src/models/qwen_text.cpp:308), and the refusal of heads_partial's odd rotation (src/models/runtime.cpp:249).
+// Tolerance: every element within 2e-3 + 1e-2 |ref|; LSE within 1e-3; head tiles within one f16 ulp.
 //   attn_test
 #include <hip/hip_runtime_api.h>
 
@@ -28,6 +31,8 @@ public:
     Harness() : TransformerRuntime(mako::gpu::Telemetry::kernels) {}
     using TransformerRuntime::attention;
     using TransformerRuntime::attention_decode;
+    using TransformerRuntime::heads;
+    using TransformerRuntime::heads_partial;
     using TransformerRuntime::encoder;
     using TransformerRuntime::finish;
     using TransformerRuntime::scratch;
@@ -191,6 +196,62 @@ int main()
         }
         check(threw, "attention refuses heads of 96");
         h.finish(enc);
+    }
+    // Head tiles through heads_partial (norm, 96 of 128 rotated, a row map) and heads (rotation, padding cleared).
+    {
+        const uint32_t T = 300, H = 4, D = 128, ld = 3 * H * D, n_pad = 320, rot = 96;
+        std::vector<float> x(size_t(T) * ld), cs(size_t(T) * D), w(D);
+        for (auto& e : x)
+            e = float(normal());
+        for (size_t i = 0; i < cs.size() / 2; ++i) {
+            const double a = 3.0 * normal();
+            cs[2 * i] = float(std::cos(a));
+            cs[2 * i + 1] = float(std::sin(a));
+        }
+        for (auto& e : w)
+            e = float(1.0 + 0.25 * normal());
+        std::vector<int32_t> map(T);
+        for (uint32_t t = 0; t < T; ++t)
+            map[t] = t % 7 == 3 ? -1 : int32_t((t * 37) % T);
+        auto xb = put(h, "x", x), cb = put(h, "cs", cs), wb = put(h, "w", w), mb = put(h, "map", map);
+        auto yb = h.scratch("y", size_t(H) * n_pad * D * 2);
+        auto within_ulp = [&](const std::vector<uint16_t>& got, const std::vector<uint16_t>& want) {
+            uint64_t bad = 0;
+            for (size_t i = 0; i < want.size(); ++i) {
+                const double g = oracle_f16_to_f32(got[i]), r = oracle_f16_to_f32(want[i]);
+                bad += !(std::fabs(g - r) <= std::fabs(r) * 0x1p-10 + 0x1p-24);
+            }
+            return bad;
+        };
+        auto* enc = h.encoder();
+        h.heads_partial(enc, xb, ld, 0, D, D, rot, H, T, n_pad, cb, wb, 1e-6f, yb, mb);
+        h.finish(enc);
+        const oracle_heads_args pa{T, ld, 0, D, D, H, n_pad, 0, 1, rot, 1e-6f, 0};
+        std::vector<uint16_t> want(size_t(H) * n_pad * D, 0), got = get<uint16_t>(yb, want.size());
+        oracle_heads(&pa, ORACLE_F16, x.data(), cs.data(), w.data(), map.data(), want.data());
+        for (uint32_t hh = 0; hh < H; ++hh)  // rows past T are not the call's: compare the first T of each head
+            for (uint32_t t = T; t < n_pad; ++t)
+                for (uint32_t i = 0; i < D; ++i)
+                    got[(size_t(hh) * n_pad + t) * D + i] = 0;
+        uint64_t bad = within_ulp(got, want);
+        check(bad == 0, "heads_partial (norm, 96 rotated, row map): " + std::to_string(bad) + " values past one ulp");
+
+        enc = h.encoder();
+        h.heads(enc, xb, ld, H * D, H, T, n_pad, cb, 1, yb);
+        h.finish(enc);
+        const oracle_heads_args ha{T, ld, H * D, D, D, H, n_pad, 0, 1, D, 0.0f, 1};
+        std::fill(want.begin(), want.end(), 0x7777);
+        oracle_heads(&ha, ORACLE_F16, x.data(), cs.data(), nullptr, nullptr, want.data());
+        bad = within_ulp(get<uint16_t>(yb, want.size()), want);
+        check(bad == 0, "heads (rope 1, padding cleared): " + std::to_string(bad) + " values past one ulp");
+
+        bool threw = false;
+        try {
+            h.heads_partial(enc, xb, ld, 0, D, D, 95, H, T, n_pad, cb, wb, 1e-6f, yb);
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()) == "heads_partial: heads of 128 with 95 rotated";
+        }
+        check(threw, "heads_partial refuses an odd rotation");
     }
     for (const auto& kt : h.kernel_times())
         std::printf("  %-20s %3u launches %8.3f ms\n", kt.kernel.c_str(), kt.count, kt.ms);
