@@ -143,3 +143,17 @@ def test_qwen3_8b_prefill_tiles():
         got = y.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
         want = O.heads(x[rows], cs[rows], w, out=O.BF16, **dict(a, rows=len(rows), n_pad=len(rows)))
         assert_tiles_close(got, want, O.BF16)
+
+
+@pytest.mark.parametrize("rope", [0, 1, 2])
+def test_unaligned_rows_take_the_general_kernel(rope):
+    """Rows whose head columns are not 16-byte aligned (col0 = 1) go through the general kernel: the same results."""
+    rng = np.random.default_rng(40 + rope)
+    T, H, D = 70, 4, 128
+    x = rng.standard_normal((T, H * D + 3)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    a = dict(rows=T, ld=H * D + 3, col0=1, stride=D, dim=D, heads=H, n_pad=80, rope=rope, rot=D if rope else 0,
+             eps=1e-6, clear=1)
+    print(f"unaligned rope={rope}", flush=True)
+    got, want = run(x, out=O.F16, cs=angles(rng, T, D // 2), w=w, **a)
+    assert_tiles_close(got, want, O.F16)
