@@ -171,6 +171,47 @@ typedef struct mako_heads_args {
 int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const float* cs, const float* w,
                const int32_t* map, void* y, void* stream);
 
+/*
+ * Split-K and gathered latent-cache primitives of the sparse latent decode (src/kernels/gemm.metal:683-870; no call
+ * site in the reference's own engines: they serve a caller that computes the softmax between them). f16 latent rows
+ * kv [*][dim], f32 accumulate, f32 outputs.
+ *
+ * mako_attn_pv (attn_pv, gemm.metal:683-730, PvArgs field for field): partial [splits][heads][dim], splits =
+ *   ceil(n_kv / keys_per_split), partial[z][h][d] = sum over keys t of split z of half(p[h][t]) * kv[t][d], with
+ *   p f32 [heads][n_kv]. Any number of heads (grid y of ceil(heads / 64), as the reference); dim and keys_per_split
+ *   multiples of 64; at most 65535 splits.
+ * mako_attn_gather_scores (attn_gather_scores, gemm.metal:743-786, GatherArgs field for field): scores f32
+ *   [tokens][heads][stride], scores[t][h][s] = q[t][h] . kv[list[t][s]] for s < count[t], 0 up to stride; q f16
+ *   [tokens][heads][dim], list u32 [tokens][stride], count u32 [tokens]. heads <= 64, dim a multiple of 256.
+ * mako_attn_gather_pv (attn_gather_pv, gemm.metal:788-844): partial f32 [splits][tokens][heads][dim],
+ *   partial[z][t][h][d] = sum over entries s of split z (per = ceil(stride / (splits * 64)) * 64 entries a split,
+ *   s < count[t]) of half(p[t][h][s]) * kv[list[t][s]][d]; p f32 [tokens][heads][stride]. heads <= 64, dim a
+ *   multiple of 128.
+ * mako_idx_dots (idx_dots, gemm.metal:846-870, IdxDotArgs field for field): dots f32 [tokens][heads][stride],
+ *   dots[t][h][p] = q[t][h] . pooled[p] in f32 for p < pools; q f32 [tokens][heads][dim], pooled f32 [pools][dim].
+ *   heads <= 32.
+ */
+typedef struct mako_pv_args {
+    uint32_t heads, dim, n_kv;
+    uint32_t keys_per_split;
+} mako_pv_args;
+
+typedef struct mako_gather_args {
+    uint32_t heads, dim, stride, splits, tokens;
+} mako_gather_args;
+
+typedef struct mako_idx_dot_args {
+    uint32_t heads, dim, pools, stride;
+} mako_idx_dot_args;
+
+int mako_attn_pv(const mako_pv_args* a, const float* p, const void* kv, float* partial, void* stream);
+int mako_attn_gather_scores(const mako_gather_args* a, const void* q, const void* kv, const uint32_t* list,
+                            const uint32_t* count, float* scores, void* stream);
+int mako_attn_gather_pv(const mako_gather_args* a, const float* p, const void* kv, const uint32_t* list,
+                        const uint32_t* count, float* partial, void* stream);
+int mako_idx_dots(const mako_idx_dot_args* a, uint32_t tokens, const float* q, const float* pooled, float* dots,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,7 +15,8 @@ U32_MAX = 0xFFFFFFFF
 
 # Every symbol include/mako_attn.h declares.
 EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
-           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode", "mako_heads")
+           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode", "mako_heads",
+           "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots")
 
 
 class AttnArgs(ctypes.Structure):
@@ -37,6 +38,18 @@ class DecodeArgs(ctypes.Structure):
 class HeadsArgs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("rows", "ld", "col0", "stride", "dim", "heads", "n_pad", "row0",
                                                "rope", "rot")] + [("eps", ctypes.c_float), ("clear", ctypes.c_uint32)]
+
+
+class PvArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("heads", "dim", "n_kv", "keys_per_split")]
+
+
+class GatherArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("heads", "dim", "stride", "splits", "tokens")]
+
+
+class IdxDotArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("heads", "dim", "pools", "stride")]
 
 
 class MakoError(RuntimeError):
@@ -67,7 +80,12 @@ def lib():
         L.mako_attn_decode_workspace.restype = SZ
         L.mako_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P, SZ, P]
         L.mako_heads.argtypes = [ctypes.POINTER(HeadsArgs), I, P, P, P, P, P, P]
-        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode", "mako_heads"):
+        L.mako_attn_pv.argtypes = [ctypes.POINTER(PvArgs), P, P, P, P]
+        L.mako_attn_gather_scores.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
+        L.mako_attn_gather_pv.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
+        L.mako_idx_dots.argtypes = [ctypes.POINTER(IdxDotArgs), U32, P, P, P, P]
+        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode", "mako_heads",
+                     "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots"):
             getattr(L, name).restype = I
         _lib = L
     return _lib
@@ -173,3 +191,31 @@ def heads(x, y, *, rows, ld, col0, stride, dim, heads, n_pad, row0=0, rope=0, ro
     a = HeadsArgs(rows, ld, col0, stride, dim, heads, n_pad, row0, rope, rot, eps, clear)
     _check(lib().mako_heads(ctypes.byref(a), dtype_code(y), _ptr(x), _ptr(cs), _ptr(w), _ptr(map_), _ptr(y),
                             _stream(stream)))
+
+
+def attn_pv(p, kv, partial, *, heads, dim, n_kv, keys_per_split, stream=None):
+    """mako_attn_pv: p float32 [heads][n_kv], kv float16 [*][dim], partial float32 [splits][heads][dim]."""
+    a = PvArgs(heads, dim, n_kv, keys_per_split)
+    _check(lib().mako_attn_pv(ctypes.byref(a), _ptr(p), _ptr(kv), _ptr(partial), _stream(stream)))
+
+
+def attn_gather_scores(q, kv, list_, count, scores, *, heads, dim, stride, tokens, splits=1, stream=None):
+    """mako_attn_gather_scores: q float16 [tokens][heads][dim], list_ / count int32 (read as u32), scores float32
+    [tokens][heads][stride]."""
+    a = GatherArgs(heads, dim, stride, splits, tokens)
+    _check(lib().mako_attn_gather_scores(ctypes.byref(a), _ptr(q), _ptr(kv), _ptr(list_), _ptr(count), _ptr(scores),
+                                         _stream(stream)))
+
+
+def attn_gather_pv(p, kv, list_, count, partial, *, heads, dim, stride, splits, tokens, stream=None):
+    """mako_attn_gather_pv: p float32 [tokens][heads][stride], partial float32 [splits][tokens][heads][dim]."""
+    a = GatherArgs(heads, dim, stride, splits, tokens)
+    _check(lib().mako_attn_gather_pv(ctypes.byref(a), _ptr(p), _ptr(kv), _ptr(list_), _ptr(count), _ptr(partial),
+                                     _stream(stream)))
+
+
+def idx_dots(q, pooled, dots, *, tokens, heads, dim, pools, stride, stream=None):
+    """mako_idx_dots: q float32 [tokens][heads][dim], pooled float32 [pools][dim], dots float32
+    [tokens][heads][stride]."""
+    a = IdxDotArgs(heads, dim, pools, stride)
+    _check(lib().mako_idx_dots(ctypes.byref(a), tokens, _ptr(q), _ptr(pooled), _ptr(dots), _stream(stream)))

@@ -7,6 +7,7 @@
  *   1 mask off by one (j < pos)          2 GQA map h % kv_heads           3 lse without the maximum
  *   4 k and v swapped in the scores      5 cube_topk ties to the larger   6 sparse dense rows ignore valid
  *   7 heads: the second value of a rotated pair takes v c - u s          8 heads: the norm divides by the sum
+ *   9 gathered lists read entries up to stride, not count[t]            10 probabilities not rounded to half
  */
 #include "attn_oracle.h"
 
@@ -638,5 +639,108 @@ int oracle_heads(const oracle_heads_args* a, int out_dtype, const float* x, cons
                 for (uint32_t i = 0; i < a->dim; ++i)
                     y[((size_t)h * a->n_pad + t) * a->dim + i] = 0;
     }
+    return 0;
+}
+
+/* ---- split-K and gathered latent-cache primitives ----------------------------------------------------------- */
+
+static double p_half(float p)
+{
+#if ORACLE_MUTANT == 10
+    return p;
+#else
+    return oracle_f16_to_f32(oracle_f32_to_f16(p)); /* half(p[...]) (gemm.metal:711, 822-827) */
+#endif
+}
+
+int oracle_attn_pv(uint32_t heads, uint32_t dim, uint32_t n_kv, uint32_t kps, const float* p, const uint16_t* kv,
+                   double* partial)
+{
+    if (!kps)
+        return 1;
+    const uint32_t splits = (n_kv + kps - 1) / kps;
+    for (uint32_t z = 0; z < splits; ++z)
+        for (uint32_t h = 0; h < heads; ++h) {
+            double* o = partial + ((size_t)z * heads + h) * dim;
+            for (uint32_t d = 0; d < dim; ++d)
+                o[d] = 0.0;
+            const uint32_t t_end = (z + 1) * kps < n_kv ? (z + 1) * kps : n_kv;
+            for (uint32_t t = z * kps; t < t_end; ++t) {
+                const double w = p_half(p[(size_t)h * n_kv + t]);
+                for (uint32_t d = 0; d < dim; ++d)
+                    o[d] += w * oracle_f16_to_f32(kv[(size_t)t * dim + d]);
+            }
+        }
+    return 0;
+}
+
+static uint32_t used(uint32_t cnt, uint32_t stride)
+{
+#if ORACLE_MUTANT == 9
+    (void)cnt;
+    return stride;
+#else
+    return cnt < stride ? cnt : stride;
+#endif
+}
+
+int oracle_gather_scores(uint32_t heads, uint32_t dim, uint32_t stride, uint32_t tokens, const uint16_t* q,
+                         const uint16_t* kv, const uint32_t* list, const uint32_t* count, double* scores)
+{
+    for (uint32_t t = 0; t < tokens; ++t) {
+        const uint32_t n = used(count[t], stride);
+        for (uint32_t h = 0; h < heads; ++h) {
+            const uint16_t* qr = q + ((size_t)t * heads + h) * dim;
+            double* o = scores + ((size_t)t * heads + h) * stride;
+            for (uint32_t s = 0; s < stride; ++s) {
+                double acc = 0.0;
+                if (s < n) {
+                    const uint16_t* kr = kv + (size_t)list[(size_t)t * stride + s] * dim;
+                    for (uint32_t d = 0; d < dim; ++d)
+                        acc += (double)oracle_f16_to_f32(qr[d]) * oracle_f16_to_f32(kr[d]);
+                }
+                o[s] = acc;
+            }
+        }
+    }
+    return 0;
+}
+
+int oracle_gather_pv(uint32_t heads, uint32_t dim, uint32_t stride, uint32_t splits, uint32_t tokens,
+                     const float* p, const uint16_t* kv, const uint32_t* list, const uint32_t* count,
+                     double* partial)
+{
+    if (!splits)
+        return 1;
+    const uint32_t per = (stride + splits * 64 - 1) / (splits * 64) * 64; /* gemm.metal:811 */
+    for (uint32_t z = 0; z < splits; ++z)
+        for (uint32_t t = 0; t < tokens; ++t) {
+            const uint32_t n = used(count[t], stride), s0 = z * per, s1 = s0 + per < n ? s0 + per : n;
+            for (uint32_t h = 0; h < heads; ++h) {
+                double* o = partial + (((size_t)z * tokens + t) * heads + h) * dim;
+                for (uint32_t d = 0; d < dim; ++d)
+                    o[d] = 0.0;
+                for (uint32_t s = s0; s < s1; ++s) {
+                    const double w = p_half(p[((size_t)t * heads + h) * stride + s]);
+                    const uint16_t* kr = kv + (size_t)list[(size_t)t * stride + s] * dim;
+                    for (uint32_t d = 0; d < dim; ++d)
+                        o[d] += w * oracle_f16_to_f32(kr[d]);
+                }
+            }
+        }
+    return 0;
+}
+
+int oracle_idx_dots(uint32_t heads, uint32_t dim, uint32_t pools, uint32_t stride, uint32_t tokens, const float* q,
+                    const float* pooled, double* dots)
+{
+    for (uint32_t t = 0; t < tokens; ++t)
+        for (uint32_t h = 0; h < heads; ++h)
+            for (uint32_t pl = 0; pl < pools; ++pl) {
+                double acc = 0.0;
+                for (uint32_t d = 0; d < dim; ++d)
+                    acc += (double)q[((size_t)t * heads + h) * dim + d] * pooled[(size_t)pl * dim + d];
+                dots[((size_t)t * heads + h) * stride + pl] = acc;
+            }
     return 0;
 }

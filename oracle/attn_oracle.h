@@ -20,6 +20,10 @@
  *   oracle_attn_decode  - one query row per sequence at position ctx - 1 against keys [0, ctx): the dense rule
  *                         with n_q = 1, q_pos0 = ctx - 1 (ops.metal:289), batched.
  *   oracle_lse_merge    - the split-K merge: o = sum_i exp(lse_i - lse) o_i, lse = log sum_i exp(lse_i).
+ *   oracle_attn_pv, oracle_gather_scores, oracle_gather_pv, oracle_idx_dots
+ *                       - attn_pv, attn_gather_scores, attn_gather_pv and idx_dots (src/kernels/gemm.metal:683-870):
+ *                         probabilities rounded to half before the product (gemm.metal:711, 822-827), gathered rows
+ *                         past count[t] as zeros (:767-774, :830-837), the split ranges of :700 and :811-812.
  *   oracle_heads        - the tile producers heads_half, heads_clear, heads_norm_half and heads_partial
  *                         (src/kernels/ops.metal:21-52, 376-407, 587-620): slice, RMS norm times w
  *                         (x / sqrt(mean(x^2) + eps)), rotation of pairs (u, v) -> (u c - v s, v c + u s),
@@ -128,6 +132,21 @@ typedef struct oracle_heads_args {
  * its angles) when map is not NULL, a zero row where map[t] < 0. Rows it does not write are left as they are. */
 int oracle_heads(const oracle_heads_args* a, int out_dtype, const float* x, const float* cs, const float* w,
                  const int32_t* map, uint16_t* y);
+
+/* attn_pv: partial [ceil(n_kv / kps)][heads][dim] from p f32 [heads][n_kv] and kv f16 bits [n_kv][dim]. */
+int oracle_attn_pv(uint32_t heads, uint32_t dim, uint32_t n_kv, uint32_t kps, const float* p, const uint16_t* kv,
+                   double* partial);
+/* attn_gather_scores: scores [tokens][heads][stride] from q f16 bits [tokens][heads][dim], kv [*][dim]. */
+int oracle_gather_scores(uint32_t heads, uint32_t dim, uint32_t stride, uint32_t tokens, const uint16_t* q,
+                         const uint16_t* kv, const uint32_t* list, const uint32_t* count, double* scores);
+/* attn_gather_pv: partial [splits][tokens][heads][dim] from p f32 [tokens][heads][stride]. */
+int oracle_gather_pv(uint32_t heads, uint32_t dim, uint32_t stride, uint32_t splits, uint32_t tokens,
+                     const float* p, const uint16_t* kv, const uint32_t* list, const uint32_t* count,
+                     double* partial);
+/* idx_dots: dots [tokens][heads][stride] (columns p < pools written) from q f32 [tokens][heads][dim] and pooled
+ * f32 [pools][dim]. */
+int oracle_idx_dots(uint32_t heads, uint32_t dim, uint32_t pools, uint32_t stride, uint32_t tokens, const float* q,
+                    const float* pooled, double* dots);
 
 void oracle_lse_merge(uint32_t n, uint32_t dim, const double* o_i, const double* lse_i, double* o, double* lse);
 

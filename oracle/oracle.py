@@ -62,6 +62,10 @@ def lib(mutant=None):
         L.oracle_attn_decode.argtypes = [U32, U32, U32, U32, U32, F, I, P, P, P, P, P, P, I]
         L.oracle_attn_decode_rows.argtypes = [U32, U32, U32, U32, U32, F, I, P, P, P, P, P, SZ, P, P, I]
         L.oracle_heads.argtypes = [ctypes.POINTER(HeadsArgs), I, P, P, P, P, P]
+        L.oracle_attn_pv.argtypes = [U32, U32, U32, U32, P, P, P]
+        L.oracle_gather_scores.argtypes = [U32, U32, U32, U32, P, P, P, P, P]
+        L.oracle_gather_pv.argtypes = [U32, U32, U32, U32, U32, P, P, P, P, P]
+        L.oracle_idx_dots.argtypes = [U32, U32, U32, U32, U32, P, P, P]
         L.oracle_lse_merge.argtypes = [U32, U32, P, P, P, P]
         L.oracle_lse_merge.restype = None
         L.oracle_f32_to_f16.argtypes = [F]
@@ -257,6 +261,64 @@ def heads(x, cs=None, w=None, map_=None, *, rows, ld, col0, stride, dim, heads, 
     if rc:
         raise ValueError("oracle_heads: bad arguments")
     return y
+
+
+def _u32(x):
+    return np.ascontiguousarray(x).astype(np.uint32, copy=False)
+
+
+def attn_pv(p, kv, *, heads, dim, n_kv, keys_per_split, mutant=None):
+    """attn_pv (src/kernels/gemm.metal:688-730): p float32 [heads][n_kv], kv float16 bits [n_kv][dim]. Returns
+    partial float64 [ceil(n_kv / keys_per_split)][heads][dim]."""
+    p = np.ascontiguousarray(p, np.float32)
+    kv = np.ascontiguousarray(kv, np.uint16)
+    assert p.size >= heads * n_kv and kv.size >= n_kv * dim
+    splits = -(-n_kv // keys_per_split)
+    out = np.zeros((splits, heads, dim), np.float64)
+    if lib(mutant).oracle_attn_pv(heads, dim, n_kv, keys_per_split, _p(p), _p(kv), _p(out)):
+        raise ValueError("oracle_attn_pv: bad arguments")
+    return out
+
+
+def gather_scores(q, kv, list_, count, *, heads, dim, stride, tokens, mutant=None):
+    """attn_gather_scores (src/kernels/gemm.metal:743-786): q float16 bits [tokens][heads][dim], kv float16 bits
+    [rows][dim], list_ [tokens][stride], count [tokens]. Returns scores float64 [tokens][heads][stride]."""
+    q = np.ascontiguousarray(q, np.uint16)
+    kv = np.ascontiguousarray(kv, np.uint16)
+    list_, count = _u32(list_), _u32(count)
+    assert q.size >= tokens * heads * dim and list_.size >= tokens * stride and count.size >= tokens
+    rows = kv.size // dim
+    for t in range(tokens):
+        assert (list_.reshape(-1)[t * stride:t * stride + min(int(count[t]), stride)] < rows).all()
+    out = np.zeros((tokens, heads, stride), np.float64)
+    lib(mutant).oracle_gather_scores(heads, dim, stride, tokens, _p(q), _p(kv), _p(list_), _p(count), _p(out))
+    return out
+
+
+def gather_pv(p, kv, list_, count, *, heads, dim, stride, splits, tokens, mutant=None):
+    """attn_gather_pv (src/kernels/gemm.metal:788-844): p float32 [tokens][heads][stride]. Returns partial float64
+    [splits][tokens][heads][dim]."""
+    p = np.ascontiguousarray(p, np.float32)
+    kv = np.ascontiguousarray(kv, np.uint16)
+    list_, count = _u32(list_), _u32(count)
+    assert p.size >= tokens * heads * stride and list_.size >= tokens * stride and count.size >= tokens
+    out = np.zeros((splits, tokens, heads, dim), np.float64)
+    if lib(mutant).oracle_gather_pv(heads, dim, stride, splits, tokens, _p(p), _p(kv), _p(list_), _p(count),
+                                    _p(out)):
+        raise ValueError("oracle_gather_pv: bad arguments")
+    return out
+
+
+def idx_dots(q, pooled, *, heads, dim, pools, stride, tokens, dots=None, mutant=None):
+    """idx_dots (src/kernels/gemm.metal:846-870): q float32 [tokens][heads][dim], pooled float32 [pools][dim].
+    Returns dots float64 [tokens][heads][stride], columns from pools on as passed in (zeros by default)."""
+    q = np.ascontiguousarray(q, np.float32)
+    pooled = np.ascontiguousarray(pooled, np.float32)
+    if dots is None:
+        dots = np.zeros((tokens, heads, stride), np.float64)
+    dots = np.ascontiguousarray(dots, np.float64)
+    lib(mutant).oracle_idx_dots(heads, dim, pools, stride, tokens, _p(q), _p(pooled), _p(dots))
+    return dots
 
 
 def to_f16_bits(x):

@@ -15,6 +15,12 @@ planted mistake), so the same checks both pass on the oracle and are shown to fa
                    product (u + i v)(c + i s); rope 2 pairs adjacent values; values past rot pass through; with w = 1
                    the normed head has unit mean square and is invariant to scaling x; a mapped row is the
                    unmapped row of its source, a negative map gives a zero row
+  gather         - attn_pv summed over its splits is numpy's product of the half-rounded p and kv; a one-hot p
+                   puts one kv row in exactly the split that owns its key; p = 1 + 2^-12 acts as 1 (half rounding);
+                   scores with the identity list are numpy's q kv^T, a permuted list permutes the columns, entries
+                   from count[t] on are 0; gather_pv with the identity list equals attn_pv at per keys a split, and
+                   a one-hot p lands in split s // per; idx_dots is numpy's float64 q pooled^T, columns past pools
+                   untouched
 """
 import glob
 import os
@@ -350,5 +356,92 @@ def check_heads(mutant=None):
     return not msgs, "; ".join(msgs)
 
 
+def check_gather(mutant=None):
+    rng = _rng(77)
+    msgs = []
+    H, D, N, kps = 5, 64, 200, 64
+    kv = _f16(rng.standard_normal((N, D)))
+    kvf = O.bits_to_f32(kv, O.F16).astype(np.float64)
+    p = rng.uniform(0.0, 1.0, (H, N)).astype(np.float32)
+    ph = p.astype(np.float16).astype(np.float64)
+    part = O.attn_pv(p, kv, heads=H, dim=D, n_kv=N, keys_per_split=kps, mutant=mutant)
+    if part.shape != (4, H, D) or not _close(part.sum(0), ph @ kvf, 1e-12):
+        msgs.append("attn_pv splits do not sum to p kv")
+    onehot = np.zeros((H, N), np.float32)
+    taus = [0, 63, 64, 150, 199]
+    for h, tau in enumerate(taus):
+        onehot[h, tau] = 1.0
+    part = O.attn_pv(onehot, kv, heads=H, dim=D, n_kv=N, keys_per_split=kps, mutant=mutant)
+    want = np.zeros_like(part)
+    for h, tau in enumerate(taus):
+        want[tau // kps, h] = kvf[tau]
+    if not np.array_equal(part, want):
+        msgs.append("attn_pv: a one-hot p does not give its kv row in its key's split")
+    part = O.attn_pv(np.full((H, N), 1.0 + 2.0 ** -12, np.float32), kv, heads=H, dim=D, n_kv=N, keys_per_split=kps,
+                     mutant=mutant)
+    if not np.array_equal(part.sum(0)[0], kvf.sum(0)):
+        msgs.append("attn_pv does not round p to half")
+
+    # gathered scores: T tokens, lists of S entries, count[t] used
+    T, S, R, DL = 3, 96, 300, 256
+    kvl = _f16(rng.standard_normal((R, DL)) * 0.5)
+    kvlf = O.bits_to_f32(kvl, O.F16).astype(np.float64)
+    q = _f16(rng.standard_normal((T, H, DL)) * 0.5)
+    qf = O.bits_to_f32(q, O.F16).astype(np.float64)
+    ident = np.tile(np.arange(S, dtype=np.uint32), (T, 1))
+    full = np.full(T, S, np.uint32)
+    sc = O.gather_scores(q, kvl, ident, full, heads=H, dim=DL, stride=S, tokens=T, mutant=mutant)
+    if not _close(sc, qf @ kvlf[:S].T, 1e-12):
+        msgs.append("gather_scores with the identity list is not q kv^T")
+    perm = np.stack([rng.permutation(R)[:S] for _ in range(T)]).astype(np.uint32)
+    sc = O.gather_scores(q, kvl, perm, full, heads=H, dim=DL, stride=S, tokens=T, mutant=mutant)
+    if not all(_close(sc[t], qf[t] @ kvlf[perm[t]].T, 1e-12) for t in range(T)):
+        msgs.append("gather_scores with a permuted list does not permute the columns")
+    cnt = np.array([0, 37, S], np.uint32)
+    sc2 = O.gather_scores(q, kvl, perm, cnt, heads=H, dim=DL, stride=S, tokens=T, mutant=mutant)
+    if not all(np.array_equal(sc2[t, :, :cnt[t]], sc[t, :, :cnt[t]]) and (sc2[t, :, cnt[t]:] == 0).all()
+               for t in range(T)):
+        msgs.append("gather_scores entries from count[t] on are not zero")
+
+    # gathered P V
+    pg = rng.uniform(0.0, 1.0, (T, H, S)).astype(np.float32)
+    for splits in (1, 2, 3):
+        per = -(-S // (splits * 64)) * 64
+        gp = O.gather_pv(pg, kvl, ident, full, heads=H, dim=DL, stride=S, splits=splits, tokens=T, mutant=mutant)
+        ok = True
+        for t in range(T):
+            ref = O.attn_pv(pg[t], kvl[:S], heads=H, dim=DL, n_kv=S, keys_per_split=per, mutant=mutant)
+            want = np.zeros((splits, H, DL))  # ceil(S / per) <= splits: trailing splits are empty
+            want[:len(ref)] = ref
+            ok &= _close(gp[:, t], want, 1e-12)
+        if not ok:
+            msgs.append(f"gather_pv with the identity list differs from attn_pv at {per} keys a split")
+    gp = O.gather_pv(pg, kvl, perm, cnt, heads=H, dim=DL, stride=S, splits=2, tokens=T, mutant=mutant)
+    pgh = pg.astype(np.float16).astype(np.float64)
+    if not all(_close(gp[:, t].sum(0), pgh[t, :, :cnt[t]] @ kvlf[perm[t, :cnt[t]]], 1e-12) for t in range(T)):
+        msgs.append("gather_pv splits do not sum to p kv over the first count[t] entries")
+    oh = np.zeros((T, H, S), np.float32)
+    picks = [(0, 0, 5), (1, 2, 36), (2, 4, 64), (2, 1, 95)]
+    for t, h, s_ in picks:
+        oh[t, h, s_] = 1.0
+    gp = O.gather_pv(oh, kvl, perm, full, heads=H, dim=DL, stride=S, splits=2, tokens=T, mutant=mutant)
+    want = np.zeros_like(gp)
+    for t, h, s_ in picks:
+        want[s_ // 64, t, h] = kvlf[perm[t, s_]]
+    if not np.array_equal(gp, want):
+        msgs.append("gather_pv: a one-hot p does not land in split s // per")
+
+    # idx_dots in float
+    P, St = 45, 64
+    qd = rng.standard_normal((T, H, 96)).astype(np.float32)
+    pooled = rng.standard_normal((P, 96)).astype(np.float32)
+    d = O.idx_dots(qd, pooled, heads=H, dim=96, pools=P, stride=St, tokens=T, dots=np.full((T, H, St), 7.0),
+                   mutant=mutant)
+    if not _close(d[:, :, :P], qd.astype(np.float64) @ pooled.astype(np.float64).T, 1e-12) or \
+            not (d[:, :, P:] == 7.0).all():
+        msgs.append("idx_dots is not q pooled^T on the first pools columns")
+    return not msgs, "; ".join(msgs)
+
+
 ALL_CHECKS = [check_goldens, check_closed_forms, check_invariants, check_sparse, check_cube_select,
-              check_decode_and_merge, check_heads]
+              check_decode_and_merge, check_heads, check_gather]

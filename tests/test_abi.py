@@ -139,3 +139,57 @@ def heads_rc(**kw):
 def test_heads_refuses(kw, code, msg):
     rc, err = heads_rc(**kw)
     assert rc == code and msg in err, (rc, err)
+
+
+def gather_rc(fn, **kw):
+    """Calls one of the four gathered decode helpers with valid arguments but for the overrides in kw."""
+    if fn == "mako_attn_pv":
+        a = dict(heads=64, dim=512, n_kv=4096, keys_per_split=256)
+        a.update(kw.pop("args", {}))
+        args = M.PvArgs(*[a[f] for f, _ in M.PvArgs._fields_])
+        ptrs = [kw.pop(n, FAKE) for n in ("p", "kv", "partial")]
+    elif fn == "mako_idx_dots":
+        a = dict(heads=32, dim=128, pools=100, stride=128)
+        a.update(kw.pop("args", {}))
+        args = M.IdxDotArgs(*[a[f] for f, _ in M.IdxDotArgs._fields_])
+        ptrs = [kw.pop("tokens", 4)] + [kw.pop(n, FAKE) for n in ("q", "pooled", "dots")]
+    else:
+        a = dict(heads=64, dim=512, stride=2048, splits=4, tokens=4)
+        a.update(kw.pop("args", {}))
+        args = M.GatherArgs(*[a[f] for f, _ in M.GatherArgs._fields_])
+        ptrs = [kw.pop(n, FAKE) for n in ("x", "kv", "list", "count", "out")]
+    rc = getattr(M.lib(), fn)(ctypes.byref(args), *ptrs, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("fn,kw,code,msg", [
+    ("mako_attn_pv", dict(args=dict(dim=96)), M.EINVAL, "heads of 96"),            # gemm.metal: TN = 64 columns
+    ("mako_attn_pv", dict(args=dict(keys_per_split=100)), M.EINVAL, "100 keys a split"),  # gemm.metal:685
+    ("mako_attn_pv", dict(args=dict(keys_per_split=64, n_kv=65536 * 64)), M.EINVAL, "65536 splits"),
+    ("mako_attn_pv", dict(kv=ctypes.c_void_p(FAKE.value + 2)), M.EINVAL, "aligned"),
+    ("mako_attn_pv", dict(p=None), M.EINVAL, "null"),
+    ("mako_attn_gather_scores", dict(args=dict(heads=65)), M.EINVAL, "65 heads"),  # gemm.metal:743 heads <= 64
+    ("mako_attn_gather_scores", dict(args=dict(dim=384)), M.EINVAL, "of 384"),    # gemm.metal:737 dim % 256
+    ("mako_attn_gather_scores", dict(args=dict(tokens=70000)), M.EINVAL, "70000 tokens"),
+    ("mako_attn_gather_scores", dict(count=None), M.EINVAL, "null"),
+    ("mako_attn_gather_pv", dict(args=dict(dim=320)), M.EINVAL, "of 320"),        # gemm.metal:789 dim / 128
+    ("mako_attn_gather_pv", dict(args=dict(splits=0)), M.EINVAL, "0 splits"),
+    ("mako_attn_gather_pv", dict(args=dict(splits=300, tokens=300)), M.EINVAL, "exceed the grid"),
+    ("mako_attn_gather_pv", dict(list=None), M.EINVAL, "null"),
+    ("mako_idx_dots", dict(args=dict(heads=33)), M.EINVAL, "33 heads"),            # gemm.metal:850 heads <= 32
+    ("mako_idx_dots", dict(args=dict(stride=64)), M.EINVAL, "rows of 64"),
+    ("mako_idx_dots", dict(pooled=None), M.EINVAL, "null"),
+])
+def test_gather_helpers_refuse(fn, kw, code, msg):
+    rc, err = gather_rc(fn, **kw)
+    assert rc == code and msg in err, (rc, err)
+
+
+@pytest.mark.parametrize("fn,kw", [("mako_attn_pv", dict(args=dict(n_kv=0))),
+                                   ("mako_attn_gather_scores", dict(args=dict(tokens=0))),
+                                   ("mako_attn_gather_pv", dict(args=dict(tokens=0))),
+                                   ("mako_idx_dots", dict(tokens=0))])
+def test_gather_helpers_empty_is_a_no_op(fn, kw):
+    """No keys or no tokens: nothing to launch, the call succeeds (no GPU needed)."""
+    rc, err = gather_rc(fn, **kw)
+    assert rc == M.OK, err
