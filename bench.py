@@ -12,7 +12,7 @@ events on the launch stream, after --warmup untimed ones; the roofline's `achiev
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
 a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,gather,copy]
 """
 import argparse
 import json
@@ -253,6 +253,54 @@ def bench_heads(torch, M, steps, warmup):
     return {"ms": ms, "kernel_ms": kms, "gbps": gbps, "bytes": nbytes, "frac": gbps / PEAK_GBPS}
 
 
+def bench_gather(torch, M, steps, warmup):
+    """The split-K and gathered latent-cache helpers (src/kernels/gemm.metal:683-870) at a sparse latent decode
+    shape: a 65536-row cache of 512-wide f16 latent rows; 64 consecutive query tokens of 64 heads, each over its own
+    list of 2048 rows (attn_gather_scores, then attn_gather_pv in one split); attn_pv of 64 heads over 32768 keys in
+    splits of 512; the float indexer (idx_dots) of 32 heads of 128 over 16384 pooled keys. Each kernel is timed on
+    its own; bytes are what it must move (rows gathered, probabilities and scores once, outputs once); the roofline
+    of each is the larger of its HBM and MFMA times (f16 MFMA 2.5 PFLOP/s, f32 MFMA 157.3 TFLOP/s)."""
+    import numpy as np
+
+    R, T, H, D, S = 65536, 64, 64, 512, 2048
+    gen = torch.Generator(device="cuda").manual_seed(512)
+    kv = (torch.randn((R, D), generator=gen, device="cuda") * 0.1).half()
+    q = (torch.randn((T, H, D), generator=gen, device="cuda") * 0.1).half()
+    rng = np.random.default_rng(512)
+    lst = torch.from_numpy(np.stack([rng.choice(R, S, replace=False) for _ in range(T)]).astype(np.int32)).cuda()
+    cnt = torch.full((T,), S, dtype=torch.int32, device="cuda")
+    scores = torch.empty((T, H, S), dtype=torch.float32, device="cuda")
+    p = torch.softmax(torch.randn((T, H, S), generator=gen, device="cuda"), -1)
+    part = torch.empty((1, T, H, D), dtype=torch.float32, device="cuda")
+    NK, KPS = 32768, 512
+    pk = torch.softmax(torch.randn((H, NK), generator=gen, device="cuda"), -1)
+    kpart = torch.empty((NK // KPS, H, D), dtype=torch.float32, device="cuda")
+    IH, ID, PL = 32, 128, 16384
+    iq = torch.randn((T, IH, ID), generator=gen, device="cuda")
+    pooled = torch.randn((PL, ID), generator=gen, device="cuda")
+    dots = torch.empty((T, IH, PL), dtype=torch.float32, device="cuda")
+    g = dict(heads=H, dim=D, stride=S, tokens=T)
+    legs = {
+        "attn_gather_scores": (lambda: M.attn_gather_scores(q, kv, lst, cnt, scores, **g),
+                               T * S * D * 2 + T * H * D * 2 + T * S * 4 + T * H * S * 4, 2.0 * T * H * S * D, 2500),
+        "attn_gather_pv": (lambda: M.attn_gather_pv(p, kv, lst, cnt, part, splits=1, **g),
+                           T * S * D * 2 + T * H * S * 4 + T * S * 4 + T * H * D * 4, 2.0 * T * H * S * D, 2500),
+        "attn_pv": (lambda: M.attn_pv(pk, kv, kpart, heads=H, dim=D, n_kv=NK, keys_per_split=KPS),
+                    NK * D * 2 + H * NK * 4 + NK // KPS * H * D * 4, 2.0 * H * NK * D, 2500),
+        "idx_dots": (lambda: M.idx_dots(iq, pooled, dots, tokens=T, heads=IH, dim=ID, pools=PL, stride=PL),
+                     T * IH * ID * 4 + PL * ID * 4 + T * IH * PL * 4, 2.0 * T * IH * PL * ID, 157.3),
+    }
+    out = {}
+    for name, (fn, nbytes, flop, peak_tf) in legs.items():
+        ms, kms = time_launches(torch, fn, steps, warmup)
+        t_hbm, t_mfma = nbytes / (PEAK_GBPS * 1e9), flop / (peak_tf * 1e12)
+        out[name] = {"ms": round(ms, 4), "kernel_ms": round(kms, 4), "bytes": nbytes, "flop": flop,
+                     "gbps": round(nbytes / (kms * 1e-3) / 1e9, 1), "tflops": round(flop / (kms * 1e-3) / 1e12, 2),
+                     "bound": "mfma" if t_mfma > t_hbm else "hbm",
+                     "frac": round(max(t_hbm, t_mfma) / (kms * 1e-3), 4)}
+    return out
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the reference point that scales the HBM byte counters."""
     n = 256 << 20
@@ -269,7 +317,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, copy")
+                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, gather, copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -290,6 +338,7 @@ def main():
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
+              "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps, args.warmup)}
         for leg in args.only.split(","):
             if leg not in fn:

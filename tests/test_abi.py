@@ -165,16 +165,16 @@ def gather_rc(fn, **kw):
 @pytest.mark.parametrize("fn,kw,code,msg", [
     ("mako_attn_pv", dict(args=dict(dim=96)), M.EINVAL, "heads of 96"),            # gemm.metal: TN = 64 columns
     ("mako_attn_pv", dict(args=dict(keys_per_split=100)), M.EINVAL, "100 keys a split"),  # gemm.metal:685
-    ("mako_attn_pv", dict(args=dict(keys_per_split=64, n_kv=65536 * 64)), M.EINVAL, "65536 splits"),
+    ("mako_attn_pv", dict(args=dict(keys_per_split=64, n_kv=1 << 31)), M.EINVAL, "exceed the grid"),
     ("mako_attn_pv", dict(kv=ctypes.c_void_p(FAKE.value + 2)), M.EINVAL, "aligned"),
     ("mako_attn_pv", dict(p=None), M.EINVAL, "null"),
     ("mako_attn_gather_scores", dict(args=dict(heads=65)), M.EINVAL, "65 heads"),  # gemm.metal:743 heads <= 64
     ("mako_attn_gather_scores", dict(args=dict(dim=384)), M.EINVAL, "of 384"),    # gemm.metal:737 dim % 256
-    ("mako_attn_gather_scores", dict(args=dict(tokens=70000)), M.EINVAL, "70000 tokens"),
+    ("mako_attn_gather_scores", dict(args=dict(tokens=1 << 23)), M.EINVAL, "exceed the grid"),
     ("mako_attn_gather_scores", dict(count=None), M.EINVAL, "null"),
     ("mako_attn_gather_pv", dict(args=dict(dim=320)), M.EINVAL, "of 320"),        # gemm.metal:789 dim / 128
     ("mako_attn_gather_pv", dict(args=dict(splits=0)), M.EINVAL, "0 splits"),
-    ("mako_attn_gather_pv", dict(args=dict(splits=300, tokens=300)), M.EINVAL, "exceed the grid"),
+    ("mako_attn_gather_pv", dict(args=dict(splits=4096, tokens=1024)), M.EINVAL, "exceed the grid"),
     ("mako_attn_gather_pv", dict(list=None), M.EINVAL, "null"),
     ("mako_idx_dots", dict(args=dict(heads=33)), M.EINVAL, "33 heads"),            # gemm.metal:850 heads <= 32
     ("mako_idx_dots", dict(args=dict(stride=64)), M.EINVAL, "rows of 64"),

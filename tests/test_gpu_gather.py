@@ -125,7 +125,9 @@ def test_attn_gather_pv(case, splits):
 IDX = [
     # tokens, heads, dim, pools, stride
     (4, 32, 128, 1000, 1024),  # the indexer: 32 heads of 128 over 1000 pooled keys
-    (3, 5, 33, 70, 80),        # odd width, part tiles of heads and pools
+    (2, 7, 36, 300, 301),      # width a multiple of 4 but not of the 32-float chunk, a part pool tile
+    (2, 32, 64, 129, 129),
+    (3, 5, 33, 70, 80),        # odd width (one float a lane a step), part tiles of heads and pools
     (1, 1, 1, 1, 1),
 ]
 
