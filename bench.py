@@ -5,8 +5,9 @@ Headline (one JSON line): causal GQA prefill at the Qwen3-8B shape (batch 1, 32 
 D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only the unmasked pairs
 (4 * D * S (S + 1) / 2 * 32). Beside it: batch-16 decode against a contiguous f16 KV cache (contexts drawn
 uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
-S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s, and the head tiles of the prefill step
-(fp32 rows to normed, rotated bf16 tiles) in GB/s. Inputs are synthetic N(0, 1), resident in
+S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s, the head tiles of the prefill step
+(fp32 rows to normed, rotated bf16 tiles) in GB/s, and the split-K / gathered latent-cache helpers of a sparse latent
+decode, each against its own roof. Inputs are synthetic N(0, 1), resident in
 HBM before the timed region. `value` and ms_per_step come from --steps back-to-back launches bracketed by HIP
 events on the launch stream, after --warmup untimed ones; the roofline's `achieved` divides by the mean of each
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
@@ -353,6 +354,7 @@ def main():
     bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup))
     spa = bench_sparse(torch, M, args.steps, args.warmup)
     hds = bench_heads(torch, M, args.steps, args.warmup)
+    gat = bench_gather(torch, M, args.steps, args.warmup)
     line = {
         "metric": "attn prefill TFLOP/s (Qwen3-8B shape, seq 4096) + decode KV HBM GB/s, 1 GPU",
         "value": round(pre["tflops"], 2),
@@ -390,7 +392,14 @@ def main():
                        "config": {"workload": "Qwen3-8B prefill head tiles: 4096 tokens, q 32 and k 8 heads of 128 "
                                               "RMS-normed and rotated, v 8 heads sliced, fp32 rows to bf16 tiles",
                                   "bytes": hds["bytes"]}},
+        "latent_decode": {name: {"kernel_ms": v["kernel_ms"], "gbps": v["gbps"], "tflops": v["tflops"],
+                                 "bound": v["bound"], "frac": v["frac"]} for name, v in gat.items()},
     }
+    line["latent_decode"]["config"] = {"workload": "sparse latent decode helpers: 65536-row cache of 512-wide f16 "
+                                                   "latent rows, 64 tokens x 64 heads over lists of 2048 (scores, "
+                                                   "then P V in one split), attn_pv of 64 heads over 32768 keys in "
+                                                   "splits of 512, f32 indexer 64 x 32 heads of 128 over 16384 "
+                                                   "pooled keys"}
     if with_cpu:
         line["cpu_baseline"] = pre["cpu_baseline"]
         line["parity"] = pre["parity"]
