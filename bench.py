@@ -13,7 +13,7 @@ events on the launch stream, after --warmup untimed ones; the roofline's `achiev
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
 a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,gather,copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,gather,proj,copy]
 """
 import argparse
 import json
@@ -302,6 +302,27 @@ def bench_gather(torch, M, steps, warmup):
     return out
 
 
+def bench_proj(torch, M, steps, warmup):
+    """The output projection after attention at Qwen3-8B's prefill shape (src/models/qwen_text.cpp:312): 4096
+    tokens x 4096 -> 4096, bf16 weights, f32 output. Three forms: bf16 activations as the attention writes them (the
+    headline of this leg), f32 activations rounded in the GEMM's loads, and f32 with the bf16 split (twice the
+    MFMA work). TFLOP/s count 2 t k n (4 t k n with the split)."""
+    t = k = n = 4096
+    gen = torch.Generator(device="cuda").manual_seed(312)
+    w = (torch.randn((n, k), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    xf = torch.randn((t, k), generator=gen, device="cuda")
+    xb = xf.to(torch.bfloat16)
+    y = torch.empty((t, n), dtype=torch.float32, device="cuda")
+    out = {}
+    for name, x, split in (("bf16_x", xb, 0), ("f32_x", xf, 0), ("f32_x_split", xf, 1)):
+        ms, kms = time_launches(torch, lambda: M.proj_bf16(w, x, y, t=t, k=k, n=n, split=split), steps, warmup)
+        flop = 2.0 * t * k * n * (2 if split else 1)
+        out[name] = {"ms": round(ms, 4), "kernel_ms": round(kms, 4), "flop": flop,
+                     "tflops": round(flop / (kms * 1e-3) / 1e12, 1),
+                     "frac": round(flop / (kms * 1e-3) / 1e12 / PEAK_TFLOPS, 4)}
+    return out
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the reference point that scales the HBM byte counters."""
     n = 256 << 20
@@ -318,7 +339,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, gather, copy")
+                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, gather, proj, copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -340,6 +361,7 @@ def main():
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
+              "proj": lambda: bench_proj(torch, M, args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps, args.warmup)}
         for leg in args.only.split(","):
             if leg not in fn:

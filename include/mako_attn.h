@@ -212,6 +212,30 @@ int mako_attn_gather_pv(const mako_gather_args* a, const float* p, const void* k
 int mako_idx_dots(const mako_idx_dot_args* a, uint32_t tokens, const float* q, const float* pooled, float* dots,
                   void* stream);
 
+/*
+ * The output projection after attention: Runtime::proj with BF16 weights (src/gpu/runtime.cpp:164-205; its call
+ * after attention at src/models/qwen_text.cpp:312 and src/models/h3.cpp:366), the dense BF16 GEMM gemm_dense
+ * (src/kernels/gemm.metal:251-296) behind it.
+ *
+ *   y[r][c] = sum_j w[c][j] * bf16(x[r][j])   (f32 accumulate), r < t, c < n, j < k
+ *
+ * mako_gemm_args is GemmArgs (gemm.metal:18-22, src/mtl/gemm.cpp:13-15) field for field: row_bytes is the weight
+ * row's bytes (2 k for BF16), ldy / ldx the row strides of y / x in elements (0: n / k). w bf16 [n][k]; y f32
+ * [t][ldy]. x_dtype MAKO_BF16: x is bf16 [t][ldx], e.g. the attention output written in bf16 by mako_attn_fwd (no
+ * conversion pass); MAKO_F32: x is f32 [t][ldx] and its rounding to bf16 (to_bf16, gemm.metal:676-681) happens in
+ * the GEMM's loads. split (f32 x only): Runtime's bf16_split_ (src/gpu/runtime.cpp:184-203; set by the Qwen encoders,
+ * src/models/qwen_text.cpp:271): the rounding's remainder bf16(x - bf16(x)) goes through the GEMM too and adds into
+ * y. k a multiple of 64 (the reference's "BF16 {k}x{n}: k must be a multiple of 64"); w and x 16-byte aligned, ldx a
+ * multiple of 8 elements.
+ */
+typedef struct mako_gemm_args {
+    uint32_t t, k, n, row_bytes;
+    uint32_t ldy, ldx;
+} mako_gemm_args;
+
+int mako_proj_bf16(const mako_gemm_args* a, int x_dtype, int split, const void* w, const void* x, float* y,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,7 +16,7 @@ U32_MAX = 0xFFFFFFFF
 # Every symbol include/mako_attn.h declares.
 EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
            "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode", "mako_heads",
-           "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots")
+           "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots", "mako_proj_bf16")
 
 
 class AttnArgs(ctypes.Structure):
@@ -52,6 +52,10 @@ class IdxDotArgs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("heads", "dim", "pools", "stride")]
 
 
+class GemmArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("t", "k", "n", "row_bytes", "ldy", "ldx")]
+
+
 class MakoError(RuntimeError):
     def __init__(self, code, msg):
         super().__init__(f"[{code}] {msg}")
@@ -84,8 +88,10 @@ def lib():
         L.mako_attn_gather_scores.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
         L.mako_attn_gather_pv.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
         L.mako_idx_dots.argtypes = [ctypes.POINTER(IdxDotArgs), U32, P, P, P, P]
+        L.mako_proj_bf16.argtypes = [ctypes.POINTER(GemmArgs), I, I, P, P, P, P]
         for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode", "mako_heads",
-                     "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots"):
+                     "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots",
+                     "mako_proj_bf16"):
             getattr(L, name).restype = I
         _lib = L
     return _lib
@@ -219,3 +225,9 @@ def idx_dots(q, pooled, dots, *, tokens, heads, dim, pools, stride, stream=None)
     [tokens][heads][stride]."""
     a = IdxDotArgs(heads, dim, pools, stride)
     _check(lib().mako_idx_dots(ctypes.byref(a), tokens, _ptr(q), _ptr(pooled), _ptr(dots), _stream(stream)))
+
+
+def proj_bf16(w, x, y, *, t, k, n, ldx=0, ldy=0, split=0, stream=None):
+    """mako_proj_bf16: w bfloat16 [n][k], x float32 or bfloat16 [t][ldx], y float32 [t][ldy]."""
+    a = GemmArgs(t, k, n, 2 * k, ldy, ldx)
+    _check(lib().mako_proj_bf16(ctypes.byref(a), dtype_code(x), split, _ptr(w), _ptr(x), _ptr(y), _stream(stream)))

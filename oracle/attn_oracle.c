@@ -8,6 +8,7 @@
  *   4 k and v swapped in the scores      5 cube_topk ties to the larger   6 sparse dense rows ignore valid
  *   7 heads: the second value of a rotated pair takes v c - u s          8 heads: the norm divides by the sum
  *   9 gathered lists read entries up to stride, not count[t]            10 probabilities not rounded to half
+ *  11 proj: x not rounded to bf16 before the product                    12 proj: the weight read as w[k][n]
  */
 #include "attn_oracle.h"
 
@@ -742,5 +743,63 @@ int oracle_idx_dots(uint32_t heads, uint32_t dim, uint32_t pools, uint32_t strid
                     acc += (double)q[((size_t)t * heads + h) * dim + d] * pooled[(size_t)pl * dim + d];
                 dots[((size_t)t * heads + h) * stride + pl] = acc;
             }
+    return 0;
+}
+
+/* ---- the output projection (Runtime::proj, BF16 weights) --------------------------------------------------------- */
+
+static double bf16_bits_to_double(uint16_t b)
+{
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+int oracle_proj_bf16(uint32_t t, uint32_t k, uint32_t n, uint32_t ldx, uint32_t ldy, int x_dtype, int split,
+                     const uint16_t* w, const void* x, double* y)
+{
+    if (x_dtype != ORACLE_F32 && x_dtype != ORACLE_BF16)
+        return 1;
+    double* hi = malloc(sizeof(double) * k);
+    double* lo = malloc(sizeof(double) * k);
+    if (!hi || !lo) {
+        free(hi);
+        free(lo);
+        return 2;
+    }
+    for (uint32_t r = 0; r < t; ++r) {
+        for (uint32_t j = 0; j < k; ++j) {
+            lo[j] = 0.0;
+            if (x_dtype == ORACLE_BF16) {
+                hi[j] = bf16_bits_to_double(((const uint16_t*)x)[(size_t)r * ldx + j]);
+                continue;
+            }
+            const float f = ((const float*)x)[(size_t)r * ldx + j];
+#if ORACLE_MUTANT == 11
+            hi[j] = f;
+            (void)split;
+#else
+            const uint16_t hb = oracle_f32_to_bf16(f); /* to_bf16 (gemm.metal:680) */
+            hi[j] = bf16_bits_to_double(hb);
+            if (split) /* bf16_lo: bfloat(x - float(hi)) (ops.metal:428) */
+                lo[j] = bf16_bits_to_double(oracle_f32_to_bf16(f - (float)hi[j]));
+#endif
+        }
+        for (uint32_t c = 0; c < n; ++c) {
+            double acc = 0.0;
+            for (uint32_t j = 0; j < k; ++j) {
+#if ORACLE_MUTANT == 12
+                const double wv = bf16_bits_to_double(w[((size_t)j * n + c) % ((size_t)n * k)]);
+#else
+                const double wv = bf16_bits_to_double(w[(size_t)c * k + j]);
+#endif
+                acc += wv * (hi[j] + lo[j]);
+            }
+            y[(size_t)r * ldy + c] = acc;
+        }
+    }
+    free(hi);
+    free(lo);
     return 0;
 }

@@ -24,6 +24,10 @@
  *                       - attn_pv, attn_gather_scores, attn_gather_pv and idx_dots (src/kernels/gemm.metal:683-870):
  *                         probabilities rounded to half before the product (gemm.metal:711, 822-827), gathered rows
  *                         past count[t] as zeros (:767-774, :830-837), the split ranges of :700 and :811-812.
+ *   oracle_proj_bf16    - Runtime::proj with BF16 weights (src/gpu/runtime.cpp:164-205): to_bf16 of the activations
+ *                         (src/kernels/gemm.metal:676-681), gemm_dense's y[t][n] = sum_k W[n][k] x[t][k]
+ *                         (gemm.metal:251-280), and with bf16_split_ the remainder bf16(x - bf16(x)) through the same
+ *                         product, added (src/kernels/ops.metal:421-437; runtime.cpp:184-203).
  *   oracle_heads        - the tile producers heads_half, heads_clear, heads_norm_half and heads_partial
  *                         (src/kernels/ops.metal:21-52, 376-407, 587-620): slice, RMS norm times w
  *                         (x / sqrt(mean(x^2) + eps)), rotation of pairs (u, v) -> (u c - v s, v c + u s),
@@ -147,6 +151,11 @@ int oracle_gather_pv(uint32_t heads, uint32_t dim, uint32_t stride, uint32_t spl
  * f32 [pools][dim]. */
 int oracle_idx_dots(uint32_t heads, uint32_t dim, uint32_t pools, uint32_t stride, uint32_t tokens, const float* q,
                     const float* pooled, double* dots);
+
+/* Runtime::proj with BF16 weights (src/gpu/runtime.cpp:164-205): y [t][ldy] (columns < n written) from w bf16 bits
+ * [n][k] and x [t][ldx], f32 (rounded to bf16 first, plus the remainder's product when split) or bf16 bits. */
+int oracle_proj_bf16(uint32_t t, uint32_t k, uint32_t n, uint32_t ldx, uint32_t ldy, int x_dtype, int split,
+                     const uint16_t* w, const void* x, double* y);
 
 void oracle_lse_merge(uint32_t n, uint32_t dim, const double* o_i, const double* lse_i, double* o, double* lse);
 

@@ -66,6 +66,7 @@ def lib(mutant=None):
         L.oracle_gather_scores.argtypes = [U32, U32, U32, U32, P, P, P, P, P]
         L.oracle_gather_pv.argtypes = [U32, U32, U32, U32, U32, P, P, P, P, P]
         L.oracle_idx_dots.argtypes = [U32, U32, U32, U32, U32, P, P, P]
+        L.oracle_proj_bf16.argtypes = [U32, U32, U32, U32, U32, I, I, P, P, P]
         L.oracle_lse_merge.argtypes = [U32, U32, P, P, P, P]
         L.oracle_lse_merge.restype = None
         L.oracle_f32_to_f16.argtypes = [F]
@@ -319,6 +320,22 @@ def idx_dots(q, pooled, *, heads, dim, pools, stride, tokens, dots=None, mutant=
     dots = np.ascontiguousarray(dots, np.float64)
     lib(mutant).oracle_idx_dots(heads, dim, pools, stride, tokens, _p(q), _p(pooled), _p(dots))
     return dots
+
+
+def proj_bf16(x, w, *, t, k, n, ldx=0, ldy=0, x_dtype=F32, split=0, y=None, mutant=None):
+    """Runtime::proj with BF16 weights (src/gpu/runtime.cpp:164-205): w bfloat16 bits [n][k], x float32 [t][ldx]
+    (x_dtype F32) or bfloat16 bits (BF16). Returns y float64 [t][ldy]; columns past n as passed in (zeros)."""
+    ldx, ldy = ldx or k, ldy or n
+    x = np.ascontiguousarray(x, np.float32 if x_dtype == F32 else np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    assert x.size >= (t - 1) * ldx + k if t else True
+    assert w.size >= n * k
+    if y is None:
+        y = np.zeros((t, ldy), np.float64)
+    y = np.ascontiguousarray(y, np.float64)
+    if lib(mutant).oracle_proj_bf16(t, k, n, ldx, ldy, x_dtype, split, _p(w), _p(x), _p(y)):
+        raise ValueError("oracle_proj_bf16: bad arguments")
+    return y
 
 
 def to_f16_bits(x):

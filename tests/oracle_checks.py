@@ -21,6 +21,9 @@ planted mistake), so the same checks both pass on the oracle and are shown to fa
                    from count[t] on are 0; gather_pv with the identity list equals attn_pv at per keys a split, and
                    a one-hot p lands in split s // per; idx_dots is numpy's float64 q pooled^T, columns past pools
                    untouched
+  proj           - y is torch's bf16 rounding of x times w^T (float64); w = I gives bf16(x) exactly, and with split
+                   bf16(x) + bf16(x - bf16(x)); split brings y within 2^-15 sum|terms| of x w^T; bf16 input is
+                   used as is; strided x and y rows, columns past n untouched
 """
 import glob
 import os
@@ -443,5 +446,43 @@ def check_gather(mutant=None):
     return not msgs, "; ".join(msgs)
 
 
+def check_proj(mutant=None):
+    import torch
+
+    rng = _rng(31)
+    msgs = []
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+    T, K, N = 5, 128, 96
+    x = (rng.standard_normal((T, K)) * 3).astype(np.float32)
+    w = O.to_bf16_bits(rng.standard_normal((N, K)) * 0.1)
+    wf = O.bits_to_f32(w, O.BF16).astype(np.float64)
+    y = O.proj_bf16(x, w, t=T, k=K, n=N, mutant=mutant)
+    if not _close(y, bf(x).astype(np.float64) @ wf.T, 1e-12):
+        msgs.append("proj is not bf16(x) w^T")
+    eye = O.to_bf16_bits(np.eye(K))
+    y = O.proj_bf16(x, eye, t=T, k=K, n=K, mutant=mutant)
+    if not np.array_equal(y, bf(x).astype(np.float64)):
+        msgs.append("proj with w = I is not bf16(x)")
+    y = O.proj_bf16(x, eye, t=T, k=K, n=K, split=1, mutant=mutant)
+    hi = bf(x)
+    if not np.array_equal(y, hi.astype(np.float64) + bf(x - hi).astype(np.float64)):
+        msgs.append("proj split with w = I is not bf16(x) + bf16(x - bf16(x))")
+    exact = x.astype(np.float64) @ wf.T
+    mag = np.abs(x).astype(np.float64) @ np.abs(wf).T
+    y = O.proj_bf16(x, w, t=T, k=K, n=N, split=1, mutant=mutant)
+    if not (np.abs(y - exact) <= 2.0 ** -15 * mag).all():
+        msgs.append("proj split is not within 2^-15 of x w^T")
+    xb = O.to_bf16_bits(x)
+    y = O.proj_bf16(xb, w, t=T, k=K, n=N, x_dtype=O.BF16, mutant=mutant)
+    if not _close(y, O.bits_to_f32(xb, O.BF16).astype(np.float64) @ wf.T, 1e-12):
+        msgs.append("proj with bf16 x is not x w^T")
+    xs = np.zeros((T, K + 64), np.float32)
+    xs[:, :K] = x
+    y = O.proj_bf16(xs, w, t=T, k=K, n=N, ldx=K + 64, ldy=N + 8, y=np.full((T, N + 8), 5.0), mutant=mutant)
+    if not _close(y[:, :N], bf(x).astype(np.float64) @ wf.T, 1e-12) or not (y[:, N:] == 5.0).all():
+        msgs.append("proj with strided rows reads or writes the wrong elements")
+    return not msgs, "; ".join(msgs)
+
+
 ALL_CHECKS = [check_goldens, check_closed_forms, check_invariants, check_sparse, check_cube_select,
-              check_decode_and_merge, check_heads, check_gather]
+              check_decode_and_merge, check_heads, check_gather, check_proj]

@@ -193,3 +193,33 @@ def test_gather_helpers_empty_is_a_no_op(fn, kw):
     """No keys or no tokens: nothing to launch, the call succeeds (no GPU needed)."""
     rc, err = gather_rc(fn, **kw)
     assert rc == M.OK, err
+
+
+def proj_rc(**kw):
+    a = dict(t=4096, k=4096, n=4096, row_bytes=8192, ldy=0, ldx=0)
+    a.update(kw.pop("args", {}))
+    args = M.GemmArgs(*[a[f] for f, _ in M.GemmArgs._fields_])
+    rc = M.lib().mako_proj_bf16(ctypes.byref(args), kw.pop("x_dtype", M.BF16), kw.pop("split", 0),
+                                kw.pop("w", FAKE), kw.pop("x", FAKE), kw.pop("y", FAKE), None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(args=dict(k=4000, row_bytes=8000)), M.EINVAL, "BF16 4000x4096: k must be a multiple of 64"),  # runtime.cpp:180
+    (dict(x_dtype=M.F16), M.EUNSUPPORTED, "activations of type 1"),
+    (dict(args=dict(row_bytes=4096)), M.EINVAL, "not 4096"),
+    (dict(split=1), M.EINVAL, "split needs f32"),
+    (dict(args=dict(ldx=2048)), M.EINVAL, "shorter"),
+    (dict(args=dict(ldx=4100)), M.EINVAL, "ldx a multiple of 8"),
+    (dict(x=ctypes.c_void_p(FAKE.value + 8)), M.EINVAL, "16-byte aligned"),
+    (dict(args=dict(t=1 << 20, ldx=8192)), M.EINVAL, "exceed 2^32"),
+    (dict(w=None), M.EINVAL, "null"),
+])
+def test_proj_refuses(kw, code, msg):
+    rc, err = proj_rc(**kw)
+    assert rc == code and msg in err, (rc, err)
+
+
+def test_proj_no_rows_is_a_no_op():
+    rc, err = proj_rc(args=dict(t=0))
+    assert rc == M.OK, err

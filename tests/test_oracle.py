@@ -47,7 +47,8 @@ MUTANTS = {1: "mask off by one", 2: "GQA map h % kv_heads", 3: "lse without the 
            4: "k and v swapped in the scores", 5: "cube_topk ties to the larger index",
            6: "sparse dense rows ignore valid", 7: "heads rotation sign of the second value",
            8: "heads norm divides by the sum", 9: "gathered lists read past count",
-           10: "probabilities not rounded to half"}
+           10: "probabilities not rounded to half", 11: "proj x not rounded to bf16",
+           12: "proj weight transposed"}
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS), ids=lambda m: MUTANTS[m].replace(" ", "_"))
