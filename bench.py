@@ -6,8 +6,8 @@ D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only 
 (4 * D * S (S + 1) / 2 * 32). Beside it: batch-16 decode against a contiguous f16 KV cache (contexts drawn
 uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
 S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s, the head tiles of the prefill step
-(fp32 rows to normed, rotated bf16 tiles) in GB/s, and the split-K / gathered latent-cache helpers of a sparse latent
-decode, each against its own roof. Inputs are synthetic N(0, 1), resident in
+(fp32 rows to normed, rotated bf16 tiles) in GB/s, the split-K / gathered latent-cache helpers of a sparse latent
+decode, each against its own roof, and the output projection after attention (Qwen3-8B o_proj) in TFLOP/s. Inputs are synthetic N(0, 1), resident in
 HBM before the timed region. `value` and ms_per_step come from --steps back-to-back launches bracketed by HIP
 events on the launch stream, after --warmup untimed ones; the roofline's `achieved` divides by the mean of each
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
@@ -320,6 +320,11 @@ def bench_proj(torch, M, steps, warmup):
         out[name] = {"ms": round(ms, 4), "kernel_ms": round(kms, 4), "flop": flop,
                      "tflops": round(flop / (kms * 1e-3) / 1e12, 1),
                      "frac": round(flop / (kms * 1e-3) / 1e12 / PEAK_TFLOPS, 4)}
+    # For scale only: the vendor library on the same shape (torch.matmul on bf16, f32 accumulate, bf16 output)
+    yb = torch.empty((t, n), dtype=torch.bfloat16, device="cuda")
+    wt = w.t()
+    ms, kms = time_launches(torch, lambda: torch.matmul(xb, wt, out=yb), steps, warmup)
+    out["vendor_library_bf16_out"] = {"kernel_ms": round(kms, 4), "tflops": round(2.0 * t * k * n / (kms * 1e-3) / 1e12, 1)}
     return out
 
 
@@ -377,6 +382,7 @@ def main():
     spa = bench_sparse(torch, M, args.steps, args.warmup)
     hds = bench_heads(torch, M, args.steps, args.warmup)
     gat = bench_gather(torch, M, args.steps, args.warmup)
+    prj = bench_proj(torch, M, max(1, args.steps // 2), args.warmup)
     line = {
         "metric": "attn prefill TFLOP/s (Qwen3-8B shape, seq 4096) + decode KV HBM GB/s, 1 GPU",
         "value": round(pre["tflops"], 2),
@@ -417,6 +423,14 @@ def main():
         "latent_decode": {name: {"kernel_ms": v["kernel_ms"], "gbps": v["gbps"], "tflops": v["tflops"],
                                  "bound": v["bound"], "frac": v["frac"]} for name, v in gat.items()},
     }
+    line["output_projection"] = {
+        "value": prj["bf16_x"]["tflops"], "unit": "TFLOP/s", "kernel_ms": prj["bf16_x"]["kernel_ms"],
+        "bound": "mfma", "frac": prj["bf16_x"]["frac"],
+        "f32_rows": {k: prj["f32_x"][k] for k in ("kernel_ms", "tflops", "frac")},
+        "f32_rows_bf16_split": {k: prj["f32_x_split"][k] for k in ("kernel_ms", "tflops", "frac")},
+        "vendor_library_bf16_out_tflops": prj["vendor_library_bf16_out"]["tflops"],
+        "config": {"workload": "Qwen3-8B o_proj after a 4096-token prefill: 4096 x 4096 bf16 weights over the "
+                               "attention's bf16 rows [4096][32 * 128], f32 output"}}
     line["latent_decode"]["config"] = {"workload": "sparse latent decode helpers: 65536-row cache of 512-wide f16 "
                                                    "latent rows, 64 tokens x 64 heads over lists of 2048 (scores, "
                                                    "then P V in one split), attn_pv of 64 heads over 32768 keys in "

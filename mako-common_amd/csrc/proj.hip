@@ -8,7 +8,7 @@
 // output and 64 MB of operands). A workgroup of 4 waves computes a BM x 256 tile of y (BM = 256; 128 with split),
 // each wave a (BM / 2) x 128 block as 32 x 32 MFMA blocks (v_mfma_f32_32x32x16_bf16) accumulating in f32.
 // 64-wide K chunks of x rows and w rows go through LDS, two buffers with one barrier a chunk; the next chunk waits in
-// registers while the current one is multiplied. Both operands are K-contiguous rows, so every 16-byte run of a row
+// registers while the current one is multiplied, and is stored, and the one after fetched, behind the first MFMAs. Both operands are K-contiguous rows, so every 16-byte run of a row
 // is one MFMA operand (8 consecutive k). LDS rows are 128 bytes; the 16-byte run c of row r sits at position
 // c ^ ((r / 2) % 8), so the 16 lanes of a ds_read_b128 (16 consecutive rows, one run) and of a ds_write_b128 (two
 // rows, eight runs) hit 64 distinct banks. f32 activations are rounded to bf16 (to nearest even) as they are
@@ -124,30 +124,54 @@ __global__ __launch_bounds__(256, 1) void proj_tiles(const ProjParams a)
         for (int bj = 0; bj < 4; ++bj)
             acc[bi][bj] = f32x16{};
     const uint32_t ra = (w >> 1) * (BM / 2), rb = (w & 1) * 128;  // this wave's first x row and w row in the tile
-    auto mma = [&](int b) __attribute__((always_inline)) {
+    struct Frag {
+        bf16x8 x[MB], xl[SPLIT ? MB : 1], w[4];
+    };
+    auto read = [&](Frag& f, int b, int kk) __attribute__((always_inline)) {
+        const uint32_t rn = 2 * kk + g;
         #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const uint32_t rn = 2 * kk + g;
-            bf16x8 xa[MB], xl[MB], wb[4];
-            #pragma unroll
-            for (int bi = 0; bi < MB; ++bi) {
-                const uint32_t p = lds_pos(ra + 32 * bi + c32, rn);
-                xa[bi] = *reinterpret_cast<const bf16x8*>(as[b] + p);
-                if (SPLIT)
-                    xl[bi] = *reinterpret_cast<const bf16x8*>(al[b] + p);
-            }
-            #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
-                wb[bj] = *reinterpret_cast<const bf16x8*>(bs[b] + lds_pos(rb + 32 * bj + c32, rn));
-            #pragma unroll
-            for (int bi = 0; bi < MB; ++bi)
-                #pragma unroll
-                for (int bj = 0; bj < 4; ++bj) {
-                    acc[bi][bj] = Elem<__bf16>::mfma32(xa[bi], wb[bj], acc[bi][bj]);
-                    if (SPLIT)
-                        acc[bi][bj] = Elem<__bf16>::mfma32(xl[bi], wb[bj], acc[bi][bj]);
-                }
+        for (int bi = 0; bi < MB; ++bi) {
+            const uint32_t p = lds_pos(ra + 32 * bi + c32, rn);
+            f.x[bi] = *reinterpret_cast<const bf16x8*>(as[b] + p);
+            if (SPLIT)
+                f.xl[bi] = *reinterpret_cast<const bf16x8*>(al[b] + p);
         }
+        #pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+            f.w[bj] = *reinterpret_cast<const bf16x8*>(bs[b] + lds_pos(rb + 32 * bj + c32, rn));
+    };
+    auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
+        #pragma unroll
+        for (int bi = 0; bi < MB; ++bi)
+            #pragma unroll
+            for (int bj = 0; bj < 4; ++bj) {
+                acc[bi][bj] = Elem<__bf16>::mfma32(f.x[bi], f.w[bj], acc[bi][bj]);
+                if (SPLIT)
+                    acc[bi][bj] = Elem<__bf16>::mfma32(f.xl[bi], f.w[bj], acc[bi][bj]);
+            }
+    };
+    // One K chunk out of buffer b: the operands of step kk + 1 are read while step kk's MFMAs run, and between(kk)
+    // (the staging of a later chunk) is issued behind step kk's MFMAs.
+    // sched_barrier keeps each read group ahead of the MFMAs it overlaps (the scheduler otherwise sinks the reads to
+    // their first use and the MFMAs wait for LDS).
+    auto chunk = [&](int b, auto between) __attribute__((always_inline)) {
+        Frag f0, f1;
+        read(f0, b, 0);
+        read(f1, b, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(f0);
+        between(0);
+        __builtin_amdgcn_sched_barrier(0);
+        read(f0, b, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(f1);
+        between(1);
+        __builtin_amdgcn_sched_barrier(0);
+        read(f1, b, 3);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(f0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(f1);
     };
     const uint32_t nk = a.k / kBK;
     Stage st;
@@ -156,15 +180,27 @@ __global__ __launch_bounds__(256, 1) void proj_tiles(const ProjParams a)
     if (nk > 1)
         fetch(st, kBK);
     __syncthreads();
-    for (uint32_t j = 0; j < nk; ++j) {
+    uint32_t j = 0;
+    for (; j + 2 < nk; ++j) {  // chunk j + 1 goes to the other buffer (last read before the previous barrier)
         const int b = j & 1;
-        mma(b);
-        if (j + 1 < nk)
-            put(st, b ^ 1);  // buffer b ^ 1 was last read before the previous barrier
-        if (j + 2 < nk)
-            fetch(st, (j + 2) * kBK);
+        chunk(b, [&](int kk) __attribute__((always_inline)) {
+            if (kk == 0)
+                put(st, b ^ 1);
+            else
+                fetch(st, (j + 2) * kBK);
+        });
         __syncthreads();
     }
+    if (j + 1 < nk) {
+        const int b = j & 1;
+        chunk(b, [&](int kk) __attribute__((always_inline)) {
+            if (kk == 0)
+                put(st, b ^ 1);
+        });
+        __syncthreads();
+        ++j;
+    }
+    chunk(j & 1, [](int) {});
     // acc[bi][bj] register r of lane (c32, g): row t0 + ra + 32 bi + 8 (r / 4) + 4 g + r % 4, column n0 + rb + 32 bj + c32
     #pragma unroll
     for (int bj = 0; bj < 4; ++bj) {
@@ -173,6 +209,154 @@ __global__ __launch_bounds__(256, 1) void proj_tiles(const ProjParams a)
             continue;
         #pragma unroll
         for (int bi = 0; bi < MB; ++bi)
+            #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = t0 + ra + 32 * bi + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (row < a.t)
+                    a.y[(size_t)row * a.ldy + c] = acc[bi][bj][r];
+            }
+    }
+}
+
+// bf16 activations: both operands go global -> LDS by the LDS DMA (global_load_lds_dwordx4: lane l of a wave writes
+// 16 bytes at the wave's LDS base + 16 l, from any address of its choosing), with no register staging, through a
+// ring of four 32-wide K stages (128 KB); a stage is refilled three chunks ahead. LDS rows are 64 bytes here: run c of
+// row r sits at position c ^ ((r / 4) % 4), so the 16 lanes of a ds_read_b128 (16 consecutive rows, one run) hit 64
+// distinct banks; a DMA instruction writes 16 rows (1 KB), lane l taking row l / 4 at position l % 4.
+constexpr int kDK = 32, kStages = 4;
+
+__device__ __forceinline__ uint32_t dpos(uint32_t row, uint32_t run) { return row * kDK + ((run ^ ((row >> 2) & 3u)) << 3); }
+
+// s_waitcnt vmcnt(n) (this wave's DMA of all but the last n / 8 chunks issued is in LDS), then the workgroup barrier.
+// The compiler's own barrier would also wait for the chunks still in flight.
+template <int N>
+__device__ __forceinline__ void dma_barrier()
+{
+    if constexpr (N == 24)
+        asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 16)
+        asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 8)
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__global__ __launch_bounds__(256, 1) void proj_dma(const ProjParams a)
+{
+    __shared__ __attribute__((aligned(16))) __bf16 as[kStages][kBN * kDK];
+    __shared__ __attribute__((aligned(16))) __bf16 bs[kStages][kBN * kDK];
+    uint32_t tm, tn;
+    if (!tile_of(a, tm, tn))
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, c32 = lane & 31;
+    const uint32_t t0 = tm * kBN, n0 = tn * kBN;
+    const __bf16* x = static_cast<const __bf16*>(a.x);
+    // DMA: wave w moves tile rows 64 w .. 64 w + 63 of both operands, four instructions of 16 rows each
+    uint32_t xo[4], wo[4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = 64 * w + 16 * i + (lane >> 2), run = (lane & 3) ^ ((row >> 2) & 3);
+        xo[i] = min(t0 + row, a.t - 1) * a.ldx + 8 * run;
+        wo[i] = min(n0 + row, a.n - 1) * a.k + 8 * run;
+    }
+    // The DMA is issued as inline asm: the compiler, seeing the builtin, waits for every DMA in flight before any
+    // LDS read (it cannot tell the stages apart), which would leave nothing in flight. Here the only waits are
+    // dma_barrier's, which count this wave's DMA instructions (8 a chunk).
+    const uint32_t wl = __builtin_amdgcn_readfirstlane(64 * w * kDK * 2);  // this wave's first row, LDS byte offset
+    auto dma = [&](const __bf16* src, const __bf16* lds) __attribute__((always_inline)) {
+        const uint32_t base = (uint32_t)(uintptr_t)lds;
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src) : "memory");
+    };
+    auto issue = [&](uint32_t c) __attribute__((always_inline)) {
+        const uint32_t s = c & (kStages - 1), k0 = c * kDK;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dma(x + (size_t)xo[i] + k0, reinterpret_cast<const __bf16*>(reinterpret_cast<const char*>(as[s]) + wl) + 16 * i * kDK);
+            dma(a.w + (size_t)wo[i] + k0, reinterpret_cast<const __bf16*>(reinterpret_cast<const char*>(bs[s]) + wl) + 16 * i * kDK);
+        }
+    };
+    f32x16 acc[4][4];
+    #pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+        #pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+            acc[bi][bj] = f32x16{};
+    const uint32_t ra = (w >> 1) * 128, rb = (w & 1) * 128;
+    struct Frag {
+        bf16x8 x[4], w[4];
+    };
+    auto read = [&](Frag& f, uint32_t s, int kk) __attribute__((always_inline)) {
+        const uint32_t rn = 2 * kk + g;
+        #pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+            f.x[bi] = *reinterpret_cast<const bf16x8*>(as[s] + dpos(ra + 32 * bi + c32, rn));
+        #pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+            f.w[bj] = *reinterpret_cast<const bf16x8*>(bs[s] + dpos(rb + 32 * bj + c32, rn));
+    };
+    auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
+        #pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+            #pragma unroll
+            for (int bj = 0; bj < 4; ++bj)
+                acc[bi][bj] = Elem<__bf16>::mfma32(f.x[bi], f.w[bj], acc[bi][bj]);
+    };
+    // Software-pipelined by one K step across the barrier: the barrier that admits chunk j + 1 sits between the
+    // two MFMA steps of chunk j, so the first step's operands of chunk j + 1 are read while chunk j's second step
+    // runs. At that barrier every wave has its chunk-j operands in registers, so stage j % 4 is free and takes
+    // chunk j + 4.
+    const uint32_t nk = a.k / kDK;
+    for (uint32_t c = 0; c < kStages && c < nk; ++c)
+        issue(c);
+    Frag fa, fb;
+    if (nk > 3)
+        dma_barrier<24>();
+    else if (nk > 2)
+        dma_barrier<16>();
+    else
+        dma_barrier<8>();  // nk >= 2 (k a multiple of 64)
+    read(fa, 0, 0);
+    read(fb, 0, 1);
+    uint32_t j = 0;
+    for (; j + 4 < nk; ++j) {  // steady: chunks j + 2 .. j + 3 may be in flight at the barrier
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_barrier<16>();
+        issue(j + 4);
+        read(fa, (j + 1) & (kStages - 1), 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fb);
+        __builtin_amdgcn_sched_barrier(0);
+        read(fb, (j + 1) & (kStages - 1), 1);
+    }
+    for (; j + 1 < nk; ++j) {  // the last chunks: nothing more to issue
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa);
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + 3 < nk)
+            dma_barrier<16>();
+        else if (j + 2 < nk)
+            dma_barrier<8>();
+        else
+            dma_barrier<0>();
+        read(fa, (j + 1) & (kStages - 1), 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fb);
+        __builtin_amdgcn_sched_barrier(0);
+        read(fb, (j + 1) & (kStages - 1), 1);
+    }
+    mfmas(fa);
+    mfmas(fb);
+    // acc[bi][bj] register r of lane (c32, g): row t0 + ra + 32 bi + 8 (r / 4) + 4 g + r % 4, column n0 + rb + 32 bj + c32
+    #pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+        const uint32_t c = n0 + rb + 32 * bj + c32;
+        if (c >= a.n)
+            continue;
+        #pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
             #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t row = t0 + ra + 32 * bi + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -225,8 +409,13 @@ extern "C" int mako_proj_bf16(const mako_gemm_args* a, int x_dtype, int split, c
         return ok();
     ProjParams p{static_cast<const __bf16*>(w), x, y, a->t, a->k, a->n, ldy, ldx, 0, 0, 0, 0};
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (x_dtype == MAKO_BF16)
-        launch_proj<256, false, false>(p, s);
+    if (x_dtype == MAKO_BF16) {
+        p.tiles_m = (p.t + kBN - 1) / kBN;
+        p.tiles_n = (p.n + kBN - 1) / kBN;
+        p.tiles = p.tiles_m * p.tiles_n;
+        p.per_xcd = (p.tiles + 7) / 8;
+        hipLaunchKernelGGL(proj_dma, dim3(8 * p.per_xcd), dim3(256), 0, s, p);
+    }
     else if (!split)
         launch_proj<256, true, false>(p, s);
     else

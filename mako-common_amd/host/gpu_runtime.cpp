@@ -1,6 +1,7 @@
 #include "gpu_runtime.hpp"
 
 #include <algorithm>
+#include <cstdio>
 #include <stdexcept>
 
 #include "mako_attn.h"
@@ -177,6 +178,22 @@ void Runtime::check(int status)
 {
     if (status != MAKO_OK)
         throw std::runtime_error(mako_last_error());
+}
+
+void Runtime::proj(Encoder*& enc, const Weight& w, Buffer* x, uint64_t x_off, Buffer* y, uint64_t y_off, uint32_t T,
+                   uint32_t ldy, bool x_bf16)
+{
+    if (w.k % 64) {  // the reference's message (src/gpu/runtime.cpp:179-180)
+        char msg[96];
+        std::snprintf(msg, sizeof msg, "BF16 %ux%u: k must be a multiple of 64", w.k, w.n);
+        throw std::runtime_error(msg);
+    }
+    const mako_gemm_args a{T, w.k, w.n, 2 * w.k, ldy, 0};
+    before(enc);
+    check(mako_proj_bf16(&a, x_bf16 ? MAKO_BF16 : MAKO_F32, bf16_split_ && !x_bf16 ? 1 : 0,
+                         static_cast<const char*>(w.buf->ptr) + w.off, static_cast<const char*>(x->ptr) + x_off,
+                         reinterpret_cast<float*>(static_cast<char*>(y->ptr) + y_off), enc->stream));
+    after(enc, bf16_split_ && !x_bf16 ? "proj BF16 split" : "proj BF16");
 }
 
 }  // namespace mako::gpu

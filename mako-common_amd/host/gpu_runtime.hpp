@@ -74,6 +74,21 @@ protected:
     // Turns a nonzero C ABI status into std::runtime_error carrying the library's message.
     static void check(int status);
 
+    // A BF16 weight matrix as proj() reads it (the reference's Tensor of type BF16 with dims {k, n}): n rows of k
+    // bf16 values, `off` bytes into buf.
+    struct Weight {
+        Buffer* buf = nullptr;
+        uint64_t off = 0;
+        uint32_t k = 0, n = 0;
+    };
+    // y[t] = W x[t] for T tokens, the BF16 branch of the reference's proj (src/gpu/runtime.cpp:164-205): x rows of k
+    // f32 values at x_off bytes (bf16 rows when x_bf16, e.g. attention output written in bf16), y f32 rows ldy
+    // apart (0: n) at y_off bytes; with bf16_split_ the rounding's remainder goes through the product too. Throws
+    // "BF16 {k}x{n}: k must be a multiple of 64" as the reference does.
+    void proj(Encoder*& enc, const Weight& w, Buffer* x, uint64_t x_off, Buffer* y, uint64_t y_off, uint32_t T,
+              uint32_t ldy = 0, bool x_bf16 = false);
+    bool bf16_split_ = false;
+
     int device_ = 0;
     Telemetry tel_ = Telemetry::off;
     Encoder enc_;

@@ -8,7 +8,10 @@
 // * the refusal of a head width the reference refuses (src/models/runtime.cpp:266-267);
 // * heads_partial with the call H3::block makes (src/models/h3.cpp:348: heads of 128, the first 96 values
 //   rotated, RMS norm, the cube row map), heads() with rotation and the padding cleared
-//   (src/models/qwen_text.cpp:308), and the refusal of heads_partial's odd rotation (src/models/runtime.cpp:249).
+//   (src/models/qwen_text.cpp:308), and the refusal of heads_partial's odd rotation (src/models/runtime.cpp:249);
+// * proj() with BF16 weights after attention (src/models/qwen_text.cpp:312): f32 rows, the bf16 split the Qwen
+//   encoders turn on (src/models/qwen_text.cpp:271), bf16 rows, a y row stride, and the refusal of k = 96
+//   (src/gpu/runtime.cpp:179-180); within the f32 summation bound 2 k 2^-24 sum|terms| (4 k with the split).
 // Tolerance: every element within 2e-3 + 1e-2 |ref|; LSE within 1e-3; head tiles within one f16 ulp.
 //   attn_test
 #include <hip/hip_runtime_api.h>
@@ -33,6 +36,9 @@ public:
     using TransformerRuntime::attention_decode;
     using TransformerRuntime::heads;
     using TransformerRuntime::heads_partial;
+    using TransformerRuntime::proj;
+    using TransformerRuntime::Weight;
+    using TransformerRuntime::bf16_split_;
     using TransformerRuntime::encoder;
     using TransformerRuntime::finish;
     using TransformerRuntime::scratch;
@@ -252,6 +258,59 @@ int main()
             threw = std::string(e.what()) == "heads_partial: heads of 128 with 95 rotated";
         }
         check(threw, "heads_partial refuses an odd rotation");
+    }
+    // The output projection after attention: proj() with BF16 weights (f32 rows, the split, bf16 rows).
+    {
+        const uint32_t T = 200, K = 512, N = 384, ldy = 400;
+        std::vector<uint16_t> w(size_t(N) * K), xb16(size_t(T) * K);
+        std::vector<float> x(size_t(T) * K), xa(x.size());
+        std::vector<uint16_t> wa(w.size()), xba(xb16.size());
+        for (size_t i = 0; i < w.size(); ++i) {
+            w[i] = oracle_f32_to_bf16(float(0.05 * normal()));
+            wa[i] = w[i] & 0x7fff;
+        }
+        for (size_t i = 0; i < x.size(); ++i) {
+            x[i] = float(3.0 * normal());
+            xa[i] = std::fabs(x[i]);
+            xb16[i] = oracle_f32_to_bf16(x[i]);
+            xba[i] = xb16[i] & 0x7fff;
+        }
+        auto wb = put(h, "w", w), xf = put(h, "x", x), xh = put(h, "xb", xb16);
+        auto yb = h.scratch("y", size_t(T) * ldy * 4);
+        const Harness::Weight W{wb, 0, K, N};
+        auto run = [&](bool split, bool bf16_in, const char* what) {
+            h.bf16_split_ = split;
+            auto* enc = h.encoder();
+            h.proj(enc, W, bf16_in ? xh : xf, 0, yb, 0, T, ldy, bf16_in);
+            h.finish(enc);
+            h.bf16_split_ = false;
+            std::vector<double> want(size_t(T) * ldy, 0.0), mag(size_t(T) * ldy, 0.0);
+            const int dt = bf16_in ? ORACLE_BF16 : ORACLE_F32;
+            oracle_proj_bf16(T, K, N, K, ldy, dt, split, w.data(), bf16_in ? (const void*)xb16.data() : x.data(),
+                             want.data());
+            oracle_proj_bf16(T, K, N, K, ldy, dt, split, wa.data(), bf16_in ? (const void*)xba.data() : xa.data(),
+                             mag.data());
+            const std::vector<float> got = get<float>(yb, want.size());
+            uint64_t bad = 0;
+            for (uint32_t t = 0; t < T; ++t)
+                for (uint32_t c = 0; c < N; ++c) {
+                    const size_t i = size_t(t) * ldy + c;
+                    bad += !(std::fabs(got[i] - want[i]) <= (split ? 4.0 : 2.0) * K * 0x1p-24 * mag[i] + 1e-30);
+                }
+            check(bad == 0, std::string(what) + ": " + std::to_string(bad) + " elements past the summation bound");
+        };
+        run(false, false, "proj, f32 rows");
+        run(true, false, "proj, f32 rows with the bf16 split");
+        run(false, true, "proj, bf16 rows");
+        bool threw = false;
+        auto* enc = h.encoder();
+        try {
+            h.proj(enc, Harness::Weight{wb, 0, 96, N}, xf, 0, yb, 0, T);
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()) == "BF16 96x384: k must be a multiple of 64";
+        }
+        h.finish(enc);
+        check(threw, "proj refuses k = 96");
     }
     for (const auto& kt : h.kernel_times())
         std::printf("  %-20s %3u launches %8.3f ms\n", kt.kernel.c_str(), kt.count, kt.ms);
