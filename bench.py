@@ -13,7 +13,7 @@ events on the launch stream, after --warmup untimed ones; the roofline's `achiev
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
 a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,gather,proj,copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,gather,proj,scan,copy]
 """
 import argparse
 import json
@@ -328,6 +328,31 @@ def bench_proj(torch, M, steps, warmup):
     return out
 
 
+def bench_scan(torch, M, steps, warmup):
+    """The gated delta rule (kda_scan) at the shape of Qwen3.5's linear-attention layers: 32 heads of 128 over 4096
+    tokens, f32, q and k unit-norm per head, g a log-decay in [-0.5, 0], beta in (0, 1), the state zeroed before
+    each call. VALU work: 896 flops a (token, head, state row) (the decay, and three 128-term fused multiply-add
+    sums); the roofline is the vector f32 peak (157.3 TFLOP/s counts packed FP32, which these kernels do not use:
+    78.6 without it)."""
+    T, H, D = 4096, 32, 128
+    gen = torch.Generator(device="cuda").manual_seed(459)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    q = unit(torch.randn((T, H, D), generator=gen, device="cuda")).reshape(T, H * D).contiguous()
+    k = unit(torch.randn((T, H, D), generator=gen, device="cuda")).reshape(T, H * D).contiguous()
+    v = torch.randn((T, H * D), generator=gen, device="cuda")
+    g = -0.5 * torch.rand((T, H * D), generator=gen, device="cuda")
+    beta = torch.rand((T, H), generator=gen, device="cuda") * 0.9 + 0.05
+    state = torch.zeros((H, D, D), device="cuda")
+    o = torch.empty((T, H * D), device="cuda")
+    ms, kms = time_launches(torch, lambda: M.kda_scan(q, k, v, g, beta, state, o, tokens=T, heads=H), steps, warmup)
+    flop = 896.0 * T * H * D
+    nbytes = 4.0 * T * H * D * 5 + 4.0 * T * H + 2 * 4.0 * H * D * D
+    return {"ms": round(ms, 4), "kernel_ms": round(kms, 4), "flop": flop, "bytes": nbytes,
+            "tflops": round(flop / (kms * 1e-3) / 1e12, 2), "gbps": round(nbytes / (kms * 1e-3) / 1e9, 1),
+            "frac_of_157": round(flop / (kms * 1e-3) / 1e12 / 157.3, 4),
+            "frac_of_78_6_unpacked": round(flop / (kms * 1e-3) / 1e12 / 78.6, 4)}
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the reference point that scales the HBM byte counters."""
     n = 256 << 20
@@ -344,7 +369,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, gather, proj, copy")
+                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, gather, proj, scan, copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -367,6 +392,7 @@ def main():
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
               "proj": lambda: bench_proj(torch, M, args.steps, args.warmup),
+              "scan": lambda: bench_scan(torch, M, args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps, args.warmup)}
         for leg in args.only.split(","):
             if leg not in fn:

@@ -236,6 +236,25 @@ typedef struct mako_gemm_args {
 int mako_proj_bf16(const mako_gemm_args* a, int x_dtype, int split, const void* w, const void* x, float* y,
                    void* stream);
 
+/*
+ * The gated delta rule with a decay per channel: kda_scan (src/kernels/ops.metal:459-519), run by the linear-
+ * attention layers that sit beside attention in Qwen3.5's encoder (src/models/qwen_text.cpp:332-391). Per head h,
+ * with S the head's state (stored transposed, state[h][j][i] = S[i][j], head_dim x head_dim f32) and, for each token
+ * t in order,
+ *   S[i][:] *= exp(g[t][i]);  delta[j] = (v[t][j] - sum_i S[i][j] k[t][i]) * beta[t][h]
+ *   S[i][j] += k[t][i] * delta[j];  o[t][j] = sum_i S[i][j] q[t][i] / sqrt(head_dim)
+ * q, k, v at t * qkv_stride + h * head_dim, g and o at t * inner + h * head_dim, beta at t * heads + h (all f32).
+ * state is read at the start and holds the state after the last token at the end; when snap is nonzero the state
+ * after `snap` tokens is also written to snap_state (the reference's rollback snapshot). mako_scan_args is ScanArgs
+ * (ops.metal:459-466) field for field; head_dim must be 128, as in the reference.
+ */
+typedef struct mako_scan_args {
+    uint32_t head_dim, tokens, qkv_stride, inner, heads, snap;
+} mako_scan_args;
+
+int mako_kda_scan(const mako_scan_args* a, const float* q, const float* k, const float* v, const float* g,
+                  const float* beta, float* state, float* o, float* snap_state, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,7 +16,8 @@ U32_MAX = 0xFFFFFFFF
 # Every symbol include/mako_attn.h declares.
 EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
            "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode", "mako_heads",
-           "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots", "mako_proj_bf16")
+           "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots", "mako_proj_bf16",
+           "mako_kda_scan")
 
 
 class AttnArgs(ctypes.Structure):
@@ -56,6 +57,10 @@ class GemmArgs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("t", "k", "n", "row_bytes", "ldy", "ldx")]
 
 
+class ScanArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("head_dim", "tokens", "qkv_stride", "inner", "heads", "snap")]
+
+
 class MakoError(RuntimeError):
     def __init__(self, code, msg):
         super().__init__(f"[{code}] {msg}")
@@ -89,9 +94,10 @@ def lib():
         L.mako_attn_gather_pv.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
         L.mako_idx_dots.argtypes = [ctypes.POINTER(IdxDotArgs), U32, P, P, P, P]
         L.mako_proj_bf16.argtypes = [ctypes.POINTER(GemmArgs), I, I, P, P, P, P]
+        L.mako_kda_scan.argtypes = [ctypes.POINTER(ScanArgs)] + [P] * 9
         for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode", "mako_heads",
                      "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots",
-                     "mako_proj_bf16"):
+                     "mako_proj_bf16", "mako_kda_scan"):
             getattr(L, name).restype = I
         _lib = L
     return _lib
@@ -231,3 +237,12 @@ def proj_bf16(w, x, y, *, t, k, n, ldx=0, ldy=0, split=0, stream=None):
     """mako_proj_bf16: w bfloat16 [n][k], x float32 or bfloat16 [t][ldx], y float32 [t][ldy]."""
     a = GemmArgs(t, k, n, 2 * k, ldy, ldx)
     _check(lib().mako_proj_bf16(ctypes.byref(a), dtype_code(x), split, _ptr(w), _ptr(x), _ptr(y), _stream(stream)))
+
+
+def kda_scan(q, k, v, g, beta, state, o, *, tokens, heads, qkv_stride=None, inner=None, snap=0, snap_state=None,
+             head_dim=128, stream=None):
+    """mako_kda_scan: float32 q, k, v rows qkv_stride apart, g and o rows inner apart, beta [tokens][heads], state
+    [heads][head_dim][head_dim] (transposed, updated in place)."""
+    a = ScanArgs(head_dim, tokens, qkv_stride or heads * head_dim, inner or heads * head_dim, heads, snap)
+    _check(lib().mako_kda_scan(ctypes.byref(a), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state), _ptr(o),
+                               _ptr(snap_state), _stream(stream)))

@@ -9,6 +9,7 @@
  *   7 heads: the second value of a rotated pair takes v c - u s          8 heads: the norm divides by the sum
  *   9 gathered lists read entries up to stride, not count[t]            10 probabilities not rounded to half
  *  11 proj: x not rounded to bf16 before the product                    12 proj: the weight read as w[k][n]
+ *  13 kda_scan: the read of S k before the decay                          14 kda_scan: beta not applied
  */
 #include "attn_oracle.h"
 
@@ -801,5 +802,63 @@ int oracle_proj_bf16(uint32_t t, uint32_t k, uint32_t n, uint32_t ldx, uint32_t 
     }
     free(hi);
     free(lo);
+    return 0;
+}
+
+/* ---- the gated delta rule (kda_scan) ---------------------------------------------------------------------------- */
+
+int oracle_kda_scan(uint32_t head_dim, uint32_t tokens, uint32_t qkv_stride, uint32_t inner, uint32_t heads,
+                    uint32_t snap, const float* q, const float* k, const float* v, const float* g, const float* beta,
+                    double* state, double* o, double* snap_state)
+{
+    const uint32_t D = head_dim;
+    if (!D || (snap && !snap_state) || snap > tokens)
+        return 1;
+    double* eg = malloc(sizeof(double) * D);
+    if (!eg)
+        return 2;
+    const double scale = 1.0 / sqrt((double)D);
+    for (uint32_t h = 0; h < heads; ++h) {
+        double* M = state + (size_t)h * D * D; /* M[j][i] = S[i][j] */
+        for (uint32_t t = 0; t < tokens; ++t) {
+            const float* qt = q + (size_t)t * qkv_stride + (size_t)h * D;
+            const float* kt = k + (size_t)t * qkv_stride + (size_t)h * D;
+            const float* vt = v + (size_t)t * qkv_stride + (size_t)h * D;
+            const float* gt = g + (size_t)t * inner + (size_t)h * D;
+#if ORACLE_MUTANT == 14
+            const double b = 1.0;
+            (void)beta;
+#else
+            const double b = beta[(size_t)t * heads + h];
+#endif
+            for (uint32_t i = 0; i < D; ++i)
+                eg[i] = exp((double)gt[i]);
+            for (uint32_t j = 0; j < D; ++j) {
+                double* Mj = M + (size_t)j * D;
+                double sum = 0.0;
+#if ORACLE_MUTANT == 13
+                for (uint32_t i = 0; i < D; ++i)
+                    sum += Mj[i] * kt[i];
+                for (uint32_t i = 0; i < D; ++i)
+                    Mj[i] *= eg[i];
+#else
+                for (uint32_t i = 0; i < D; ++i) {
+                    Mj[i] *= eg[i];             /* S[i][:] *= exp(g[i]) (ops.metal:496) */
+                    sum += Mj[i] * kt[i];       /* sum_i S[i][j] k[i] (:497) */
+                }
+#endif
+                const double delta = ((double)vt[j] - sum) * b; /* (:501) */
+                double out = 0.0;
+                for (uint32_t i = 0; i < D; ++i) {
+                    Mj[i] += kt[i] * delta;     /* (:504) */
+                    out += Mj[i] * qt[i];       /* (:505) */
+                }
+                o[(size_t)t * inner + (size_t)h * D + j] = out * scale;
+            }
+            if (t + 1 == snap)
+                memcpy(snap_state + (size_t)h * D * D, M, sizeof(double) * D * D);
+        }
+    }
+    free(eg);
     return 0;
 }

@@ -28,6 +28,9 @@
  *                         (src/kernels/gemm.metal:676-681), gemm_dense's y[t][n] = sum_k W[n][k] x[t][k]
  *                         (gemm.metal:251-280), and with bf16_split_ the remainder bf16(x - bf16(x)) through the same
  *                         product, added (src/kernels/ops.metal:421-437; runtime.cpp:184-203).
+ *   oracle_kda_scan     - the gated delta rule with a decay per channel (src/kernels/ops.metal:459-519): per head,
+ *                         S[i][:] *= exp(g[i]); delta[j] = (v[j] - sum_i S[i][j] k[i]) beta; S[i][j] += k[i] delta[j];
+ *                         o[j] = sum_i S[i][j] q[i] / sqrt(head_dim), token after token.
  *   oracle_heads        - the tile producers heads_half, heads_clear, heads_norm_half and heads_partial
  *                         (src/kernels/ops.metal:21-52, 376-407, 587-620): slice, RMS norm times w
  *                         (x / sqrt(mean(x^2) + eps)), rotation of pairs (u, v) -> (u c - v s, v c + u s),
@@ -156,6 +159,13 @@ int oracle_idx_dots(uint32_t heads, uint32_t dim, uint32_t pools, uint32_t strid
  * [n][k] and x [t][ldx], f32 (rounded to bf16 first, plus the remainder's product when split) or bf16 bits. */
 int oracle_proj_bf16(uint32_t t, uint32_t k, uint32_t n, uint32_t ldx, uint32_t ldy, int x_dtype, int split,
                      const uint16_t* w, const void* x, double* y);
+
+/* kda_scan (src/kernels/ops.metal:459-519): state double [heads][head_dim][head_dim], transposed as the reference
+ * stores it (state[h][j][i] = S[i][j]), read and updated in place; o double at t * inner + h * head_dim; snap_state
+ * (may be NULL when snap is 0) the state after `snap` tokens. */
+int oracle_kda_scan(uint32_t head_dim, uint32_t tokens, uint32_t qkv_stride, uint32_t inner, uint32_t heads,
+                    uint32_t snap, const float* q, const float* k, const float* v, const float* g, const float* beta,
+                    double* state, double* o, double* snap_state);
 
 void oracle_lse_merge(uint32_t n, uint32_t dim, const double* o_i, const double* lse_i, double* o, double* lse);
 

@@ -67,6 +67,7 @@ def lib(mutant=None):
         L.oracle_gather_pv.argtypes = [U32, U32, U32, U32, U32, P, P, P, P, P]
         L.oracle_idx_dots.argtypes = [U32, U32, U32, U32, U32, P, P, P]
         L.oracle_proj_bf16.argtypes = [U32, U32, U32, U32, U32, I, I, P, P, P]
+        L.oracle_kda_scan.argtypes = [U32, U32, U32, U32, U32, U32, P, P, P, P, P, P, P, P]
         L.oracle_lse_merge.argtypes = [U32, U32, P, P, P, P]
         L.oracle_lse_merge.restype = None
         L.oracle_f32_to_f16.argtypes = [F]
@@ -336,6 +337,30 @@ def proj_bf16(x, w, *, t, k, n, ldx=0, ldy=0, x_dtype=F32, split=0, y=None, muta
     if lib(mutant).oracle_proj_bf16(t, k, n, ldx, ldy, x_dtype, split, _p(w), _p(x), _p(y)):
         raise ValueError("oracle_proj_bf16: bad arguments")
     return y
+
+
+def kda_scan(q, k, v, g, beta, state=None, *, tokens, heads, qkv_stride=None, inner=None, snap=0, head_dim=128,
+             o=None, mutant=None):
+    """kda_scan (src/kernels/ops.metal:459-519): q, k, v float32 rows qkv_stride apart, g rows inner apart, beta
+    [tokens][heads]; state float64 [heads][head_dim][head_dim] (transposed, zeros by default). Returns (o float64
+    rows inner apart, the final state, the state after `snap` tokens or None)."""
+    D = head_dim
+    qkv_stride = qkv_stride or heads * D
+    inner = inner or heads * D
+    q, k, v, g, beta = (np.ascontiguousarray(a, np.float32) for a in (q, k, v, g, beta))
+    for a_, ld in ((q, qkv_stride), (k, qkv_stride), (v, qkv_stride), (g, inner)):
+        assert a_.size >= (tokens - 1) * ld + heads * D if tokens else True
+    assert beta.size >= tokens * heads
+    state = np.zeros((heads, D, D)) if state is None else np.array(state, np.float64, copy=True)
+    state = np.ascontiguousarray(state, np.float64)
+    if o is None:
+        o = np.zeros((tokens, inner), np.float64)
+    o = np.ascontiguousarray(o, np.float64)
+    snap_state = np.zeros((heads, D, D)) if snap else None
+    if lib(mutant).oracle_kda_scan(D, tokens, qkv_stride, inner, heads, snap, _p(q), _p(k), _p(v), _p(g), _p(beta),
+                                   _p(state), _p(o), _p(snap_state)):
+        raise ValueError("oracle_kda_scan: bad arguments")
+    return o, state, snap_state
 
 
 def to_f16_bits(x):

@@ -24,6 +24,11 @@ planted mistake), so the same checks both pass on the oracle and are shown to fa
   proj           - y is torch's bf16 rounding of x times w^T (float64); w = I gives bf16(x) exactly, and with split
                    bf16(x) + bf16(x - bf16(x)); split brings y within 2^-15 sum|terms| of x w^T; bf16 input is
                    used as is; strided x and y rows, columns past n untouched
+  kda_scan       - from a zero state one token gives o = (k.q) beta v / sqrt(D); with beta = 0 the state only decays
+                   (numpy's exp of the summed g times the initial state, and o from it); orthonormal keys with g = 0,
+                   beta = 1 are recalled exactly (delta rule), a key written twice keeps the second value; full decay
+                   (g = -60) forgets the state before the token's read; two calls carrying the state equal one; the
+                   snapshot equals the state of a call that stops there; heads in strided rows run independently
 """
 import glob
 import os
@@ -484,5 +489,87 @@ def check_proj(mutant=None):
     return not msgs, "; ".join(msgs)
 
 
+def check_kda(mutant=None):
+    rng = _rng(459)
+    msgs = []
+    D = 128
+    sq = np.sqrt(D)
+    unit = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)
+    # one token from a zero state
+    q, k, v = rng.standard_normal((3, 1, D)).astype(np.float32)
+    g = rng.uniform(-1, 0, (1, D)).astype(np.float32)
+    beta = np.array([[0.7]], np.float32)
+    o, st, _ = O.kda_scan(q, k, v, g, beta, tokens=1, heads=1, mutant=mutant)
+    want = float(np.dot(k[0].astype(np.float64), q[0])) * float(beta[0, 0]) * v[0].astype(np.float64) / sq
+    if not _close(o[0], want, 1e-9):
+        msgs.append("kda one token from zero state is not (k.q) beta v / sqrt(D)")
+    # beta = 0: pure decay of a given state
+    T = 6
+    S0 = rng.standard_normal((1, D, D))
+    q = rng.standard_normal((T, D)).astype(np.float32)
+    k = rng.standard_normal((T, D)).astype(np.float32)
+    v = rng.standard_normal((T, D)).astype(np.float32)
+    g = rng.uniform(-0.5, 0, (T, D)).astype(np.float32)
+    o, st, _ = O.kda_scan(q, k, v, g, np.zeros((T, 1), np.float32), S0, tokens=T, heads=1, mutant=mutant)
+    cum = np.cumsum(g.astype(np.float64), 0)
+    ok = _close(st[0], S0[0] * np.exp(cum[-1])[None, :], 1e-9)
+    for t in range(T):
+        ok &= _close(o[t], (S0[0] * np.exp(cum[t])[None, :]) @ q[t].astype(np.float64) / sq, 1e-9)
+    if not ok:
+        msgs.append("kda with beta = 0 is not the decayed initial state")
+    # exact recall of orthonormal keys (g = 0, beta = 1), then reads (beta = 0) with q = k_b
+    n = 5
+    Q, _ = np.linalg.qr(rng.standard_normal((D, D)))
+    keys = Q[:n].astype(np.float32)
+    vals = rng.standard_normal((n, D)).astype(np.float32)
+    kk = np.concatenate([keys, np.zeros((n, D), np.float32)])
+    qq = np.concatenate([np.zeros((n, D), np.float32), keys])
+    vv = np.concatenate([vals, np.zeros((n, D), np.float32)])
+    bb = np.concatenate([np.ones((n, 1)), np.zeros((n, 1))]).astype(np.float32)
+    o, _, _ = O.kda_scan(qq, kk, vv, np.zeros((2 * n, D), np.float32), bb, tokens=2 * n, heads=1, mutant=mutant)
+    if not _close(o[n:], vals.astype(np.float64) / sq, 1e-6):
+        msgs.append("kda does not recall orthonormal keys exactly")
+    # the same key twice: the second value replaces the first
+    k1 = unit(rng.standard_normal(D)).astype(np.float32)
+    v1, v2 = rng.standard_normal((2, D)).astype(np.float32)
+    o, _, _ = O.kda_scan(np.stack([k1 * 0, k1 * 0, k1]), np.stack([k1, k1, k1 * 0]), np.stack([v1, v2, v1 * 0]),
+                         np.zeros((3, D), np.float32), np.array([[1], [1], [0]], np.float32), tokens=3, heads=1,
+                         mutant=mutant)
+    if not _close(o[2], v2.astype(np.float64) / sq, 1e-6):
+        msgs.append("kda does not overwrite a key written twice")
+    # full decay: g = -60 forgets the state before the token's read
+    o, _, _ = O.kda_scan(np.stack([k1 * 0, k1]), np.stack([k1, k1]), np.stack([v1, v2]),
+                         np.stack([np.zeros(D), np.full(D, -60.0)]).astype(np.float32),
+                         np.ones((2, 1), np.float32), tokens=2, heads=1, mutant=mutant)
+    if not _close(o[1], float(np.dot(k1.astype(np.float64), k1)) * v2.astype(np.float64) / sq, 1e-6):
+        msgs.append("kda full decay does not forget the state before the read")
+    # two calls carrying the state equal one call; the snapshot equals the state of a call that stops there
+    T, H = 12, 2
+    q = unit(rng.standard_normal((T, H, D))).astype(np.float32).reshape(T, H * D)
+    k = unit(rng.standard_normal((T, H, D))).astype(np.float32).reshape(T, H * D)
+    v = rng.standard_normal((T, H * D)).astype(np.float32)
+    g = rng.uniform(-0.3, 0, (T, H * D)).astype(np.float32)
+    beta = rng.uniform(0, 1, (T, H)).astype(np.float32)
+    o, st, snap = O.kda_scan(q, k, v, g, beta, tokens=T, heads=H, snap=5, mutant=mutant)
+    o1, st1, _ = O.kda_scan(q[:5], k[:5], v[:5], g[:5], beta[:5], tokens=5, heads=H, mutant=mutant)
+    o2, st2, _ = O.kda_scan(q[5:], k[5:], v[5:], g[5:], beta[5:], st1, tokens=T - 5, heads=H, mutant=mutant)
+    if not (_close(np.concatenate([o1, o2]), o, 1e-12) and _close(st2, st, 1e-12) and _close(snap, st1, 1e-12)):
+        msgs.append("kda split calls, or the snapshot, differ from one call")
+    # heads in strided rows run independently
+    ld = H * D + 64
+    pad = lambda x: np.concatenate([x, np.zeros((T, 64), np.float32)], 1)
+    oh, sth, _ = O.kda_scan(pad(q), pad(k), pad(v), pad(g), beta, tokens=T, heads=H, qkv_stride=ld, inner=ld,
+                            mutant=mutant)
+    ok = _close(oh[:, :H * D], o, 1e-12)
+    for h in range(H):
+        sl = slice(h * D, (h + 1) * D)
+        oo, ss, _ = O.kda_scan(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, h:h + 1], tokens=T, heads=1,
+                               mutant=mutant)
+        ok &= _close(oo, o[:, sl], 1e-12) and _close(ss[0], st[h], 1e-12)
+    if not ok:
+        msgs.append("kda heads are not independent of each other and of the row stride")
+    return not msgs, "; ".join(msgs)
+
+
 ALL_CHECKS = [check_goldens, check_closed_forms, check_invariants, check_sparse, check_cube_select,
-              check_decode_and_merge, check_heads, check_gather, check_proj]
+              check_decode_and_merge, check_heads, check_gather, check_proj, check_kda]

@@ -223,3 +223,26 @@ def test_proj_refuses(kw, code, msg):
 def test_proj_no_rows_is_a_no_op():
     rc, err = proj_rc(args=dict(t=0))
     assert rc == M.OK, err
+
+
+def scan_rc(**kw):
+    a = dict(head_dim=128, tokens=4096, qkv_stride=4096, inner=4096, heads=32, snap=0)
+    a.update(kw.pop("args", {}))
+    args = M.ScanArgs(*[a[f] for f, _ in M.ScanArgs._fields_])
+    ptrs = [kw.pop(n, FAKE) for n in ("q", "k", "v", "g", "beta", "state", "o", "snap_state")]
+    rc = M.lib().mako_kda_scan(ctypes.byref(args), *ptrs, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(args=dict(head_dim=64)), M.EUNSUPPORTED, "head_dim 64"),      # ops.metal:481 "head_dim must be 128"
+    (dict(args=dict(qkv_stride=2048)), M.EINVAL, "32 heads of 128"),
+    (dict(args=dict(inner=4098)), M.EINVAL, "multiples of 4"),
+    (dict(k=ctypes.c_void_p(FAKE.value + 4)), M.EINVAL, "16-byte aligned"),
+    (dict(args=dict(snap=5000)), M.EINVAL, "5000 of 4096"),
+    (dict(args=dict(snap=5), snap_state=None), M.EINVAL, "null"),
+    (dict(beta=None), M.EINVAL, "null"),
+])
+def test_kda_scan_refuses(kw, code, msg):
+    rc, err = scan_rc(**kw)
+    assert rc == code and msg in err, (rc, err)

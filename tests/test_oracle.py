@@ -48,7 +48,7 @@ MUTANTS = {1: "mask off by one", 2: "GQA map h % kv_heads", 3: "lse without the 
            6: "sparse dense rows ignore valid", 7: "heads rotation sign of the second value",
            8: "heads norm divides by the sum", 9: "gathered lists read past count",
            10: "probabilities not rounded to half", 11: "proj x not rounded to bf16",
-           12: "proj weight transposed"}
+           12: "proj weight transposed", 13: "kda read before the decay", 14: "kda beta not applied"}
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS), ids=lambda m: MUTANTS[m].replace(" ", "_"))
