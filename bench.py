@@ -7,7 +7,8 @@ D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only 
 uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
 S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s, the head tiles of the prefill step
 (fp32 rows to normed, rotated bf16 tiles) in GB/s, the split-K / gathered latent-cache helpers of a sparse latent
-decode, each against its own roof, and the output projection after attention (Qwen3-8B o_proj) in TFLOP/s. Inputs are synthetic N(0, 1), resident in
+decode, each against its own roof, the output projection after attention (Qwen3-8B o_proj) in TFLOP/s, and the
+gated delta rule of the linear-attention layers in TFLOP/s. Inputs are synthetic N(0, 1), resident in
 HBM before the timed region. `value` and ms_per_step come from --steps back-to-back launches bracketed by HIP
 events on the launch stream, after --warmup untimed ones; the roofline's `achieved` divides by the mean of each
 launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
@@ -409,6 +410,7 @@ def main():
     hds = bench_heads(torch, M, args.steps, args.warmup)
     gat = bench_gather(torch, M, args.steps, args.warmup)
     prj = bench_proj(torch, M, max(1, args.steps // 2), args.warmup)
+    scn = bench_scan(torch, M, max(1, args.steps // 4), max(1, args.warmup))
     line = {
         "metric": "attn prefill TFLOP/s (Qwen3-8B shape, seq 4096) + decode KV HBM GB/s, 1 GPU",
         "value": round(pre["tflops"], 2),
@@ -457,6 +459,10 @@ def main():
         "vendor_library_bf16_out_tflops": prj["vendor_library_bf16_out"]["tflops"],
         "config": {"workload": "Qwen3-8B o_proj after a 4096-token prefill: 4096 x 4096 bf16 weights over the "
                                "attention's bf16 rows [4096][32 * 128], f32 output"}}
+    line["linear_attention"] = {
+        "value": scn["tflops"], "unit": "TFLOP/s", "kernel_ms": scn["kernel_ms"], "bound": "valu",
+        "frac": scn["frac_of_157"], "frac_without_packed_fp32": scn["frac_of_78_6_unpacked"],
+        "config": {"workload": "gated delta rule (kda_scan), 32 heads of 128 over 4096 tokens, f32, state zeroed"}}
     line["latent_decode"]["config"] = {"workload": "sparse latent decode helpers: 65536-row cache of 512-wide f16 "
                                                    "latent rows, 64 tokens x 64 heads over lists of 2048 (scores, "
                                                    "then P V in one split), attn_pv of 64 heads over 32768 keys in "

@@ -60,6 +60,18 @@ void TransformerRuntime::heads_partial(gpu::Encoder*& enc, gpu::Buffer* x, uint3
     after(enc, "heads_partial");
 }
 
+void TransformerRuntime::kda_scan(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, gpu::Buffer* v, gpu::Buffer* g,
+                                  gpu::Buffer* beta, gpu::Buffer* state, gpu::Buffer* o, uint32_t T,
+                                  uint32_t qkv_stride, uint32_t inner, uint32_t n_heads, uint32_t snap,
+                                  gpu::Buffer* snap_state)
+{
+    const mako_scan_args a{kHeadDim, T, qkv_stride, inner, n_heads, snap};
+    auto f = [](gpu::Buffer* b) { return b ? static_cast<float*>(b->ptr) : nullptr; };
+    before(enc);
+    check(mako_kda_scan(&a, f(q), f(k), f(v), f(g), f(beta), f(state), f(o), f(snap_state), enc->stream));
+    after(enc, "kda_scan");
+}
+
 void TransformerRuntime::attention(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, gpu::Buffer* v, gpu::Buffer* o,
                                    uint32_t n_q, uint32_t q_pad, uint32_t n_k, uint32_t k_pad, uint32_t n_heads,
                                    uint32_t kv_heads, uint32_t q_pos0, uint32_t block, uint32_t dim,

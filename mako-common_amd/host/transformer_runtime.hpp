@@ -70,6 +70,13 @@ protected:
                           uint32_t width, uint32_t n_cubes, uint32_t topk, uint32_t dense0, uint32_t dense1,
                           gpu::Buffer* sel, gpu::Buffer* nsel, gpu::Buffer* valid, gpu::Buffer* map,
                           const AttnOptions& opt = {});
+    // The gated delta rule of the linear-attention layers (the reference dispatches kda_scan by name in
+    // QwenText::linear_layer, src/models/qwen_text.cpp:374-382, with ScanArgs {128, T, vw, vw, VH, 0}): q, k, v rows
+    // qkv_stride floats apart, g and o rows `inner` apart, beta [T][heads], state [heads][128][128] (transposed,
+    // updated in place), snap_state the state after `snap` tokens when snap is nonzero.
+    void kda_scan(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, gpu::Buffer* v, gpu::Buffer* g,
+                  gpu::Buffer* beta, gpu::Buffer* state, gpu::Buffer* o, uint32_t T, uint32_t qkv_stride,
+                  uint32_t inner, uint32_t heads, uint32_t snap = 0, gpu::Buffer* snap_state = nullptr);
     // One new token for each of `batch` sequences against a contiguous cache: q [batch][heads][128],
     // k and v [batch][kv_heads][cap][128], ctx_len u32 [batch] (device), o [batch][heads * 128]; split-K with the
     // partials in the Runtime-owned scratch "attn_decode". No counterpart in the reference (it decodes one sequence

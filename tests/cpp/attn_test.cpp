@@ -11,7 +11,9 @@
 //   (src/models/qwen_text.cpp:308), and the refusal of heads_partial's odd rotation (src/models/runtime.cpp:249);
 // * proj() with BF16 weights after attention (src/models/qwen_text.cpp:312): f32 rows, the bf16 split the Qwen
 //   encoders turn on (src/models/qwen_text.cpp:271), bf16 rows, a y row stride, and the refusal of k = 96
-//   (src/gpu/runtime.cpp:179-180); within the f32 summation bound 2 k 2^-24 sum|terms| (4 k with the split).
+//   (src/gpu/runtime.cpp:179-180); within the f32 summation bound 2 k 2^-24 sum|terms| (4 k with the split);
+// * kda_scan with the arguments QwenText::linear_layer passes (src/models/qwen_text.cpp:374-382: {128, T, vw, vw, VH,
+//   0}, the state zeroed), 4 heads over 100 tokens; within 2e-5 + 1e-4 |ref| of the oracle.
 // Tolerance: every element within 2e-3 + 1e-2 |ref|; LSE within 1e-3; head tiles within one f16 ulp.
 //   attn_test
 #include <hip/hip_runtime_api.h>
@@ -37,6 +39,7 @@ public:
     using TransformerRuntime::heads;
     using TransformerRuntime::heads_partial;
     using TransformerRuntime::proj;
+    using TransformerRuntime::kda_scan;
     using TransformerRuntime::Weight;
     using TransformerRuntime::bf16_split_;
     using TransformerRuntime::encoder;
@@ -311,6 +314,49 @@ int main()
         }
         h.finish(enc);
         check(threw, "proj refuses k = 96");
+    }
+    // The gated delta rule as the linear-attention layer calls it.
+    {
+        const uint32_t T = 100, VH = 4, D = 128, vw = VH * D;
+        std::vector<float> q(size_t(T) * vw), k(q.size()), v(q.size()), g(q.size()), beta(size_t(T) * VH);
+        for (uint32_t t = 0; t < T; ++t)
+            for (uint32_t hh = 0; hh < VH; ++hh) {
+                double nq = 0, nk = 0;
+                float* qr = &q[size_t(t) * vw + hh * D];
+                float* kr = &k[size_t(t) * vw + hh * D];
+                for (uint32_t i = 0; i < D; ++i) {
+                    qr[i] = float(normal());
+                    kr[i] = float(normal());
+                    nq += double(qr[i]) * qr[i];
+                    nk += double(kr[i]) * kr[i];
+                }
+                for (uint32_t i = 0; i < D; ++i) {  // unit q and k per head, as the layer's L2 norm gives them
+                    qr[i] = float(qr[i] / std::sqrt(nq));
+                    kr[i] = float(kr[i] / std::sqrt(nk));
+                }
+                beta[size_t(t) * VH + hh] = float(0.5 + 0.4 * std::tanh(normal()));
+            }
+        for (size_t i = 0; i < v.size(); ++i) {
+            v[i] = float(normal());
+            g[i] = float(-0.25 * std::fabs(normal()));
+        }
+        std::vector<float> zero(size_t(VH) * D * D, 0.0f);
+        auto qb = put(h, "kq", q), kb = put(h, "kk", k), vb = put(h, "kv", v), gb = put(h, "kg", g);
+        auto bb = put(h, "kbeta", beta), sb = put(h, "kstate", zero);
+        auto ob = h.scratch("ko", q.size() * 4);
+        auto* enc = h.encoder();
+        h.kda_scan(enc, qb, kb, vb, gb, bb, sb, ob, T, vw, vw, VH);
+        h.finish(enc);
+        std::vector<double> want_o(q.size()), want_s(zero.size(), 0.0);
+        oracle_kda_scan(D, T, vw, vw, VH, 0, q.data(), k.data(), v.data(), g.data(), beta.data(), want_s.data(),
+                        want_o.data(), nullptr);
+        const std::vector<float> got_o = get<float>(ob, want_o.size()), got_s = get<float>(sb, want_s.size());
+        uint64_t bad = 0;
+        for (size_t i = 0; i < want_o.size(); ++i)
+            bad += !(std::fabs(got_o[i] - want_o[i]) <= 2e-5 + 1e-4 * std::fabs(want_o[i]));
+        for (size_t i = 0; i < want_s.size(); ++i)
+            bad += !(std::fabs(got_s[i] - want_s[i]) <= 2e-5 + 1e-4 * std::fabs(want_s[i]));
+        check(bad == 0, "kda_scan, 4 heads over 100 tokens: " + std::to_string(bad) + " values out of tolerance");
     }
     for (const auto& kt : h.kernel_times())
         std::printf("  %-20s %3u launches %8.3f ms\n", kt.kernel.c_str(), kt.count, kt.ms);
