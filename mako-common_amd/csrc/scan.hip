@@ -5,22 +5,23 @@
 //   S[i][j] += k[i] * delta[j];  o[j] = sum_i S[i][j] q[i] / sqrt(128)
 //
 // The design is this one's own. Row j of a head's transposed state evolves on its own: it needs the token's shared
-// q, k, g and its own v[j]. A row is 16 lanes (one DPP row) of 8 values each, lane l holding channels 4l .. 4l + 3
-// and 64 + 4l .. 64 + 4l + 3, so the two sums over channels are 8 fused multiply-adds a lane and four DPP adds
-// (quad swaps, half-row and row mirrors), with no LDS and no barrier. A workgroup of 4 waves takes 16 rows of one
-// head (grid: heads x 8), so 1024 waves cover 32 heads. Tokens go through LDS in batches of 16, two buffers: the
-// workgroup stages a batch's q, k and exp(g) rows once (coalesced 16-byte loads fetched into registers while the
-// previous batch runs; the exponential computed once a channel, not once a row), its v and beta; each lane runs the
-// batch's tokens out of LDS (the lane's 8 channels are two 16-byte reads a vector, 16 lanes reading 256 contiguous
-// bytes), reading a token's operands one token ahead of the state's chain, and the batch's outputs leave as one
-// coalesced store after the next barrier. One barrier a batch.
-// Bound: the VALU (no packed FP32 here): 7 flops a channel a row a token.
+// q, k, g and its own v[j]. A row is 32 lanes of 4 values (lane l: channels 4l .. 4l + 3), so the two sums over
+// channels are 4 fused multiply-adds a lane, four v_add_f32_dpp within each 16-lane DPP row and one ds_swizzle
+// across the pair, with no barrier inside a token. A workgroup of 4 waves takes 8 rows of one head (grid: heads x
+// 16), so 32 heads make 2048 waves, two a SIMD. Tokens go through LDS in batches of 16, two buffers: the workgroup
+// stages a batch's q, k and exp(g) rows once (coalesced 16-byte loads fetched into registers while the previous
+// batch runs; the exponential computed once a channel, not once a row), its v and beta; each lane runs the batch's
+// tokens out of LDS (a vector is one 16-byte read a lane, 32 lanes reading 512 contiguous bytes), reading a token's
+// operands one token ahead of the state's chain, and the batch's outputs leave as one coalesced store after the
+// next barrier. One barrier a batch.
+// Bound: the token recurrence (a dependent chain of decay, dot product, lane reduction and update per token) and
+// the VALU (no packed FP32 here): 7 flops a channel a row a token.
 #include "device.hpp"
 
 namespace mako {
 namespace {
 
-constexpr int kD = 128, kRows = 16, kBatch = 16;
+constexpr int kD = 128, kBatch = 16;
 
 struct ScanParams {
     const float *q, *k, *v, *g, *beta;
@@ -30,7 +31,6 @@ struct ScanParams {
     uint32_t tokens, qkv_stride, inner, heads, snap;
 };
 
-// Sum over the 16 lanes of a DPP row, in every lane: xor 1 and xor 2 within quads, then the half-row and row mirrors.
 // bound_ctrl set: every source lane of these patterns is inside the row, and the compiler then folds the move into
 // the add (v_add_f32_dpp).
 template <int CTRL>
@@ -39,37 +39,48 @@ __device__ __forceinline__ float dpp(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
 }
 
-__device__ __forceinline__ float row_sum16(float x)
+// Sum over the LANES lanes of a state row, in every lane: xor 1 and xor 2 within quads, the half-row and row mirrors
+// (16 lanes), then, for 32-lane rows, lane ^ 16 by ds_swizzle (bit mode: and 0x1f, or 0, xor 0x10).
+template <int LANES>
+__device__ __forceinline__ float row_sum(float x)
 {
     x += dpp<0xb1>(x);   // quad_perm [1, 0, 3, 2]
     x += dpp<0x4e>(x);   // quad_perm [2, 3, 0, 1]
     x += dpp<0x141>(x);  // row_half_mirror
     x += dpp<0x140>(x);  // row_mirror
+    if (LANES == 32)
+        x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401f));
     return x;
 }
 
+// LANES lanes a state row, V = 128 / LANES values a lane in G = V / 4 runs of 4 channels: run r of lane l holds
+// channels 4 LANES r + 4 l .. + 3, so a run of the lanes of a row is 16 LANES contiguous bytes of a vector.
+template <int LANES>
 __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
 {
+    constexpr int V = kD / LANES, G = V / 4, ROWS = 256 / LANES;
     // two batch buffers: the next batch's rows are fetched into registers while this batch runs out of LDS
     __shared__ __attribute__((aligned(16))) float qs[2][kBatch][kD];
     __shared__ __attribute__((aligned(16))) float ks[2][kBatch][kD];
     __shared__ __attribute__((aligned(16))) float es[2][kBatch][kD];
-    __shared__ float vs[2][kBatch][kRows], bs[2][kBatch], os[2][kBatch][kRows];
-    const uint32_t tid = threadIdx.x, h = blockIdx.x, j0 = blockIdx.y * kRows, row = tid >> 4, l = tid & 15;
-    const uint32_t c0 = 4 * l, c1 = 64 + 4 * l;  // this lane's channels: c0 .. c0 + 3 and c1 .. c1 + 3
+    __shared__ float vs[2][kBatch][ROWS], bs[2][kBatch], os[2][kBatch][ROWS];
+    const uint32_t tid = threadIdx.x, h = blockIdx.x, j0 = blockIdx.y * ROWS, row = tid / LANES, l = tid % LANES;
+    uint32_t ch[G];
+    #pragma unroll
+    for (int r = 0; r < G; ++r)
+        ch[r] = 4 * LANES * r + 4 * l;
     float* mg = a.state + ((size_t)h * kD + j0 + row) * kD;
-    float m[8];
-    {
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(mg + c0), x1 = *reinterpret_cast<const f32x4*>(mg + c1);
-        for (int n = 0; n < 4; ++n) {
-            m[n] = x0[n];
-            m[4 + n] = x1[n];
-        }
+    float m[V];
+    #pragma unroll
+    for (int r = 0; r < G; ++r) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(mg + ch[r]);
+        for (int n = 0; n < 4; ++n)
+            m[4 * r + n] = x[n];
     }
     const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
     const size_t hq = (size_t)h * kD;
     // Staging of a batch: thread tid moves runs tid and tid + 256 (token run / 32, channels 4 (run % 32) ..) of q, k
-    // and g, v of (token tid / 16, row tid % 16) and beta of token tid; loads past the last token are not issued.
+    // and g, v of (token tid / ROWS, row tid % ROWS) and beta of token tid; loads past the last token are not issued.
     struct Stage {
         f32x4 q[2], k[2], g[2];
         float v, b;
@@ -86,8 +97,8 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
                 st.g[i] = *reinterpret_cast<const f32x4*>(a.g + go);
             }
         }
-        if (tid < np * kRows)
-            st.v = a.v[(size_t)(t0 + (tid >> 4)) * a.qkv_stride + hq + j0 + (tid & 15)];
+        if (tid < np * ROWS)
+            st.v = a.v[(size_t)(t0 + tid / ROWS) * a.qkv_stride + hq + j0 + tid % ROWS];
         if (tid < np)
             st.b = a.beta[(size_t)(t0 + tid) * a.heads + h];
     };
@@ -103,60 +114,67 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
                     f32x4{__expf(st.g[i][0]), __expf(st.g[i][1]), __expf(st.g[i][2]), __expf(st.g[i][3])};
             }
         }
-        if (tid < np * kRows)
-            vs[b][tid >> 4][tid & 15] = st.v;
+        if (tid < np * ROWS)
+            vs[b][tid / ROWS][tid % ROWS] = st.v;
         if (tid < np)
             bs[b][tid] = st.b;
     };
     // One token out of buffer b; the operands of the token are read before the state's chain needs them.
     struct Ops {
-        f32x4 e0, e1, k0, k1, q0, q1;
+        f32x4 e[G], k[G], q[G];
         float v, b;
     };
     auto ops = [&](Ops& x, int b, uint32_t tt) __attribute__((always_inline)) {
-        x.e0 = *reinterpret_cast<const f32x4*>(&es[b][tt][c0]);
-        x.e1 = *reinterpret_cast<const f32x4*>(&es[b][tt][c1]);
-        x.k0 = *reinterpret_cast<const f32x4*>(&ks[b][tt][c0]);
-        x.k1 = *reinterpret_cast<const f32x4*>(&ks[b][tt][c1]);
-        x.q0 = *reinterpret_cast<const f32x4*>(&qs[b][tt][c0]);
-        x.q1 = *reinterpret_cast<const f32x4*>(&qs[b][tt][c1]);
+        #pragma unroll
+        for (int r = 0; r < G; ++r) {
+            x.e[r] = *reinterpret_cast<const f32x4*>(&es[b][tt][ch[r]]);
+            x.k[r] = *reinterpret_cast<const f32x4*>(&ks[b][tt][ch[r]]);
+            x.q[r] = *reinterpret_cast<const f32x4*>(&qs[b][tt][ch[r]]);
+        }
         x.v = vs[b][tt][row];
         x.b = bs[b][tt];
     };
     auto step = [&](const Ops& x, int b, uint32_t t, uint32_t tt) __attribute__((always_inline)) {
-        const float ev[8] = {x.e0[0], x.e0[1], x.e0[2], x.e0[3], x.e1[0], x.e1[1], x.e1[2], x.e1[3]};
-        const float kv[8] = {x.k0[0], x.k0[1], x.k0[2], x.k0[3], x.k1[0], x.k1[1], x.k1[2], x.k1[3]};
-        const float qv[8] = {x.q0[0], x.q0[1], x.q0[2], x.q0[3], x.q1[0], x.q1[1], x.q1[2], x.q1[3]};
+        float ev[V], kv[V], qv[V];
+        #pragma unroll
+        for (int r = 0; r < G; ++r)
+            #pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                ev[4 * r + n] = x.e[r][n];
+                kv[4 * r + n] = x.k[r][n];
+                qv[4 * r + n] = x.q[r][n];
+            }
         float s0 = 0.0f, s1 = 0.0f;
         #pragma unroll
-        for (int n = 0; n < 4; ++n) {
+        for (int n = 0; n < V; n += 2) {
             m[n] *= ev[n];
-            m[4 + n] *= ev[4 + n];
+            m[n + 1] *= ev[n + 1];
             s0 = fmaf(m[n], kv[n], s0);
-            s1 = fmaf(m[4 + n], kv[4 + n], s1);
+            s1 = fmaf(m[n + 1], kv[n + 1], s1);
         }
-        const float d = (x.v - row_sum16(s0 + s1)) * x.b;
+        const float d = (x.v - row_sum<LANES>(s0 + s1)) * x.b;
         float u0 = 0.0f, u1 = 0.0f;
         #pragma unroll
-        for (int n = 0; n < 4; ++n) {
+        for (int n = 0; n < V; n += 2) {
             m[n] = fmaf(kv[n], d, m[n]);
-            m[4 + n] = fmaf(kv[4 + n], d, m[4 + n]);
+            m[n + 1] = fmaf(kv[n + 1], d, m[n + 1]);
             u0 = fmaf(m[n], qv[n], u0);
-            u1 = fmaf(m[4 + n], qv[4 + n], u1);
+            u1 = fmaf(m[n + 1], qv[n + 1], u1);
         }
-        const float out = row_sum16(u0 + u1);
+        const float out = row_sum<LANES>(u0 + u1);
         if (l == 0)
             os[b][tt][row] = out * scale;
         if (t + 1 == a.snap) {  // the state after `snap` tokens (uniform across the workgroup)
             float* sg = a.snap_state + ((size_t)h * kD + j0 + row) * kD;
-            *reinterpret_cast<f32x4*>(sg + c0) = f32x4{m[0], m[1], m[2], m[3]};
-            *reinterpret_cast<f32x4*>(sg + c1) = f32x4{m[4], m[5], m[6], m[7]};
+            #pragma unroll
+            for (int r = 0; r < G; ++r)
+                *reinterpret_cast<f32x4*>(sg + ch[r]) = f32x4{m[4 * r], m[4 * r + 1], m[4 * r + 2], m[4 * r + 3]};
         }
     };
     auto store_out = [&](int b, uint32_t t0) __attribute__((always_inline)) {
         const uint32_t np = min((uint32_t)kBatch, a.tokens - t0);
-        if (tid < np * kRows)
-            a.o[(size_t)(t0 + (tid >> 4)) * a.inner + hq + j0 + (tid & 15)] = os[b][tid >> 4][tid & 15];
+        if (tid < np * ROWS)
+            a.o[(size_t)(t0 + tid / ROWS) * a.inner + hq + j0 + tid % ROWS] = os[b][tid / ROWS][tid % ROWS];
     };
     if (a.tokens > 0) {
         Stage st;
@@ -189,9 +207,12 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
         }
         store_out(b ^ 1, (a.tokens - 1) / kBatch * kBatch);
     }
-    *reinterpret_cast<f32x4*>(mg + c0) = f32x4{m[0], m[1], m[2], m[3]};
-    *reinterpret_cast<f32x4*>(mg + c1) = f32x4{m[4], m[5], m[6], m[7]};
+    #pragma unroll
+    for (int r = 0; r < G; ++r)
+        *reinterpret_cast<f32x4*>(mg + ch[r]) = f32x4{m[4 * r], m[4 * r + 1], m[4 * r + 2], m[4 * r + 3]};
 }
+
+constexpr int kScanLanes = 32;  // lanes a state row: 4 values a lane, two waves a SIMD at 32 heads
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -218,6 +239,7 @@ extern "C" int mako_kda_scan(const mako_scan_args* a, const float* q, const floa
     if (a->heads > 65535u)
         return fail(MAKO_EINVAL, "kda_scan: %u heads exceed the grid", a->heads);
     ScanParams p{q, k, v, g, beta, state, o, snap_state, a->tokens, a->qkv_stride, a->inner, a->heads, a->snap};
-    hipLaunchKernelGGL(kda_scan_rows, dim3(a->heads, kD / kRows), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+    hipLaunchKernelGGL(kda_scan_rows<kScanLanes>, dim3(a->heads, kD / (256 / kScanLanes)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), p);
     return check_launch("kda_scan");
 }
