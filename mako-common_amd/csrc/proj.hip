@@ -264,9 +264,13 @@ __global__ __launch_bounds__(256, 1) void proj_dma(const ProjParams a)
     // LDS read (it cannot tell the stages apart), which would leave nothing in flight. Here the only waits are
     // dma_barrier's, which count this wave's DMA instructions (8 a chunk).
     const uint32_t wl = __builtin_amdgcn_readfirstlane(64 * w * kDK * 2);  // this wave's first row, LDS byte offset
+    // M0 (the DMA's LDS base) is listed as clobbered; nothing else in this kernel uses it.
     auto dma = [&](const __bf16* src, const __bf16* lds) __attribute__((always_inline)) {
         const uint32_t base = (uint32_t)(uintptr_t)lds;
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src) : "memory");
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src) : "memory", "m0");
+#pragma clang diagnostic pop
     };
     auto issue = [&](uint32_t c) __attribute__((always_inline)) {
         const uint32_t s = c & (kStages - 1), k0 = c * kDK;
