@@ -356,18 +356,32 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
                 st.v[i] = buffer_load16(vrs, ((2 * v_kp + i) * D + v_cc * 8) * sizeof(T));
         }
     };
+    // This lane's V^T positions in a buffer (the key pair's 8 dims), kept in registers: recomputing them beside
+    // each store cost two VALU instructions a store.
+    uint32_t vt_off[8];
+    {
+        const uint32_t key = hk + 2 * v_kp, kc = key / 8, off = key % 8;
+        #pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t d = v_cc * 8 + e;
+            vt_off[e] = d * VS + ((kc ^ vt_swz(d)) * 8) + off;
+        }
+        #pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            u32x4 u = {vt_off[e], vt_off[e + 1], vt_off[e + 2], vt_off[e + 3]};
+            settle(u);
+            for (int i = 0; i < 4; ++i)
+                vt_off[e + i] = u[i];
+        }
+    }
     auto store_half = [&](uint32_t buf, const Half& st) __attribute__((always_inline)) {
         #pragma unroll
         for (int i = 0; i < NKG; ++i)
             *reinterpret_cast<u32x4*>(&ks[buf][(hk + slot_of(k_row + GRPI * i)) * KS + k_col * 8]) = st.k[i];
         if (v_on) {
-            const uint32_t key = hk + 2 * v_kp, kc = key / 8, off = key % 8;
             #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t d = v_cc * 8 + e;
-                *reinterpret_cast<uint32_t*>(&vt[buf][d * VS + ((kc ^ vt_swz(d)) * 8) + off]) =
-                    f16_pair<T>(st.v[0], st.v[1], e);
-            }
+            for (int e = 0; e < 8; ++e)
+                *reinterpret_cast<uint32_t*>(&vt[buf][vt_off[e]]) = f16_pair<T>(st.v[0], st.v[1], e);
         }
     };
 
