@@ -81,6 +81,7 @@ GATHER = [
     (4, 64, 512, 2048, 20000, [2048, 0, 1, 1500]),  # lists of 2048 over a 20000-row latent cache
     (2, 16, 256, 100, 300, [100, 37]),              # lists that are not a multiple of 64
     (3, 7, 768, 64, 64, [64, 63, 5]),
+    (2, 64, 512, 192, 5000, [500, 191]),           # a count past the list's length reads only the list
 ]
 
 
