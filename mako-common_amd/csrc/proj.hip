@@ -308,11 +308,21 @@ __global__ __launch_bounds__(256, 1) void proj_dma(const ProjParams a)
     };
     // Software-pipelined by one K step across the barrier: the barrier that admits chunk j + 1 sits between the
     // two MFMA steps of chunk j, so the first step's operands of chunk j + 1 are read while chunk j's second step
-    // runs. At that barrier every wave has its chunk-j operands in registers, so stage j % 4 is free and takes
-    // chunk j + 4.
+    // runs, and its second step's operands while chunk j + 1's first step runs. At that barrier every wave has its
+    // chunk-j operands in registers, so stage j % 4 is free and takes chunk j + 4.
     const uint32_t nk = a.k / kDK;
     for (uint32_t c = 0; c < kStages && c < nk; ++c)
         issue(c);
+    // The 8 LDS reads of a step go out one behind each of the first 8 of the 16 MFMAs they overlap, not as a burst
+    // ahead of them.
+    auto interleave = []() __attribute__((always_inline)) {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    };
     Frag fa, fb;
     if (nk > 3)
         dma_barrier<24>();
@@ -322,36 +332,40 @@ __global__ __launch_bounds__(256, 1) void proj_dma(const ProjParams a)
         dma_barrier<8>();  // nk >= 2 (k a multiple of 64)
     read(fa, 0, 0);
     read(fb, 0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa);
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t j = 0;
     for (; j + 4 < nk; ++j) {  // steady: chunks j + 2 .. j + 3 may be in flight at the barrier
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa);
-        __builtin_amdgcn_sched_barrier(0);
         dma_barrier<16>();
         issue(j + 4);
-        read(fa, (j + 1) & (kStages - 1), 0);
         __builtin_amdgcn_sched_barrier(0);
+        read(fa, (j + 1) & (kStages - 1), 0);
         mfmas(fb);
+        interleave();
         __builtin_amdgcn_sched_barrier(0);
         read(fb, (j + 1) & (kStages - 1), 1);
+        mfmas(fa);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
     }
     for (; j + 1 < nk; ++j) {  // the last chunks: nothing more to issue
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa);
-        __builtin_amdgcn_sched_barrier(0);
         if (j + 3 < nk)
             dma_barrier<16>();
         else if (j + 2 < nk)
             dma_barrier<8>();
         else
             dma_barrier<0>();
-        read(fa, (j + 1) & (kStages - 1), 0);
         __builtin_amdgcn_sched_barrier(0);
+        read(fa, (j + 1) & (kStages - 1), 0);
         mfmas(fb);
+        interleave();
         __builtin_amdgcn_sched_barrier(0);
         read(fb, (j + 1) & (kStages - 1), 1);
+        mfmas(fa);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
     }
-    mfmas(fa);
     mfmas(fb);
     // acc[bi][bj] register r of lane (c32, g): row t0 + ra + 32 bi + 8 (r / 4) + 4 g + r % 4, column n0 + rb + 32 bj + c32
     #pragma unroll
