@@ -6,17 +6,22 @@
 //
 // The design is this one's own. Row j of a head's transposed state evolves on its own: it needs the token's shared
 // q, k, g and its own v[j]. A row is 32 lanes of 4 values (lane l: channels 4l .. 4l + 3), so the two sums over
-// channels are 4 fused multiply-adds a lane, four v_add_f32_dpp within each 16-lane DPP row and one ds_swizzle
-// across the pair, with no barrier inside a token. A workgroup of 4 waves takes 8 rows of one head (grid: heads x
-// 16), so 32 heads make 2048 waves, two a SIMD. Tokens go through LDS in batches of 16, two buffers: the workgroup
-// stages a batch's q, k and exp(g) rows once (coalesced 16-byte loads fetched into registers while the previous
-// batch runs; the exponential computed once a channel, not once a row), its v and beta; each lane runs the batch's
-// tokens out of LDS (a vector is one 16-byte read a lane, 32 lanes reading 512 contiguous bytes), reading a token's
-// operands one token ahead of the state's chain, and the batch's outputs leave as one coalesced store after the
-// next barrier. One barrier a batch.
+// channels are 4 fused multiply-adds a lane, four v_add_f32_dpp within each 16-lane DPP row and one
+// v_permlane16_swap across the pair: all VALU, no LDS round trip and no barrier inside a token. A workgroup of 4
+// waves takes 8 rows of one head (grid: heads x 16), so 32 heads make 2048 waves, two a SIMD. Tokens go through LDS
+// in batches of 16, two buffers: the workgroup stages a batch's q, k and exp(g) rows once (coalesced 16-byte loads
+// fetched into registers while the previous batch runs; the exponential computed once a channel, not once a row),
+// its v and beta; each lane runs the batch's tokens out of LDS (a vector is one 16-byte read a lane, 32 lanes
+// reading 512 contiguous bytes), reading a token's operands one token ahead of the state's chain, and the batch's
+// outputs leave as one coalesced store after the next barrier. One barrier a batch. The token loop is one basic
+// block: a token's output reduction is issued after the next token's state update (it is off the state's chain),
+// the rollback snapshot has a loop of its own for the one batch that holds it, and nothing in the loop is
+// conditional.
 // Bound: the token recurrence (a dependent chain of decay, dot product, lane reduction and update per token) and
 // the VALU (no packed FP32 here): 7 flops a channel a row a token.
 #include "device.hpp"
+
+#include <type_traits>
 
 namespace mako {
 namespace {
@@ -40,7 +45,9 @@ __device__ __forceinline__ float dpp(float v)
 }
 
 // Sum over the LANES lanes of a state row, in every lane: xor 1 and xor 2 within quads, the half-row and row mirrors
-// (16 lanes), then, for 32-lane rows, lane ^ 16 by ds_swizzle (bit mode: and 0x1f, or 0, xor 0x10).
+// (16 lanes), then, for 32-lane rows, the two 16-lane rows of each pair added by v_permlane16_swap_b32 (with both
+// operands x it returns the pair's even row and its odd row in every lane of the pair), a VALU exchange with no
+// LDS round trip.
 template <int LANES>
 __device__ __forceinline__ float row_sum(float x)
 {
@@ -48,8 +55,10 @@ __device__ __forceinline__ float row_sum(float x)
     x += dpp<0x4e>(x);   // quad_perm [2, 3, 0, 1]
     x += dpp<0x141>(x);  // row_half_mirror
     x += dpp<0x140>(x);  // row_mirror
-    if (LANES == 32)
-        x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401f));
+    if (LANES == 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false);
+        x = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
     return x;
 }
 
@@ -80,27 +89,25 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
     const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
     const size_t hq = (size_t)h * kD;
     // Staging of a batch: thread tid moves runs tid and tid + 256 (token run / 32, channels 4 (run % 32) ..) of q, k
-    // and g, v of (token tid / ROWS, row tid % ROWS) and beta of token tid; loads past the last token are not issued.
+    // and g, v of (token tid / ROWS, row tid % ROWS) and beta of token tid. Past the last token the loads read the
+    // last token again (put skips them): loads issued on every path let the compiler wait for exactly the older
+    // memory operations in the token loop, where a load under a branch made it wait for these too.
     struct Stage {
         f32x4 q[2], k[2], g[2];
         float v, b;
     };
     auto fetch = [&](Stage& st, uint32_t t0) __attribute__((always_inline)) {
-        const uint32_t np = min((uint32_t)kBatch, a.tokens - t0);
+        const uint32_t last = a.tokens - 1;
         #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const uint32_t e = tid + 256 * i, tt = e >> 5, c = 4 * (e & 31);
-            if (tt < np) {
-                const size_t qo = (size_t)(t0 + tt) * a.qkv_stride + hq + c, go = (size_t)(t0 + tt) * a.inner + hq + c;
-                st.q[i] = *reinterpret_cast<const f32x4*>(a.q + qo);
-                st.k[i] = *reinterpret_cast<const f32x4*>(a.k + qo);
-                st.g[i] = *reinterpret_cast<const f32x4*>(a.g + go);
-            }
+            const uint32_t e = tid + 256 * i, t = min(t0 + (e >> 5), last), c = 4 * (e & 31);
+            const size_t qo = (size_t)t * a.qkv_stride + hq + c, go = (size_t)t * a.inner + hq + c;
+            st.q[i] = *reinterpret_cast<const f32x4*>(a.q + qo);
+            st.k[i] = *reinterpret_cast<const f32x4*>(a.k + qo);
+            st.g[i] = *reinterpret_cast<const f32x4*>(a.g + go);
         }
-        if (tid < np * ROWS)
-            st.v = a.v[(size_t)(t0 + tid / ROWS) * a.qkv_stride + hq + j0 + tid % ROWS];
-        if (tid < np)
-            st.b = a.beta[(size_t)(t0 + tid) * a.heads + h];
+        st.v = a.v[(size_t)min(t0 + tid / ROWS, last) * a.qkv_stride + hq + j0 + tid % ROWS];
+        st.b = a.beta[(size_t)min(t0 + tid, last) * a.heads + h];
     };
     auto put = [&](const Stage& st, int b, uint32_t t0) __attribute__((always_inline)) {
         const uint32_t np = min((uint32_t)kBatch, a.tokens - t0);
@@ -134,7 +141,10 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
         x.v = vs[b][tt][row];
         x.b = bs[b][tt];
     };
-    auto step = [&](const Ops& x, int b, uint32_t t, uint32_t tt) __attribute__((always_inline)) {
+    // The state's update by one token; returns this lane's part of the token's output (its channels' terms). SNAP:
+    // the batch holds token `snap` - 1, so the state after it is copied out.
+    auto state = [&](auto SNAP_, const Ops& x, uint32_t t) __attribute__((always_inline)) {
+        constexpr bool SNAP = decltype(SNAP_)::value;
         float ev[V], kv[V], qv[V];
         #pragma unroll
         for (int r = 0; r < G; ++r)
@@ -161,15 +171,18 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
             u0 = fmaf(m[n], qv[n], u0);
             u1 = fmaf(m[n + 1], qv[n + 1], u1);
         }
-        const float out = row_sum<LANES>(u0 + u1);
-        if (l == 0)
-            os[b][tt][row] = out * scale;
-        if (t + 1 == a.snap) {  // the state after `snap` tokens (uniform across the workgroup)
+        if (SNAP && t + 1 == a.snap) {  // the state after `snap` tokens (uniform across the workgroup)
             float* sg = a.snap_state + ((size_t)h * kD + j0 + row) * kD;
             #pragma unroll
             for (int r = 0; r < G; ++r)
                 *reinterpret_cast<f32x4*>(sg + ch[r]) = f32x4{m[4 * r], m[4 * r + 1], m[4 * r + 2], m[4 * r + 3]};
         }
+        return u0 + u1;
+    };
+    // The token's output: the row's sum of the lanes' parts, into the batch's output buffer.
+    auto emit = [&](float u, int b, uint32_t tt) __attribute__((always_inline)) {
+        const float out = row_sum<LANES>(u);
+        os[b][tt][row] = out * scale;  // every lane of the row holds the same sum
     };
     auto store_out = [&](int b, uint32_t t0) __attribute__((always_inline)) {
         const uint32_t np = min((uint32_t)kBatch, a.tokens - t0);
@@ -184,23 +197,33 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
         int b = 0;
         for (uint32_t t0 = 0; t0 < a.tokens; t0 += kBatch, b ^= 1) {
             const bool more = t0 + kBatch < a.tokens;
+            // The previous batch's outputs (written before the last barrier), stored before the next batch's loads
+            // are issued: the token loop reuses the store's registers, and the wait for the store (memory
+            // operations complete in order) then leaves the loads in flight.
+            if (t0 > 0)
+                store_out(b ^ 1, t0 - kBatch);
             if (more)
                 fetch(st, t0 + kBatch);  // in flight while this batch runs
-            if (t0 > 0)
-                store_out(b ^ 1, t0 - kBatch);  // the previous batch's outputs (written before the last barrier)
             const uint32_t np = min((uint32_t)kBatch, a.tokens - t0);
-            Ops x0, x1;
-            ops(x0, b, 0);
-            uint32_t tt = 0;
-            for (; tt + 1 < np; tt += 2) {  // two tokens a trip: each token's operands read a token ahead
-                ops(x1, b, tt + 1);
-                step(x0, b, t0 + tt, tt);
-                if (tt + 2 < np)
-                    ops(x0, b, tt + 2);
-                step(x1, b, t0 + tt + 1, tt + 1);
-            }
-            if (tt < np)
-                step(x0, b, t0 + tt, tt);
+            auto tokens = [&](auto SNAP) __attribute__((always_inline)) {
+                Ops x0, x1;
+                ops(x0, b, 0);
+                uint32_t tt = 0;
+                for (; tt + 1 < np; tt += 2) {  // two tokens a trip: each token's operands read a token ahead
+                    ops(x1, b, tt + 1);
+                    const float u0 = state(SNAP, x0, t0 + tt);
+                    ops(x0, b, min(tt + 2, (uint32_t)kBatch - 1));  // (past the batch: read, not used)
+                    const float u1 = state(SNAP, x1, t0 + tt + 1);
+                    emit(u0, b, tt);  // off the state's chain: its reduction fills the next token's wait states
+                    emit(u1, b, tt + 1);
+                }
+                if (tt < np)
+                    emit(state(SNAP, x0, t0 + tt), b, tt);
+            };
+            if (a.snap > t0 && a.snap <= t0 + np)
+                tokens(std::true_type{});
+            else
+                tokens(std::false_type{});
             if (more)
                 put(st, b ^ 1, t0 + kBatch);  // buffer b ^ 1 was last read before the previous barrier
             __syncthreads();
