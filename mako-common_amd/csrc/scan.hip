@@ -5,18 +5,19 @@
 //   S[i][j] += k[i] * delta[j];  o[j] = sum_i S[i][j] q[i] / sqrt(128)
 //
 // The design is this one's own. Row j of a head's transposed state evolves on its own: it needs the token's shared
-// q, k, g and its own v[j]. A row is 32 lanes of 4 values (lane l: channels 4l .. 4l + 3), so the two sums over
-// channels are 4 fused multiply-adds a lane, four v_add_f32_dpp within each 16-lane DPP row and one
-// v_permlane16_swap across the pair: all VALU, no LDS round trip and no barrier inside a token. A workgroup of 4
-// waves takes 8 rows of one head (grid: heads x 16), so 32 heads make 2048 waves, two a SIMD. Tokens go through LDS
-// in batches of 16, two buffers: the workgroup stages a batch's q, k and exp(g) rows once (coalesced 16-byte loads
-// fetched into registers while the previous batch runs; the exponential computed once a channel, not once a row),
-// its v and beta; each lane runs the batch's tokens out of LDS (a vector is one 16-byte read a lane, 32 lanes
-// reading 512 contiguous bytes), reading a token's operands one token ahead of the state's chain, and the batch's
-// outputs leave as one coalesced store after the next barrier. One barrier a batch. The token loop is one basic
-// block: a token's output reduction is issued after the next token's state update (it is off the state's chain),
-// the rollback snapshot has a loop of its own for the one batch that holds it, and nothing in the loop is
-// conditional.
+// q, k, g and its own v[j]. A row is 16 lanes (one DPP row) of 8 values (lane l: channels 4l .. 4l + 3 and
+// 64 + 4l .. 64 + 4l + 3), so the two sums over channels are 8 fused multiply-adds a lane and four v_add_f32_dpp:
+// all VALU, no LDS round trip and no barrier inside a token. A workgroup of 4 waves takes 16 rows of one head
+// (grid: heads x 8), so 32 heads make 1024 waves, one a SIMD. (The kernel also takes 32-lane rows of 4 values, the
+// two DPP rows of a pair added by v_permlane16_swap: twice the waves, a third more instructions a token, slower.)
+// Tokens go through LDS in batches of 16, two buffers: the workgroup stages a batch's q, k and exp(g) rows once
+// (coalesced 16-byte loads fetched into registers while the previous batch runs; the exponential computed once a
+// channel, not once a row), its v and beta; each lane runs the batch's tokens out of LDS (a lane reads its runs of
+// a vector as 16-byte reads, a row's lanes reading contiguous 256-byte runs), reading a token's operands one token
+// ahead of the state's chain, and the batch's outputs leave as one coalesced store after the next barrier. One
+// barrier a batch. The token loop is one basic block: a token's output reduction is issued after the next token's
+// state update (it is off the state's chain), the rollback snapshot has a loop of its own for the one batch that
+// holds it, and nothing in the loop is conditional.
 // Bound: the token recurrence (a dependent chain of decay, dot product, lane reduction and update per token) and
 // the VALU (no packed FP32 here): 7 flops a channel a row a token.
 #include "device.hpp"
@@ -235,7 +236,7 @@ __global__ __launch_bounds__(256) void kda_scan_rows(const ScanParams a)
         *reinterpret_cast<f32x4*>(mg + ch[r]) = f32x4{m[4 * r], m[4 * r + 1], m[4 * r + 2], m[4 * r + 3]};
 }
 
-constexpr int kScanLanes = 32;  // lanes a state row: 4 values a lane, two waves a SIMD at 32 heads
+constexpr int kScanLanes = 16;  // lanes a state row: 8 values a lane, one wave a SIMD at 32 heads
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
