@@ -130,6 +130,8 @@ IDX = [
     (2, 32, 64, 129, 129),
     (3, 5, 33, 70, 80),        # odd width (one float a lane a step), part tiles of heads and pools
     (1, 1, 1, 1, 1),
+    (3, 32, 128, 700, 700),    # an odd token count on the 16-byte path (token pairs: the last one alone)
+    (1, 20, 128, 256, 260),
 ]
 
 
@@ -139,12 +141,15 @@ def test_idx_dots(case):
     rng = np.random.default_rng(pools + dim)
     q = rng.standard_normal((tokens, heads, dim)).astype(np.float32)
     pooled = rng.standard_normal((pools, dim)).astype(np.float32)
-    out = torch.full((tokens, heads, stride), SENTINEL, dtype=torch.float32, device="cuda")
+    # one more token's rows than the call covers: they must stay untouched
+    out = torch.full((tokens + 1, heads, stride), SENTINEL, dtype=torch.float32, device="cuda")
     print(f"idx_dots {case}", flush=True)
     M.idx_dots(dev(q, np.float32), dev(pooled, np.float32), out, tokens=tokens, heads=heads, dim=dim, pools=pools,
                stride=stride)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
+    assert (got[tokens] == SENTINEL).all(), "idx_dots wrote past the last token"
+    got = got[:tokens]
     want = O.idx_dots(q, pooled, heads=heads, dim=dim, pools=pools, stride=stride, tokens=tokens,
                       dots=np.full((tokens, heads, stride), SENTINEL))
     mag = O.idx_dots(np.abs(q), np.abs(pooled), heads=heads, dim=dim, pools=pools, stride=stride, tokens=tokens)
