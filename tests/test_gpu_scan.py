@@ -1,7 +1,8 @@
 """The gated delta rule (mako_kda_scan, the reference's kda_scan) on the GPU against the CPU oracle: the inputs the
 linear-attention layers feed it (q and k L2-normalised per head, v normal, g a log-decay in [-0.5, 0], beta in
-(0, 1)), a nonzero starting state, strided rows, the rollback snapshot, a batch boundary (token counts that are not
-multiples of 16), no tokens, and the Qwen3.5 shape (32 heads of 128 over 4096 tokens, four heads checked).
+(0, 1)), a nonzero starting state, strided rows, the rollback snapshot (after the first token, the last, and at a
+boundary of the kernel's 16-token batches), token counts one past and one short of a batch multiple, no tokens,
+and the Qwen3.5 shape (32 heads of 128 over 4096 tokens, four heads checked).
 
 Tolerance: the oracle runs in double; the kernel in f32 with a different summation order (8 values a lane, then a
 16-lane tree) and the hardware exponential. Every output and state element within 2e-5 + 1e-4 |ref| (the f32
@@ -62,8 +63,10 @@ def run(q, k, v, g, beta, state, *, T, H, ld=None, snap=0):
     return o.cpu().numpy(), st.cpu().numpy(), (snap_d.cpu().numpy() if snap else None)
 
 
-@pytest.mark.parametrize("T,H,ld,snap", [(200, 4, 0, 0), (37, 2, 320, 20), (1, 1, 0, 1), (16, 3, 0, 16)],
-                         ids=["t200h4", "t37h2_strided_snap20", "t1", "t16h3_snap16"])
+@pytest.mark.parametrize("T,H,ld,snap", [(200, 4, 0, 0), (37, 2, 320, 20), (1, 1, 0, 1), (16, 3, 0, 16),
+                                         (17, 2, 0, 17), (33, 1, 0, 32), (47, 3, 400, 1), (31, 2, 0, 0)],
+                         ids=["t200h4", "t37h2_strided_snap20", "t1", "t16h3_snap16", "t17h2_snap_last",
+                              "t33h1_snap_batch_edge", "t47h3_strided_snap_first", "t31h2"])
 def test_kda_scan(T, H, ld, snap):
     rng = np.random.default_rng(T * 7 + H)
     q, k, v, g, beta, state = inputs(rng, T, H, ld or None, scale_state=0.3)
