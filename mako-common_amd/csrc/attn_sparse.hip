@@ -583,6 +583,42 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
             }
     };
 
+    // The steady state's matrix phase in one stream, as in flash_fwd: Q K^T of the next pass then P V of the
+    // current one, each operand read kRing reads ahead of its MFMA (the compiler alone kept two or three).
+    auto matrix = [&](uint32_t bk, uint32_t bv) __attribute__((always_inline)) {
+        constexpr int NQ = 2 * NKK, N = NQ + 4 * NDB, kRing = 4;
+        const T* kr = &ks[bk][c32 * KS + 8 * g];
+        auto rd = [&](int i) __attribute__((always_inline)) {
+            if (i < NQ)
+                return *reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * KS + 16 * (i >> 1));
+            const int cc = (i - NQ) / NDB, db = (i - NQ) % NDB;
+            const uint32_t d = 32 * db + c32;
+            return *reinterpret_cast<const u32x4*>(&vt[bv][d * VS + (((2 * cc + g) ^ vt_swz(d)) * 8)]);
+        };
+        u32x4 ring[kRing];
+#pragma unroll
+        for (int i = 0; i < kRing; ++i)
+            ring[i] = rd(i);
+        s[0] = f32x16{};
+        s[1] = f32x16{};
+        __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);  // the first kRing LDS reads
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const u32x4 op = ring[i % kRing];
+            if (i + kRing < N)
+                ring[i % kRing] = rd(i + kRing);
+            if (i < NQ) {  // same order as qk
+                s[i & 1] = E::mfma32(__builtin_bit_cast(V8, op), qreg[i >> 1], s[i & 1]);
+            } else {  // same order as pv
+                const int cc = (i - NQ) / NDB, db = (i - NQ) % NDB;
+                oacc[db] = H::mfma32(__builtin_bit_cast(H8, op), pb(cc), oacc[db]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // this MFMA
+            if (i + kRing < N)
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // then the read kRing ahead
+        }
+    };
+
     // Prologue: passes 0 .. 2 by both groups (loads in flight together with Q's), group 1's half of pass 3.
     Half st;
     {
@@ -628,8 +664,9 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_sparse8(const SparseParams
         // matrix phase: scores of pass j + 1, P V of pass j; pass j + 1's validity flags in flight
         vflag = valid_flag(j + 1);
         __builtin_amdgcn_s_setprio(1);
-        qk(s, b1);
-        pv(b0);
+        __builtin_amdgcn_sched_barrier(0);
+        matrix(b1, b0);
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // vector phase: softmax of pass j + 1, and the staging
