@@ -136,6 +136,19 @@ int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_dtype out, c
                      size_t workspace_bytes, void* stream);
 
 /*
+ * mako_attn_decode with no workspace argument and no allocation of any kind: the split-K partials live in a
+ * static device array of MAKO_DECODE_SCRATCH_BYTES inside the library (one copy on each GPU it runs on, held
+ * until the process ends). No counterpart in the reference: it is for callers that cannot allocate device memory
+ * while they run (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * split and results as mako_attn_decode; MAKO_EWORKSPACE when the partials that split needs
+ * (mako_attn_decode_workspace(a) bytes) exceed the static array. Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (two streams, two threads) race and must be serialised by the caller.
+ */
+#define MAKO_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
+int mako_attn_decode_noalloc(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                             const void* v, const uint32_t* ctx_len, void* o, float* lse, void* stream);
+
+/*
  * Head tiles from fp32 rows: head h of token t, x[t][col0 + h * stride .. + dim), written as y row
  * [h][row0 + t][dim] in f16 (the reference's half tiles) or bf16, optionally RMS-normed (times w) and then rotated by
  * the angle table cs. One call stands for each of the reference's tile producers (src/kernels/ops.metal:11-52,

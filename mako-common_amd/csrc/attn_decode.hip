@@ -24,6 +24,7 @@
 // * Partials: the unnormalised O^T columns, the running maximum and the row sum; the merge rescales a
 //   segment's pieces to their common maximum and divides once.
 #include <algorithm>
+#include <mutex>
 
 #include "device.hpp"
 
@@ -345,6 +346,39 @@ size_t workspace_for(uint32_t n_waves, const mako_decode_args* a)
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The split-K partials of mako_attn_decode_noalloc: a file-scope device array, one copy on every GPU the library
+// runs on, held until the process ends. Its host-side name is not a device address: kernels and copies take the
+// address hipGetSymbolAddress returns for the current device (scratch_ptr).
+constexpr size_t kScratchBytes = MAKO_DECODE_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices];  // per device: the address of its copy of `scratch` (null until looked up)
+
+// The current device's copy of `scratch`, looked up once per device with that device current; null (with the
+// error recorded) when the lookup fails.
+void* scratch_ptr()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fail(MAKO_EHIP, "attention_decode_noalloc: no current device (or more than %d)", kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_dev[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            fail(MAKO_EHIP, "attention_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                 hipGetErrorString(e));
+            return nullptr;
+        }
+        scratch_dev[dev] = ptr;
+    }
+    return scratch_dev[dev];
+}
+
 }  // namespace
 }  // namespace mako
 
@@ -358,46 +392,44 @@ extern "C" size_t mako_attn_decode_workspace(const mako_decode_args* a)
     return resident ? workspace_for(waves_for(a, resident), a) : 0;
 }
 
-extern "C" int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q,
-                                const void* k, const void* v, const uint32_t* ctx_len, void* o, float* lse,
-                                void* workspace, size_t workspace_bytes, void* stream)
+namespace {
+
+// The checks both decode entry points make (what: the name in the messages).
+int check_args(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k, const void* v,
+               const uint32_t* ctx_len, const void* o, const char* what)
 {
     if (!a || !q || !k || !v || !ctx_len || !o)
-        return fail(MAKO_EINVAL, "attention_decode: a null argument");
+        return fail(MAKO_EINVAL, "%s: a null argument", what);
     if (a->dim != kD)
-        return fail(MAKO_EUNSUPPORTED, "attention_decode: heads of %u (128)", a->dim);
+        return fail(MAKO_EUNSUPPORTED, "%s: heads of %u (128)", what, a->dim);
     if (in != MAKO_F16 && in != MAKO_BF16)
-        return fail(MAKO_EUNSUPPORTED, "attention_decode: input type %d (f16 or bf16)", (int)in);
+        return fail(MAKO_EUNSUPPORTED, "%s: input type %d (f16 or bf16)", what, (int)in);
     if (out != MAKO_F32 && out != in)
-        return fail(MAKO_EUNSUPPORTED, "attention_decode: output type %d (f32 or the input's)", (int)out);
+        return fail(MAKO_EUNSUPPORTED, "%s: output type %d (f32 or the input's)", what, (int)out);
     if (!a->heads || !a->kv_heads || a->heads % a->kv_heads || a->heads / a->kv_heads > 32)
-        return fail(MAKO_EINVAL, "attention_decode: %u heads over %u kv heads (groups of at most 32)", a->heads,
-                    a->kv_heads);
+        return fail(MAKO_EINVAL, "%s: %u heads over %u kv heads (groups of at most 32)", what, a->heads, a->kv_heads);
     if (a->max_ctx > a->cap)
-        return fail(MAKO_EINVAL, "attention_decode: max_ctx %u over the cache's %u rows", a->max_ctx, a->cap);
+        return fail(MAKO_EINVAL, "%s: max_ctx %u over the cache's %u rows", what, a->max_ctx, a->cap);
     if ((uint64_t)a->cap * kD * 2 > 0x7fffffffu)
-        return fail(MAKO_EINVAL, "attention_decode: %u cache rows exceed 2 GiB a head", a->cap);
+        return fail(MAKO_EINVAL, "%s: %u cache rows exceed 2 GiB a head", what, a->cap);
     if ((uint64_t)a->batch * a->kv_heads * a->max_ctx >= (1ull << 32))
-        return fail(MAKO_EINVAL, "attention_decode: %u x %u x %u rows exceed 2^32", a->batch, a->kv_heads,
-                    a->max_ctx);
+        return fail(MAKO_EINVAL, "%s: %u x %u x %u rows exceed 2^32", what, a->batch, a->kv_heads, a->max_ctx);
     if (a->split % 64)
-        return fail(MAKO_EINVAL, "attention_decode: %u keys a split (a multiple of 64, or 0)", a->split);
+        return fail(MAKO_EINVAL, "%s: %u keys a split (a multiple of 64, or 0)", what, a->split);
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
-        return fail(MAKO_EINVAL, "attention_decode: q, k, v and o must be 16-byte aligned");
+        return fail(MAKO_EINVAL, "%s: q, k, v and o must be 16-byte aligned", what);
     if (!(a->scale > 0.0f) || a->scale == INFINITY)
-        return fail(MAKO_EINVAL, "attention_decode: scale %g (positive and finite)", (double)a->scale);
-    const uint32_t resident = resident_waves();
-    if (!resident)
-        return fail(MAKO_EHIP, "attention_decode: no device to size the split for");
-    const uint32_t n_waves = waves_for(a, resident);
-    const size_t need = workspace_for(n_waves, a);
-    if (!workspace || workspace_bytes < need || !aligned16(workspace))
-        return fail(MAKO_EWORKSPACE, "attention_decode: workspace of %zu bytes, %zu needed (16-byte aligned)",
-                    workspace_bytes, need);
-    if (a->batch == 0)
-        return ok();
-    float* part_o = static_cast<float*>(workspace);
-    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_o_bytes(n_waves, a));
+        return fail(MAKO_EINVAL, "%s: scale %g (positive and finite)", what, (double)a->scale);
+    return MAKO_OK;
+}
+
+// The split kernel and the merge on `stream`, with the partials in `ws` (at least workspace_for(n_waves, a) bytes).
+int launch_decode(const mako_decode_args* a, uint32_t n_waves, mako_dtype in, mako_dtype out, const void* q,
+                  const void* k, const void* v, const uint32_t* ctx_len, void* o, float* lse, void* ws, void* stream,
+                  const char* what)
+{
+    float* part_o = static_cast<float*>(ws);
+    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + part_o_bytes(n_waves, a));
     const DecParams p{q, k, v, ctx_len, part_o, part_ml, a->batch, a->heads, a->kv_heads, a->heads / a->kv_heads,
                       a->cap, a->max_ctx, n_waves, a->scale * kLog2e};
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -412,5 +444,52 @@ extern "C" int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_d
         hipLaunchKernelGGL(decode_merge<__bf16>, mgrid, dim3(kD), 0, s, p, static_cast<__bf16*>(o), lse);
     else
         hipLaunchKernelGGL(decode_merge<_Float16>, mgrid, dim3(kD), 0, s, p, static_cast<_Float16*>(o), lse);
-    return check_launch("attention_decode");
+    return check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q,
+                                const void* k, const void* v, const uint32_t* ctx_len, void* o, float* lse,
+                                void* workspace, size_t workspace_bytes, void* stream)
+{
+    const char* what = "attention_decode";
+    if (const int rc = check_args(a, in, out, q, k, v, ctx_len, o, what))
+        return rc;
+    const uint32_t resident = resident_waves();
+    if (!resident)
+        return fail(MAKO_EHIP, "%s: no device to size the split for", what);
+    const uint32_t n_waves = waves_for(a, resident);
+    const size_t need = workspace_for(n_waves, a);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace))
+        return fail(MAKO_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed (16-byte aligned)", what,
+                    workspace_bytes, need);
+    if (a->batch == 0)
+        return ok();
+    return launch_decode(a, n_waves, in, out, q, k, v, ctx_len, o, lse, workspace, stream, what);
+}
+
+extern "C" int mako_attn_decode_noalloc(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q,
+                                        const void* k, const void* v, const uint32_t* ctx_len, void* o, float* lse,
+                                        void* stream)
+{
+    const char* what = "attention_decode_noalloc";
+    if (const int rc = check_args(a, in, out, q, k, v, ctx_len, o, what))
+        return rc;
+    const uint32_t resident = resident_waves();
+    if (!resident)
+        return fail(MAKO_EHIP, "%s: no device to size the split for", what);
+    const uint32_t n_waves = waves_for(a, resident);
+    const size_t need = workspace_for(n_waves, a);
+    if (need > kScratchBytes)
+        return fail(MAKO_EWORKSPACE,
+                    "%s: the split-K partials need %zu bytes, over the library's static scratch of %zu bytes "
+                    "(fewer sequences, kv heads or query heads a group, or a larger split, or mako_attn_decode "
+                    "with a workspace)", what, need, kScratchBytes);
+    void* ws = scratch_ptr();
+    if (!ws)
+        return MAKO_EHIP;
+    if (a->batch == 0)
+        return ok();
+    return launch_decode(a, n_waves, in, out, q, k, v, ctx_len, o, lse, ws, stream, what);
 }

@@ -15,7 +15,8 @@ U32_MAX = 0xFFFFFFFF
 
 # Every symbol include/mako_attn.h declares.
 EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
-           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode", "mako_heads",
+           "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode",
+           "mako_attn_decode_noalloc", "mako_heads",
            "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots", "mako_proj_bf16",
            "mako_kda_scan")
 
@@ -88,6 +89,7 @@ def lib():
         L.mako_attn_decode_workspace.argtypes = [ctypes.POINTER(DecodeArgs)]
         L.mako_attn_decode_workspace.restype = SZ
         L.mako_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P, SZ, P]
+        L.mako_attn_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P]
         L.mako_heads.argtypes = [ctypes.POINTER(HeadsArgs), I, P, P, P, P, P, P]
         L.mako_attn_pv.argtypes = [ctypes.POINTER(PvArgs), P, P, P, P]
         L.mako_attn_gather_scores.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
@@ -95,7 +97,8 @@ def lib():
         L.mako_idx_dots.argtypes = [ctypes.POINTER(IdxDotArgs), U32, P, P, P, P]
         L.mako_proj_bf16.argtypes = [ctypes.POINTER(GemmArgs), I, I, P, P, P, P]
         L.mako_kda_scan.argtypes = [ctypes.POINTER(ScanArgs)] + [P] * 9
-        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode", "mako_heads",
+        for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode",
+                     "mako_attn_decode_noalloc", "mako_heads",
                      "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots",
                      "mako_proj_bf16", "mako_kda_scan"):
             getattr(L, name).restype = I
@@ -172,6 +175,15 @@ def attn_decode(a, q, k, v, ctx_len, o, workspace, *, lse=None, stream=None):
                                   _ptr(ctx_len), _ptr(o), _ptr(lse), _ptr(workspace),
                                   0 if workspace is None else workspace.numel() * workspace.element_size(),
                                   _stream(stream)))
+
+
+def attn_decode_noalloc(a, q, k, v, ctx_len, o, *, lse=None, stream=None):
+    """mako_attn_decode_noalloc: mako_attn_decode with the partials in the library's static device scratch."""
+    _check(lib().mako_attn_decode_noalloc(ctypes.byref(a), dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v),
+                                          _ptr(ctx_len), _ptr(o), _ptr(lse), _stream(stream)))
+
+
+DECODE_SCRATCH_BYTES = 16 << 20  # MAKO_DECODE_SCRATCH_BYTES
 
 
 def window_random_blocks(n_blocks, lists, window=8, n_random=8, seed=0):
