@@ -1,6 +1,8 @@
 """Dense flash attention (mako_attn_fwd) on the GPU against the CPU oracle: the golden fixtures, the f16 S512
 causal GQA case in full, a sweep of masks / head widths / GQA groups / ragged sizes, untouched rows past n_q,
 and sampled rows of the Qwen3-8B-shape causal prefill (S4096) and the bidirectional S16384 case."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -77,7 +79,7 @@ SWEEP = [
                                                                                       else c[6]))
 def test_sweep(case):
     heads, kv, dim, n_q, n_k, q_pos0, block, dt, out = case
-    rng = np.random.default_rng(hash(case) & 0xFFFF)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))  # the same inputs in every process
     q_pad, k_pad = (n_q + 63) // 64 * 64, (n_k + 127) // 128 * 128
     qb = G.randn_bits(rng, (heads, q_pad, dim), dt)
     kb = G.randn_bits(rng, (kv, k_pad, dim), dt)
