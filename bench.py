@@ -11,10 +11,14 @@ decode, each against its own roof, the output projection after attention (Qwen3-
 gated delta rule of the linear-attention layers in TFLOP/s. Inputs are synthetic N(0, 1), resident in
 HBM before the timed region. `value` and ms_per_step come from --steps back-to-back launches bracketed by HIP
 events on the launch stream, after --warmup untimed ones; the roofline's `achieved` divides by the mean of each
-launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is the oracle (oracle/attn_oracle.c, double precision, pthreads) timed on
-a bounded random sample of the same rows, on up to 16 host threads, and scaled to the metric's unit.
+launch's own event pair (the kernel's duration, which rocprofv3's kernel trace also reports). The CPU baseline is
+the oracle (oracle/attn_oracle.c, double precision, pthreads) on the host's cores (at most 16 threads: one GPU's
+share of the host), timed on the whole S512 case and on a bounded random sample of the rows of every other
+configuration, scaled to the metric's unit by the sample's share of the algorithmic work; the same sampled rows are
+the parity check of the GPU output against the oracle.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only prefill,decode,bidir,sparse,heads,gather,proj,scan,copy]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+                  [--only prefill,s512,decode,bidir,sparse,heads,gather,proj,scan,copy]
 """
 import argparse
 import json
@@ -70,7 +74,60 @@ def traffic(kernel):
 
 
 def cpu_threads():
-    return max(1, min(16, os.cpu_count() or 1))
+    """Threads of the CPU baseline: the cores this process may run on, at most 16 (the host's share for one GPU)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(16, avail))
+
+
+def cpu_info():
+    """What the CPU baseline ran on: the thread count used, the host's logical CPUs, and the CPU model."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return {"cores": cpu_threads(), "nproc": os.cpu_count(), "affinity": avail, "cpu_model": model,
+            "threads": "oracle pthreads over (head, row) items, min(16, CPUs available to the process)"}
+
+
+ATOL, RTOL, LSE_TOL = 2e-3, 1e-2, 1e-3
+
+
+def parity_of(got, want, dim, lse_got=None, lse_want=None):
+    """Parity of GPU rows against the oracle's: max abs error, max relative error (over |ref| >= 1e-2), the worst
+    error as a fraction of the element tolerance 2e-3 + 1e-2 |ref|, the worst row's relative L2 (the reference's
+    measure, threshold 5e-3) and the LSE's max abs error."""
+    import numpy as np
+
+    got = np.asarray(got, np.float64).reshape(-1, dim)
+    want = np.asarray(want, np.float64).reshape(-1, dim)
+    err = np.abs(got - want)
+    big = np.abs(want) >= 1e-2
+    nrm = np.maximum((want ** 2).sum(1), 1e-30)
+    out = {"rows": int(got.shape[0]), "max_abs_err": float(err.max()),
+           "max_rel_err": float((err[big] / np.abs(want[big])).max()) if big.any() else 0.0,
+           "worst_over_tol": float((err / (ATOL + RTOL * np.abs(want))).max()),
+           "worst_row_rel_l2": float(np.sqrt(((got - want) ** 2).sum(1) / nrm).max())}
+    ok = bool(np.all(err <= ATOL + RTOL * np.abs(want))) and out["worst_row_rel_l2"] < 5e-3
+    if lse_got is not None:
+        lg, lw = np.asarray(lse_got, np.float64).ravel(), np.asarray(lse_want, np.float64).ravel()
+        fin = np.isfinite(lw)
+        out["lse_max_abs_err"] = float(np.abs(lg[fin] - lw[fin]).max()) if fin.any() else 0.0
+        ok = ok and out["lse_max_abs_err"] <= LSE_TOL and bool(np.array_equal(np.isfinite(lg), fin))
+    out["tolerance"] = "|err| <= 2e-3 + 1e-2 |ref| element-wise, worst row rel L2 < 5e-3, lse within 1e-3"
+    out["within_tolerance"] = ok
+    return out
 
 
 def bits(torch, t):
@@ -88,6 +145,48 @@ def cpu_sample(run, n0, budget):
         if dt >= budget / 4 or n >= 1 << 16:
             return n, dt
         n = int(n * min(8.0, max(2.0, budget / 2 / max(dt, 1e-3))))
+
+
+def dense_cpu_leg(torch, M, O, q, k, v, o, lse, args, dtype, seed, n0, label, full=False):
+    """The CPU baseline and parity of a dense leg: the oracle on every (head, row) pair (full) or on a random sample
+    of them, timed; the sampled rows of the GPU output (o [n_q][heads * D], lse [heads][n_q]) against the oracle's.
+    Returns (cpu_baseline, parity)."""
+    import numpy as np
+
+    H, D, S, nk = args["heads"], args["dim"], args["n_q"], args["n_k"]
+    qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
+    rng = np.random.default_rng(seed)
+    gpu_o, gpu_l = o.float().cpu().numpy(), lse.cpu().numpy()
+    state = {}
+
+    def keys_of(r):  # keys row r sees (prefix-causal rule with q_pos0)
+        pos = args["q_pos0"] + int(r)
+        return nk if pos >= args["block"] else min(nk, pos + 1)
+
+    def run(n):
+        if full:
+            hr = np.stack(np.meshgrid(np.arange(H), np.arange(S), indexing="ij"), -1).reshape(-1, 2).astype(np.uint32)
+        else:
+            hr = np.stack([rng.integers(0, H, n), rng.integers(0, S, n)], 1).astype(np.uint32)
+        want, wl = O.attn_dense_rows(qb, kb, vb, hr, dtype=dtype, nthreads=cpu_threads(), **args)
+        state["hr"], state["want"], state["wl"] = hr, want, wl
+
+    if full:
+        t0 = time.perf_counter()
+        run(0)
+        n, dt = H * S, time.perf_counter() - t0
+    else:
+        n, dt = cpu_sample(run, n0, CPU_SECONDS)
+    hr, want, wl = state["hr"], state["want"], state["wl"]
+    sample_flop = float(sum(4.0 * D * keys_of(r) for _, r in hr))
+    got = np.stack([gpu_o[r, h * D:(h + 1) * D] for h, r in hr])
+    got_l = np.array([gpu_l[h, r] for h, r in hr])
+    base = {"value": sample_flop / dt / 1e12, "unit": "TFLOP/s", "kind": "port", "extrapolated": not full,
+            "sample": (f"every (head, row) pair of {label}" if full else
+                       f"{n} random (head, row) pairs of {label}") +
+                      f", double precision, {dt:.2f} s wall; TFLOP/s of the unmasked pairs computed"}
+    base.update(cpu_info())
+    return base, parity_of(got, want, D, got_l, wl), (hr, want, wl)
 
 
 def bench_prefill(torch, M, steps, warmup, with_cpu):
@@ -111,27 +210,46 @@ def bench_prefill(torch, M, steps, warmup, with_cpu):
     if with_cpu:
         import oracle as O
 
-        qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
-        rng = np.random.default_rng(7)
-        gpu_o = o.float().cpu().numpy()
-        state = {}
+        base, par, (hr, want, _) = dense_cpu_leg(torch, M, O, q, k, v, o, lse, args, O.BF16, 7, 64,
+                                                 "the S4096 causal prefill")
+        # The same rows with an f32 output: the kernel's own error, apart from the rounding of the bf16 output
+        # (half an ulp of bf16 is 7.8e-3 at |o| in [2, 4)).
+        o32 = torch.empty((S, H * D), dtype=torch.float32, device="cuda")
+        M.attn_fwd(q, k, v, o32, **args)
+        g32 = o32.cpu().numpy()
+        par["f32_output"] = {k_: v_ for k_, v_ in parity_of(np.stack([g32[r, h * D:(h + 1) * D] for h, r in hr]),
+                                                            want, D).items() if k_ != "tolerance"}
+        out["cpu_baseline"], out["parity"] = base, par
+    return out
 
-        def run(n):
-            hr = np.stack([rng.integers(0, H, n), rng.integers(0, S, n)], 1).astype(np.uint32)
-            want, _ = O.attn_dense_rows(qb, kb, vb, hr, dtype=O.BF16, nthreads=cpu_threads(), **args)
-            state["hr"], state["want"] = hr, want
 
-        n, dt = cpu_sample(run, 64, CPU_SECONDS)
-        hr, want = state["hr"], state["want"]
-        sample_flop = float(sum(4.0 * D * (int(r) + 1) for _, r in hr))
-        got = np.stack([gpu_o[r, h * D:(h + 1) * D] for h, r in hr])
-        err = np.abs(got - want)
-        out["cpu_baseline"] = {"value": sample_flop / dt / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
-                               "kind": "port",
-                               "sample": f"{n} random (head, row) pairs of the S4096 causal prefill, double "
-                                         f"precision, {dt:.2f} s wall; extrapolated by unmasked-pair FLOPs"}
-        out["parity"] = {"rows": n, "max_abs_err": float(err.max()),
-                         "within_tolerance": bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))}
+def bench_s512(torch, M, steps, warmup, with_cpu):
+    """The reference-CPU-runnable case: causal GQA, 16 query heads over 8 kv heads, D 128, S 512, f16 in, f32 out
+    (the reference's output), LSE; the CPU baseline runs it whole and every output row is checked."""
+    S, H, KV, D = 512, 16, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(512)
+    q = torch.randn((H, S, D), generator=gen, device="cuda").half()
+    k = torch.randn((KV, S, D), generator=gen, device="cuda").half()
+    v = torch.randn((KV, S, D), generator=gen, device="cuda").half()
+    o = torch.empty((S, H * D), dtype=torch.float32, device="cuda")
+    lse = torch.empty((H, S), dtype=torch.float32, device="cuda")
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, q_pos0=0, block=U32_MAX, dim=D)
+    ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
+    flop = 4.0 * D * (S * (S + 1) / 2) * H
+    kt = flop / (kms * 1e-3) / 1e12
+    out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+           "dtype": "f16",
+           "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_causal_s512"),
+                        "kernel": "flash_fwd<f16,f32,128>", "kernel_ms": kms,
+                        "note": "1.08 GFLOP: 16 workgroups on 256 CUs, launch- and latency-bound"},
+           "config": {"workload": "causal GQA prefill, batch 1, 16 query heads / 8 kv heads, D 128, S 512, f16 in, "
+                                  "f32 out, LSE (the reference-CPU-runnable case)"}}
+    if with_cpu:
+        import oracle as O
+
+        out["cpu_baseline"], out["parity"], _ = dense_cpu_leg(torch, M, O, q, k, v, o, lse, args, O.F16, 0, 0,
+                                                              "the S512 causal prefill", full=True)
     return out
 
 
@@ -162,45 +280,57 @@ def bench_decode(torch, M, steps, warmup, with_cpu):
 
         qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
         rng = np.random.default_rng(11)
-        gpu_o = o.float().cpu().numpy()
+        gpu_o, gpu_l = o.float().cpu().numpy(), lse.cpu().numpy()
         state = {}
 
         def run(n):
             sh = np.stack([rng.integers(0, B, n), rng.integers(0, H, n)], 1).astype(np.uint32)
-            want, _ = O.attn_decode_rows(qb, kb, vb, ctx, sh, batch=B, heads=H, kv_heads=KV, dim=D, cap=cap,
-                                         dtype=O.F16, nthreads=cpu_threads())
-            state["sh"], state["want"] = sh, want
+            want, wl = O.attn_decode_rows(qb, kb, vb, ctx, sh, batch=B, heads=H, kv_heads=KV, dim=D, cap=cap,
+                                          dtype=O.F16, nthreads=cpu_threads())
+            state["sh"], state["want"], state["wl"] = sh, want, wl
 
         n, dt = cpu_sample(run, 16, CPU_SECONDS)
-        sh, want = state["sh"], state["want"]
+        sh, want, wl = state["sh"], state["want"], state["wl"]
         # a (sequence, head) pair's share of the K + V bytes: its kv head's rows serve H / KV query heads
         sample_bytes = float(sum(4096 * int(ctx[b]) / H for b, _ in sh))
         got = np.stack([gpu_o[b, h * D:(h + 1) * D] for b, h in sh])
-        err = np.abs(got - want)
-        out["cpu_baseline"] = {"value": sample_bytes / dt / 1e9, "unit": "GB/s", "cores": cpu_threads(),
-                               "kind": "port",
+        out["cpu_baseline"] = {"value": sample_bytes / dt / 1e9, "unit": "GB/s", "kind": "port", "extrapolated": True,
                                "sample": f"{n} random (sequence, head) pairs of the batch-16 decode, double "
                                          f"precision, {dt:.2f} s wall; each pair credited its share of K + V bytes"}
-        out["parity"] = {"rows": n, "max_abs_err": float(err.max()),
-                         "within_tolerance": bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))}
+        out["cpu_baseline"].update(cpu_info())
+        out["parity"] = parity_of(got, want, D, np.array([gpu_l[b, h] for b, h in sh]), wl)
     return out
 
 
-def bench_bidir(torch, M, steps, warmup):
+def bench_bidir(torch, M, steps, warmup, with_cpu):
     S, H, D = 16384, 24, 128
     gen = torch.Generator(device="cuda").manual_seed(16384)
     q, k, v = (torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(3))
     o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((H, S), dtype=torch.float32, device="cuda")
     args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=H, q_pos0=0, block=0, dim=D)
-    ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, **args), steps, warmup)
+    ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
     flop = 4.0 * D * S * S * H
-    tflops = flop / (ms * 1e-3) / 1e12
-    return {"ms": ms, "kernel_ms": kms, "tflops": tflops, "flop": flop, "frac": flop / (kms * 1e-3) / 1e12 / PEAK_TFLOPS}
+    kt = flop / (kms * 1e-3) / 1e12
+    out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+           "kernel_ms": round(kms, 4), "frac": round(kt / PEAK_TFLOPS, 4), "dtype": "bf16",
+           "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_bidir_s16384"),
+                        "kernel": "flash_fwd<bf16,bf16,128>", "kernel_ms": kms},
+           "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16 in/out, LSE"}}
+    if with_cpu:
+        import oracle as O
+
+        out["cpu_baseline"], out["parity"], _ = dense_cpu_leg(torch, M, O, q, k, v, o, lse, args, O.BF16, 5, 16,
+                                                              "the S16384 bidirectional case")
+    return out
 
 
-def bench_sparse(torch, M, steps, warmup):
+def bench_sparse(torch, M, steps, warmup, with_cpu):
     """Block-sparse causal attention, S16384, 32 query heads over 8 kv heads, 64x64 blocks: each block attends
-    itself (causal), the 8 before it and 8 random earlier ones (seed 16384, one list per kv head)."""
+    itself (causal), the 8 before it and 8 random earlier ones (seed 16384, one list per kv head). MFMA-bound: the
+    gathered K / V (each block once per query block and kv head, 1.105 GB) is mostly served by the L2s (the byte
+    counters measure about half a gigabyte of HBM traffic), so the roofline divides the unmasked-pair FLOPs."""
     import numpy as np
 
     S, H, KV, D = 16384, 32, 8, 128
@@ -211,22 +341,60 @@ def bench_sparse(torch, M, steps, warmup):
     k = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
     v = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
     o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((H, S), dtype=torch.float32, device="cuda")
     sel_d = torch.from_numpy(sel.view(np.int16)).to("cuda")
     nsel_d = torch.from_numpy(nsel.view(np.int16)).to("cuda")
     valid = torch.ones(S, dtype=torch.uint8, device="cuda")
     map_ = torch.arange(S, dtype=torch.int32, device="cuda")
     args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, n_cubes=nb, max_sel=sel.shape[2], dense0=S,
                 dense1=S, causal=1, sel_heads=KV)
-    ms, kms = time_launches(torch, lambda: M.attn_sparse(q, k, v, o, sel_d, nsel_d, valid, map_, **args), steps,
-                            warmup)
+    ms, kms = time_launches(torch, lambda: M.attn_sparse(q, k, v, o, sel_d, nsel_d, valid, map_, lse=lse, **args),
+                            steps, warmup)
     blocks = int(nsel[0].astype(np.int64).sum())          # blocks a head attends (the same count for every list)
     pairs = (blocks - nb) * 64 * 64 + nb * (64 * 65 // 2)  # full blocks, plus the causal diagonal ones
     flop = 4.0 * D * pairs * H
     gathered = float(blocks) * KV * 64 * D * 2 * 2        # K + V of each block once per (query block, kv head)
-    tflops, gbps = flop / (ms * 1e-3) / 1e12, gathered / (ms * 1e-3) / 1e9
-    t_mfma, t_hbm = flop / (PEAK_TFLOPS * 1e12), gathered / (PEAK_GBPS * 1e9)
-    return {"ms": ms, "kernel_ms": kms, "tflops": tflops, "gbps": gbps, "flop": flop, "gathered_bytes": gathered,
-            "blocks": blocks, "bound": "mfma" if t_mfma >= t_hbm else "hbm", "frac": max(t_mfma, t_hbm) / (kms * 1e-3)}
+    kt = flop / (kms * 1e-3) / 1e12
+    hbm = traffic("flash_sparse_s16384")
+    out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+           "kernel_ms": round(kms, 4), "dtype": "bf16", "blocks": blocks,
+           "gathered_gbps": round(gathered / (kms * 1e-3) / 1e9, 1),
+           "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": kt / PEAK_TFLOPS, "traffic": hbm, "kernel": "flash_sparse8<bf16,bf16>",
+                        "kernel_ms": kms,
+                        "hbm_frac": None if hbm is None else hbm / (kms * 1e-3) / 1e9 / PEAK_GBPS,
+                        "note": "gathered K + V (1.105 GB) is L2 traffic; HBM moves the counted bytes"},
+           "config": {"workload": "causal block-sparse, 32 query heads / 8 kv heads, D 128, S 16384, 64x64 blocks: "
+                                  "diagonal + 8 preceding + 8 random earlier (seed 16384, per kv head), bf16",
+                      "blocks_per_head": blocks}}
+    if with_cpu:
+        import oracle as O
+
+        qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
+        rng = np.random.default_rng(3)
+        gpu_o, gpu_l = o.float().cpu().numpy(), lse.cpu().numpy()
+        valid_h = np.ones(S, np.uint8)
+        state = {}
+
+        def run(n):
+            hr = np.stack([rng.integers(0, H, n), rng.integers(0, S, n)], 1).astype(np.uint32)
+            want, wl = O.attn_sparse_rows(qb, kb, vb, sel, nsel, valid_h, hr, dtype=O.BF16, nthreads=cpu_threads(),
+                                          **args)
+            state["hr"], state["want"], state["wl"] = hr, want, wl
+
+        n, dt = cpu_sample(run, 64, CPU_SECONDS)
+        hr, want, wl = state["hr"], state["want"], state["wl"]
+        # keys a row sees: 64 per full block of its list, plus the causal part of its diagonal block
+        sample_flop = float(sum(4.0 * D * ((int(nsel[h // (H // KV), r // 64]) - 1) * 64 + r % 64 + 1)
+                                for h, r in hr))
+        got = np.stack([gpu_o[r, h * D:(h + 1) * D] for h, r in hr])
+        out["cpu_baseline"] = {"value": sample_flop / dt / 1e12, "unit": "TFLOP/s", "kind": "port",
+                               "extrapolated": True,
+                               "sample": f"{n} random (head, row) pairs of the S16384 block-sparse case, double "
+                                         f"precision, {dt:.2f} s wall; TFLOP/s of the unmasked pairs computed"}
+        out["cpu_baseline"].update(cpu_info())
+        out["parity"] = parity_of(got, want, D, np.array([gpu_l[h, r] for h, r in hr]), wl)
+    return out
 
 
 def bench_heads(torch, M, steps, warmup):
@@ -368,9 +536,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline and parity legs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs to run alone: prefill, decode, bidir, sparse, heads, gather, proj, scan, copy")
+                    help="comma-separated legs to run alone (no CPU legs unless --cpu): prefill, s512, decode, "
+                         "bidir, sparse, heads, gather, proj, scan, copy")
+    ap.add_argument("--cpu", action="store_true", help="with --only: run the legs' CPU-baseline and parity parts")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path is built and "
@@ -384,12 +554,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     if args.only:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        fn = {"prefill": lambda: bench_prefill(torch, M, args.steps, args.warmup, False),
-              "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, False),
-              "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup),
-              "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup),
+        c = args.cpu
+        fn = {"prefill": lambda: bench_prefill(torch, M, args.steps, args.warmup, c),
+              "s512": lambda: bench_s512(torch, M, args.steps, args.warmup, c),
+              "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, c),
+              "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup, c),
+              "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup, c),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
               "proj": lambda: bench_proj(torch, M, args.steps, args.warmup),
@@ -401,12 +573,11 @@ def main():
             print(json.dumps({leg: fn[leg]()}), flush=True)
         return
     with_cpu = not args.no_cpu
-    if with_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
     pre = bench_prefill(torch, M, args.steps, args.warmup, with_cpu)
+    s512 = bench_s512(torch, M, args.steps, args.warmup, with_cpu)
     dec = bench_decode(torch, M, args.steps, args.warmup, with_cpu)
-    bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup))
-    spa = bench_sparse(torch, M, args.steps, args.warmup)
+    bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup), with_cpu)
+    spa = bench_sparse(torch, M, args.steps, args.warmup, with_cpu)
     hds = bench_heads(torch, M, args.steps, args.warmup)
     gat = bench_gather(torch, M, args.steps, args.warmup)
     prj = bench_proj(torch, M, max(1, args.steps // 2), args.warmup)
@@ -428,21 +599,14 @@ def main():
                                "in/out, fp32 accumulate, LSE", "global_batch": 1, "seq_len": 4096,
                    "parallelism": "single GPU"},
         "roofline": pre["roofline"],
+        "prefill_s512": s512,
         "decode": {"value": round(dec["gbps"], 1), "unit": "GB/s", "ms_per_step": round(dec["ms"], 4),
                    "dtype": "f16", "config": {"workload": "decode, batch 16, 32 query heads / 8 kv heads, D 128, "
                                                           "contexts U[1024, 32768] seed 2026, f16 cache",
                                               "sum_ctx": dec["sum_ctx"]},
                    "roofline": dec["roofline"]},
-        "bidirectional": {"value": round(bid["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(bid["ms"], 4),
-                          "kernel_ms": round(bid["kernel_ms"], 4),
-                          "frac": round(bid["frac"], 4),
-                          "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16"}},
-        "block_sparse": {"value": round(spa["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(spa["ms"], 4),
-                         "kernel_ms": round(spa["kernel_ms"], 4),
-                         "gathered_gbps": round(spa["gbps"], 1), "bound": spa["bound"], "frac": round(spa["frac"], 4),
-                         "config": {"workload": "causal block-sparse, 32 query heads / 8 kv heads, D 128, S 16384, "
-                                                "64x64 blocks: diagonal + 8 preceding + 8 random earlier (seed "
-                                                "16384, per kv head), bf16", "blocks_per_head": spa["blocks"]}},
+        "bidirectional": bid,
+        "block_sparse": spa,
         "head_tiles": {"value": round(hds["gbps"], 1), "unit": "GB/s", "ms_per_step": round(hds["ms"], 4),
                        "kernel_ms": round(hds["kernel_ms"], 4), "bound": "hbm", "frac": round(hds["frac"], 4),
                        "config": {"workload": "Qwen3-8B prefill head tiles: 4096 tokens, q 32 and k 8 heads of 128 "
