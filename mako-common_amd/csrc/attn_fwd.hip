@@ -616,9 +616,20 @@ __global__ __launch_bounds__(kWaves8 * 64) void flash_fwd(const FwdParams p)
 // Query rows a workgroup covers for heads of `dim` with hq heads a workgroup.
 uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uint32_t)kWaves8) * 32u / hq; }
 
+}  // namespace
+
+// flash_fwd_r64 (attn_fwd64.hip): heads of 128 with 64 rows a wave; false when a size does not fit its offsets.
 template <class T, class TO>
-void launch_d(uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
+bool launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+                  float* lse, hipStream_t s);
+
+namespace {
+
+template <class T, class TO>
+void launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
 {
+    if (dim == 128 && launch_fwd64<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s))
+        return;
     switch (dim) {
     case 64:
         hipLaunchKernelGGL((flash_fwd<T, TO, 64>), grid, dim3(kWaves8 * 64), 0, s, p);
@@ -678,14 +689,14 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (in == MAKO_BF16) {
         if (out == MAKO_F32)
-            launch_d<__bf16, float>(dim, p, grid, s);
+            launch_d<__bf16, float>(a, dim, p, grid, s);
         else
-            launch_d<__bf16, __bf16>(dim, p, grid, s);
+            launch_d<__bf16, __bf16>(a, dim, p, grid, s);
     } else {
         if (out == MAKO_F32)
-            launch_d<_Float16, float>(dim, p, grid, s);
+            launch_d<_Float16, float>(a, dim, p, grid, s);
         else
-            launch_d<_Float16, _Float16>(dim, p, grid, s);
+            launch_d<_Float16, _Float16>(a, dim, p, grid, s);
     }
     return check_launch("attention");
 }
