@@ -40,7 +40,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 K_ROW = 272             # LDS bytes of a K row (256 + 16 of padding: 16-byte reads down a column are conflict-free)
 K_TILE = 64 * K_ROW     # 17408
 V_TILE = 128 * 64 * 2   # 16384: V^T, 128 head dims x 64 keys in f16
-RING = 4                # LDS operand reads in flight ahead of their MFMAs
+RING = 8                # LDS operand ring slots
+AHEAD = 6               # operand reads in flight ahead of their MFMAs (a slot is refilled two fragments after its
+                        # last MFMA was issued)
 
 # ---- registers ---------------------------------------------------------------------------------------------------
 
@@ -72,32 +74,29 @@ def RINGR(s):
     return f"a[{192 + 4 * s}:{192 + 4 * s + 3}]"
 
 
-def VREG(i):
-    return f"v{i}"
+# Two staging sets (tiles alternate between them, so a tile's loads are issued two tiles ahead of its LDS writes):
+# K rows as loaded in the accumulator registers, V rows in vector registers.
+def KST(i, st):         # staged K of set st, key i of the thread's four
+    b = 224 + 16 * st + 4 * i
+    return f"a[{b}:{b + 3}]"
 
 
-def KST(i, base):       # staged K, key i of the thread's four
-    return f"v[{base + 4 * i}:{base + 4 * i + 3}]"
+def VST(i, p, st):      # staged V of set st, key i, dword p (head dims 2p, 2p + 1 of the thread's 8)
+    return f"v{176 + 16 * st + 4 * i + p}"
 
 
-def VST(i, p, base):    # staged V, key i, dword p (head dims 2p, 2p + 1 of the thread's 8)
-    return f"v{base + 4 * i + p}"
+def VSTQ(i, st):
+    b = 176 + 16 * st + 4 * i
+    return f"v[{b}:{b + 3}]"
 
 
-def VSTQ(i, base):
-    return f"v[{base + 4 * i}:{base + 4 * i + 3}]"
+def VTO(e, half):       # transposed V, head dim e of the thread's 8: keys (0, 1) in half 0, (2, 3) in half 1
+    return f"v{160 + 2 * e + half}"
 
 
-def VTO(e, half, base):  # transposed V, head dim e of the thread's 8: keys (0, 1) in half 0, (2, 3) in half 1
-    return f"v{base + 2 * e + half}"
+def VTO2(e):
+    return f"v[{160 + 2 * e}:{161 + 2 * e}]"
 
-
-def VTO2(e, base):
-    return f"v[{base + 2 * e}:{base + 2 * e + 1}]"
-
-
-STAGE = dict(k=160, v=176, o=192)           # the loop's staging registers
-STAGE_PRO = dict(k=64, v=80, o=96)          # a second set for the prologue (inside the second score tile)
 
 NEGMU = ("v208", "v209")   # -(running maximum) of the lane's row, 0 while it is -inf
 LSUM = ("v210", "v211")    # row sum over this lane's keys
@@ -124,7 +123,7 @@ SMASK = ("s[88:89]", "s[90:91]", "s[92:93]", "s[94:95]")  # lane masks of the ke
 SINC = {K_TILE: ("s84", "s85"), V_TILE: ("s86", "s87")}   # (step, wrap) of a buffer rotation, by stride
 
 CLOBBER_V = 232
-CLOBBER_A = 208
+CLOBBER_A = 256
 CLOBBER_S = (60, 96)
 
 
@@ -159,20 +158,22 @@ def rotate(sidx, role, regs):
     return ops
 
 
-WREGS = [("%[kw]", K_TILE)] + [(f"%[vw{i}]", V_TILE) for i in range(4)]
+WREGS = [("%[kw]", K_TILE), ("%[vwx]", V_TILE)]
 KREGS = [("%[kr]", K_TILE)]
 VREGS = [(f"%[vr{i}]", V_TILE) for i in range(4)]
 
 
-def stage_loads(rs):
-    """The thread's four K rows and four V rows (16 bytes each) of the tile at voffset %[st] (rows past the
-    workgroup's keys lie outside the buffers and load as zeros)."""
-    ops = [f"buffer_load_dwordx4 {KST(i, rs['k'])}, %[st], %[krs], 0 offen offset:{256 * i}" for i in range(4)]
-    ops += [f"buffer_load_dwordx4 {VSTQ(i, rs['v'])}, %[st], %[vrs], 0 offen offset:{256 * i}" for i in range(4)]
+def stage_loads(st):
+    """Staging set st gets the thread's four K rows (voffset %[st]) and four V rows (%[stv]), 16 bytes each, of the
+    next tile to load; both offsets then move on by a tile. Rows past the workgroup's keys lie outside the buffers
+    and load as zeros."""
+    ops = [f"buffer_load_dwordx4 {KST(i, st)}, %[st], %[krs], 0 offen offset:{256 * i}" for i in range(4)]
+    ops += [f"buffer_load_dwordx4 {VSTQ(i, st)}, %[stv], %[vrs], 0 offen offset:{256 * i}" for i in range(4)]
+    ops += ["v_add_u32 %[st], 0x4000, %[st]", "v_add_u32 %[stv], 0x4000, %[stv]"]
     return ops
 
 
-def stage_convert(bf16, rs):
+def stage_convert(bf16, st):
     """V of keys 0..3 (dword p: head dims 2p, 2p + 1) into f16 pairs of consecutive keys for each head dim
     (bf16 -> f16 rounds toward zero, as the C++ kernels' staging does)."""
     ops = []
@@ -180,8 +181,8 @@ def stage_convert(bf16, rs):
         for lohi in range(2):
             e = 2 * p + lohi
             for half in range(2):
-                a, b = VST(2 * half, p, rs["v"]), VST(2 * half + 1, p, rs["v"])
-                dst = VTO(e, half, rs["o"])
+                a, b = VST(2 * half, p, st), VST(2 * half + 1, p, st)
+                dst = VTO(e, half)
                 if bf16:
                     if lohi == 0:
                         ops += [f"v_lshlrev_b32 {TMP[12]}, 16, {a}", f"v_lshlrev_b32 {TMP[13]}, 16, {b}"]
@@ -193,17 +194,21 @@ def stage_convert(bf16, rs):
     return ops
 
 
-def stage_writes(rs):
-    ops = [f"ds_write_b128 %[kw], {KST(i, rs['k'])} offset:{K_ROW * i}" for i in range(4)]
-    ops += [f"ds_write_b64 %[vw{e >> 1}], {VTO2(e, rs['o'])} offset:{128 * (e & 1)}" for e in range(8)]
+def stage_writes(st):
+    """K rows to their LDS rows; V^T: head dim 8 c + e of the thread's keys at %[vwx] ^ 16 e (the chunk swizzle of
+    row d is (d % 8) ^ (d / 8 % 4), here e ^ a per-lane constant folded into %[vwx]) plus the row, 128 e."""
+    ops = [f"ds_write_b128 %[kw], {KST(i, st)} offset:{K_ROW * i}" for i in range(4)]
+    for e in range(8):
+        t = TMP[8 + (e % 4)]
+        ops.append(f"v_xor_b32 {t}, {16 * e}, %[vwx]")
+        ops.append(f"ds_write_b64 {t}, {VTO2(e)} offset:{128 * e}")
     return ops
 
 
-def staging(bf16):
-    """One tile's staging in the loop: wait for its loads, convert, write to LDS, rotate the write addresses, then
-    load the tile after next."""
-    return (["s_waitcnt vmcnt(0)"] + stage_convert(bf16, STAGE) + stage_writes(STAGE) + rotate(SBW, "w", WREGS)
-            + ["v_add_u32 %[st], 0x4000, %[st]"])
+def staging(bf16, st):
+    """A tile's staging in the loop (staging set st): wait for its loads (the next tile's stay in flight), convert,
+    write to LDS and rotate the write addresses; then load the tile two ahead into the same set."""
+    return (["s_waitcnt vmcnt(8)"] + stage_convert(bf16, st) + stage_writes(st) + rotate(SBW, "w", WREGS))
 
 
 def k_reads(addr):
@@ -249,7 +254,7 @@ def interleave(e, reads, mfmas, valu):
         issued.append(f"R{f}")
 
     nxt = 0
-    while nxt < min(RING, len(reads)):
+    while nxt < min(AHEAD, len(reads)):
         issue(nxt)
         nxt += 1
     n = len(mfmas)
@@ -455,23 +460,18 @@ def body(in_dtype, out_dtype):
     for rb in range(2):
         for kk in range(8):
             e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen offset:{32 * kk}")
-    # tiles 0 and 1 (the second through registers of the second score tile), then tile 2 in flight
-    for op in stage_loads(STAGE):
+    # tiles 0 and 1 through the two staging sets, then tiles 2 and 3 in flight
+    for op in stage_loads(0) + stage_loads(1):
         e(op)
-    e("v_add_u32 %[st], 0x4000, %[st]")
-    for op in stage_loads(STAGE_PRO):
-        e(op)
-    e("v_add_u32 %[st], 0x4000, %[st]")
     for i in range(128):
         e(f"v_accvgpr_write_b32 a{i}, 0")
     e(f"s_mov_b32 {SBW}, 0")
-    e("s_waitcnt vmcnt(8)")
-    for op in stage_convert(bf16, STAGE) + stage_writes(STAGE) + rotate(SBW, "w", WREGS):
-        e(op)
     e("s_waitcnt vmcnt(0)")
-    for op in stage_convert(bf16, STAGE_PRO) + stage_writes(STAGE_PRO) + rotate(SBW, "w", WREGS):
+    for op in stage_convert(bf16, 0) + stage_writes(0) + rotate(SBW, "w", WREGS):
         e(op)
-    for op in stage_loads(STAGE):
+    for op in stage_convert(bf16, 1) + stage_writes(1) + rotate(SBW, "w", WREGS):
+        e(op)
+    for op in stage_loads(0) + stage_loads(1):
         e(op)
     e(f"s_mov_b32 {SJ}, 0")
     e(f"s_mov_b32 {SBK}, 0")
@@ -492,11 +492,11 @@ def body(in_dtype, out_dtype):
         path)."""
         cur, nxt = par, 1 - par
         tag = f"{variant}{par}"
-        # phase QK
-        valu = staging(bf16)
+        # phase QK (tile j's staging set is j % 2 = par)
+        valu = staging(bf16, par)
         if variant != "first":
             valu += pack_and_sum(cur)
-        valu += stage_loads(STAGE)
+        valu += stage_loads(par)
         if variant != "last":
             interleave(e, k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu)
         else:
@@ -559,7 +559,7 @@ def body(in_dtype, out_dtype):
 
     def iteration_first_masked():
         # as iteration(0, 'first') with the next tile masked
-        valu = staging(bf16) + stage_loads(STAGE)
+        valu = staging(bf16, 0) + stage_loads(0)
         interleave(e, k_reads("%[kr]"), qk_mfmas(in_dtype, 1), valu)
         for op in rotate(SBK, "k", KREGS):
             e(op)
@@ -576,7 +576,7 @@ def body(in_dtype, out_dtype):
     e(f"s_branch {lbl('L_iter1')}")
     # the last iteration of the wave, by entry point
     e.label("L_last_first")
-    valu = staging(bf16) + stage_loads(STAGE)
+    valu = staging(bf16, 0) + stage_loads(0)
     for op in valu:
         e(op)
     interleave(e, v_reads(), pv_mfmas(), [])
@@ -592,16 +592,21 @@ def body(in_dtype, out_dtype):
     for par in (0, 1):
         for variant in ("plain", "masked", "last"):
             exact_block(par, variant)
-    # staging-only iterations for the tiles the workgroup's other waves still compute
+    # staging-only iterations for the tiles the workgroup's other waves still compute (staging set j % 2)
     e.label("L_tail")
-    e("s_cmp_ge_u32 %s, %%[nt]" % SJ)
-    e(f"s_cbranch_scc1 {lbl('L_epi')}")
-    e("s_waitcnt lgkmcnt(0)")
-    e("s_barrier")
-    for op in staging(bf16) + stage_loads(STAGE):
-        e(op)
-    e(f"s_add_u32 {SJ}, {SJ}, 1")
-    e(f"s_branch {lbl('L_tail')}")
+    e(f"s_and_b32 {ST[3]}, {SJ}, 1")
+    e(f"s_cmp_eq_u32 {ST[3]}, 1")
+    e(f"s_cbranch_scc1 {lbl('L_tail1')}")
+    for par in (0, 1):
+        e.label(f"L_tail{par}")
+        e("s_cmp_ge_u32 %s, %%[nt]" % SJ)
+        e(f"s_cbranch_scc1 {lbl('L_epi')}")
+        e("s_waitcnt lgkmcnt(0)")
+        e("s_barrier")
+        for op in staging(bf16, par) + stage_loads(par):
+            e(op)
+        e(f"s_add_u32 {SJ}, {SJ}, 1")
+    e(f"s_branch {lbl('L_tail0')}")
     e.label("L_epi")
     epilogue(e, out_dtype)
     return e.out
@@ -613,12 +618,24 @@ def clobbers():
     return ", ".join(regs)
 
 
+def check_registers(lines):
+    """Every register the stream names must be one the clobber list reserves (the wave is only given those)."""
+    import re
+    for ln in lines:
+        for kind, one, lo, hi in re.findall(r"\b([vas])(?:(\d+)|\[(\d+):(\d+)\])", ln.split(";")[0]):
+            top = int(one) if one else int(hi)
+            bot = int(one) if one else int(lo)
+            limit = {"v": (0, CLOBBER_V), "a": (0, CLOBBER_A), "s": CLOBBER_S}[kind]
+            assert limit[0] <= bot and top < limit[1], f"{kind}{bot}..{top} outside the reserved registers: {ln}"
+
+
 def main():
     out = ["// Generated by gen_attn_fwd64.py (the instruction stream of flash_fwd_r64; the design is described there).",
            "// Do not edit: change the generator and run it.", "#pragma once", ""]
     for ind in ("bf16", "f16"):
         for outd in ("f32", ind):
             lines = body(ind, outd)
+            check_registers(lines)
             name = f"MAKO_FWD64_ASM_{ind.upper()}_{outd.upper()}"
             out.append(f"#define {name} \\")
             for ln in lines:
