@@ -206,7 +206,7 @@ def bench_prefill(torch, M, steps, warmup, with_cpu):
     out = {"ms": ms, "kernel_ms": kms, "tflops": tflops, "flop": flop,
            "roofline": {"bound": "mfma", "achieved": ktflops, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": ktflops / PEAK_TFLOPS, "traffic": traffic("flash_fwd_causal_s4096"),
-                        "kernel": "flash_fwd<bf16,bf16,128>", "kernel_ms": kms}}
+                        "kernel": "vt_image<bf16> + flash_fwd_r64<bf16,bf16> (one call, both kernels)", "kernel_ms": kms}}
     if with_cpu:
         import oracle as O
 
@@ -241,7 +241,7 @@ def bench_s512(torch, M, steps, warmup, with_cpu):
            "dtype": "f16",
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_causal_s512"),
-                        "kernel": "flash_fwd<f16,f32,128>", "kernel_ms": kms,
+                        "kernel": "vt_image<f16> + flash_fwd_r64<f16,f32> (one call, both kernels)", "kernel_ms": kms,
                         "note": "1.08 GFLOP: 16 workgroups on 256 CUs, launch- and latency-bound"},
            "config": {"workload": "causal GQA prefill, batch 1, 16 query heads / 8 kv heads, D 128, S 512, f16 in, "
                                   "f32 out, LSE (the reference-CPU-runnable case)"}}
@@ -316,7 +316,7 @@ def bench_bidir(torch, M, steps, warmup, with_cpu):
            "kernel_ms": round(kms, 4), "frac": round(kt / PEAK_TFLOPS, 4), "dtype": "bf16",
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_bidir_s16384"),
-                        "kernel": "flash_fwd<bf16,bf16,128>", "kernel_ms": kms},
+                        "kernel": "vt_image<bf16> + flash_fwd_r64<bf16,bf16> (one call, both kernels)", "kernel_ms": kms},
            "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16 in/out, LSE"}}
     if with_cpu:
         import oracle as O

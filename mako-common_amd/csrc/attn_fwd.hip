@@ -618,18 +618,23 @@ uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uin
 
 }  // namespace
 
-// flash_fwd_r64 (attn_fwd64.hip): heads of 128 with 64 rows a wave; false when a size does not fit its offsets.
+// flash_fwd_r64 (attn_fwd64.hip): heads of 128 with 64 rows a wave; 1 launched, 0 when a size does not fit its
+// offsets, -1 when its workspace could not be allocated.
 template <class T, class TO>
-bool launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                   float* lse, hipStream_t s);
 
 namespace {
 
+// false when flash_fwd_r64's workspace could not be allocated (nothing was launched).
 template <class T, class TO>
-void launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
+bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
 {
-    if (dim == 128 && launch_fwd64<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s))
-        return;
+    if (dim == 128) {
+        const int r = launch_fwd64<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s);
+        if (r)
+            return r > 0;
+    }
     switch (dim) {
     case 64:
         hipLaunchKernelGGL((flash_fwd<T, TO, 64>), grid, dim3(kWaves8 * 64), 0, s, p);
@@ -641,6 +646,7 @@ void launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 gr
         hipLaunchKernelGGL((flash_fwd_wide<T, TO, 256>), grid, dim3(kThreads), 0, s, p);
         break;
     }
+    return true;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -687,16 +693,15 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
         return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
     const dim3 grid(a->heads / hq, p.n_qblk);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (in == MAKO_BF16) {
-        if (out == MAKO_F32)
-            launch_d<__bf16, float>(a, dim, p, grid, s);
-        else
-            launch_d<__bf16, __bf16>(a, dim, p, grid, s);
-    } else {
-        if (out == MAKO_F32)
-            launch_d<_Float16, float>(a, dim, p, grid, s);
-        else
-            launch_d<_Float16, _Float16>(a, dim, p, grid, s);
-    }
+    bool launched;
+    if (in == MAKO_BF16)
+        launched = out == MAKO_F32 ? launch_d<__bf16, float>(a, dim, p, grid, s)
+                                   : launch_d<__bf16, __bf16>(a, dim, p, grid, s);
+    else
+        launched = out == MAKO_F32 ? launch_d<_Float16, float>(a, dim, p, grid, s)
+                                   : launch_d<_Float16, _Float16>(a, dim, p, grid, s);
+    if (!launched)
+        return fail(MAKO_EHIP, "attention: no device memory for the V^T tile images (%u kv heads x %u keys)",
+                    a->kv_heads, a->n_k);
     return check_launch("attention");
 }

@@ -11,14 +11,21 @@ per-lane addresses and passes them in as operands.
 Per wave: rows q0 .. q0 + 63 as two 32-row blocks (rb 0, 1). Scores are S^T = K Q^T on v_mfma_f32_32x32x16 (K from
 LDS as the A operand, Q from the accumulator registers as B), so each lane holds one query row's scores for 16 keys
 of each 32-key half; P V is O^T += V^T P^T with V^T from LDS (f16) and the f16 probabilities as B. Every K / V^T
-operand read from LDS feeds both row blocks' MFMAs. Keys go by tiles of 64 through three LDS buffers: tile j + 2 is
-written while tiles j and j + 1 are read, one workgroup barrier a tile.
+operand read from LDS feeds both row blocks' MFMAs.
+
+Keys go by tiles of 64 through three LDS buffers (a padded K image and a V^T image each). Staging is straight
+copies, 16 bytes a lane, with no conversion: the K image from K as it lies in memory (five 1 KiB pieces a wave, each
+lane loading the 16 bytes its LDS slot holds), the V^T image from the f16 V^T tile images that vt_image
+(attn_fwd64.hip) writes before the kernel runs (four contiguous 1 KiB pieces a wave). In iteration j the wave reads
+K(j + 1) and V^T(j), writes tile j + 2 (loaded into its staging registers during iteration j - 1) into the buffer
+of tile j - 1 and loads tile j + 3 into the staging registers; one workgroup barrier a tile. Loads past the
+workgroup's keys lie outside the buffer descriptors and load zeros. (LDS DMA would save the staging registers and
+the writes, but on this part it holds the shader clock near 1.9 GHz where register staging runs at 2.33 GHz.)
 
 Iteration j, with S_cur holding tile j's exponentials (f32, made against the running maximum known when they were
 made) and S_nxt receiving tile j + 1's scores:
-  phase QK: 32 MFMAs, S_nxt = K(j + 1) Q^T, beside the vector work: the staging of tile j + 2 (K as loaded, V
-            converted to f16 and transposed), P = f16(S_cur), the row sums of those f16 values (v_dot2), and the
-            loads of tile j + 3. Then the check: when some lane's sum over its 32 keys exceeds 256 (a score above the
+  phase QK: 32 MFMAs, S_nxt = K(j + 1) Q^T, beside the staging (the writes of tile j + 2, the loads of tile
+            j + 3), P = f16(S_cur) and the row sums of those f16 values. Then the check: when some lane's sum over its 32 keys exceeds 256 (a score above the
             running maximum by more than 8, base 2) or is not a number, the wave takes the exact path, which
             recomputes tile j's scores from LDS, masks them, moves the running maximum by the reference's rule (only
             when a score passes it by more than 8), rescales the outputs and sums, and makes the exponentials, P and
@@ -27,9 +34,9 @@ made) and S_nxt receiving tile j + 1's scores:
             wave does not see all of its keys).
 The loop is unrolled twice so that S_cur and S_nxt swap registers statically.
 
-Register map: a0..a127 the outputs O[rb][db] (32 head dims a block), a128..a191 Q[rb][kk], a192..a207 the LDS
-operand ring; v0..v127 the two score tiles, v128..v159 P[rb], v160..v207 staging, v208..v231 softmax state and
-temporaries; s60..s91 scalars. The C++ operands sit in the registers the clobber list leaves free.
+Register map: a0..a127 the outputs O[rb][db] (32 head dims a block), a128..a191 Q[rb][kk], a192..a223 the LDS
+operand ring; v0..v127 the two score tiles, v128..v159 P[rb], v160..v183 softmax state and temporaries,
+v184..v219 the staged tile; s60..s99 scalars. The C++ operands sit in the registers the clobber list leaves free.
 
 Run: python3 gen_attn_fwd64.py  (writes attn_fwd64_asm.inc beside this file; the Makefile reruns it when it changes)
 """
@@ -38,8 +45,11 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 K_ROW = 272             # LDS bytes of a K row (256 + 16 of padding: 16-byte reads down a column are conflict-free)
-K_TILE = 64 * K_ROW     # 17408
+K_TILE = 64 * K_ROW     # 17408: 17 pieces of 1 KiB
 V_TILE = 128 * 64 * 2   # 16384: V^T, 128 head dims x 64 keys in f16
+STAGING = os.environ.get("MAKO_FWD64_STAGING", "dma")   # "dma": LDS DMA, "reg": through the staging registers
+NBUF = 4 if STAGING == "dma" else 3   # LDS tile buffers
+DMA_PER_TILE = 9        # LDS DMA loads a wave issues a tile (5 K pieces, 4 V^T pieces)
 RING = 8                # LDS operand ring slots
 AHEAD = 6               # operand reads in flight ahead of their MFMAs (a slot is refilled two fragments after its
                         # last MFMA was issued)
@@ -74,36 +84,12 @@ def RINGR(s):
     return f"a[{192 + 4 * s}:{192 + 4 * s + 3}]"
 
 
-# Two staging sets (tiles alternate between them, so a tile's loads are issued two tiles ahead of its LDS writes):
-# K rows as loaded in the accumulator registers, V rows in vector registers.
-def KST(i, st):         # staged K of set st, key i of the thread's four
-    b = 224 + 16 * st + 4 * i
-    return f"a[{b}:{b + 3}]"
-
-
-def VST(i, p, st):      # staged V of set st, key i, dword p (head dims 2p, 2p + 1 of the thread's 8)
-    return f"v{176 + 16 * st + 4 * i + p}"
-
-
-def VSTQ(i, st):
-    b = 176 + 16 * st + 4 * i
-    return f"v[{b}:{b + 3}]"
-
-
-def VTO(e, half):       # transposed V, head dim e of the thread's 8: keys (0, 1) in half 0, (2, 3) in half 1
-    return f"v{160 + 2 * e + half}"
-
-
-def VTO2(e):
-    return f"v[{160 + 2 * e}:{161 + 2 * e}]"
-
-
-NEGMU = ("v208", "v209")   # -(running maximum) of the lane's row, 0 while it is -inf
-LSUM = ("v210", "v211")    # row sum over this lane's keys
-MAXV = ("v212", "v213")    # running maximum (base 2), -inf until a key was seen
-NINF = "v214"              # -inf
-ZERO = "v215"              # 0
-TMP = [f"v{216 + i}" for i in range(16)]   # v216 .. v231
+NEGMU = ("v160", "v161")   # -(running maximum) of the lane's row, 0 while it is -inf
+LSUM = ("v162", "v163")    # row sum over this lane's keys
+MAXV = ("v164", "v165")    # running maximum (base 2), -inf until a key was seen
+NINF = "v166"              # -inf
+ZERO = "v167"              # 0
+TMP = [f"v{168 + i}" for i in range(16)]   # v168 .. v183
 
 SJ = "s60"        # j
 SBK = "s61"       # buffer of the tile whose K is read next
@@ -111,20 +97,34 @@ SBV = "s62"       # buffer of the tile whose V^T is read next
 SBW = "s63"       # buffer written next
 S256 = "s64"      # 256.0f
 SONES = "s65"     # f16 pair (1, 1)
-SHIMASK = "s66"   # 0xffff0000
-SPLO = "s67"      # v_perm selector: the low halves of two dwords
-SPHI = "s68"      # v_perm selector: the high halves
-SJ0 = "s69"       # first key of the next tile (its mask)
-SJX = "s70"       # first key of the tile on the exact path
-SROT = {"w": ("s72", "s73"), "k": ("s74",), "v": ("s75",)}   # rotation increments, by role
+KRS = ("s68", "s69", "s70", "s71")   # buffer descriptor of K from the tile loaded next (4-aligned)
+VRS = ("s72", "s73", "s74", "s75")   # buffer descriptor of the V^T tile images from the tile loaded next
 ST = ["s76", "s77", "s78", "s79"]
 SCMP = ("s[80:81]", "s[82:83]")
+SJ0 = "s85"       # first key of the next tile (its mask)
+SJX = "s86"       # first key of the tile on the exact path
 SMASK = ("s[88:89]", "s[90:91]", "s[92:93]", "s[94:95]")  # lane masks of the key mask, in rotation
-SINC = {K_TILE: ("s84", "s85"), V_TILE: ("s86", "s87")}   # (step, wrap) of a buffer rotation, by stride
+SROT = {"k": "s96", "v": "s97", "wk": "s98", "wv": "s99"}   # rotation increments, by role
+SKW = "s66"       # DMA: LDS address of the K image of buffer SBW
+SKWW = "s67"      # DMA: SKW + 1 KiB x (wave index), this wave's first K piece
+SVWW = "s84"      # DMA: LDS address of this wave's 4 KiB of the V^T image of buffer SBW
 
-CLOBBER_V = 232
-CLOBBER_A = 256
-CLOBBER_S = (60, 96)
+
+def KSTG(m):      # staged K piece m (0..3: pieces w + 4 m; 4: piece 16)
+    return f"v[{184 + 4 * m}:{187 + 4 * m}]"
+
+
+def VSTG(i):      # staged V^T piece i of the wave's 4 KiB
+    return f"v[{204 + 4 * i}:{207 + 4 * i}]"
+
+
+def quad(r):
+    return f"s[{r[0][1:]}:{r[3][1:]}]"
+
+
+CLOBBER_V = 184 if STAGING == "dma" else 220
+CLOBBER_A = 224
+CLOBBER_S = (60, 100)
 
 
 class Emit:
@@ -144,71 +144,94 @@ def lbl(name):
 
 # ---- pieces (each returns a list of instructions) -----------------------------------------------------------------
 
-def rotate(sidx, role, regs):
-    """Moves the LDS addresses `regs` ((register, buffer stride) pairs) to the next of the three buffers; sidx holds
-    the current buffer index. The increments go through role-specific scalars, so rotations can be queued."""
-    tmps = SROT[role]
-    strides = sorted({st for _, st in regs})
-    tmp = dict(zip(strides, tmps))
-    ops = [f"s_cmp_eq_u32 {sidx}, 2"]
-    for st in strides:
-        ops.append(f"s_cselect_b32 {tmp[st]}, {SINC[st][1]}, {SINC[st][0]}")
-    ops += [f"v_add_u32 {r}, {tmp[st]}, {r}" for r, st in regs]
-    ops += [f"s_add_u32 {sidx}, {sidx}, 1", f"s_cmp_eq_u32 {sidx}, 3", f"s_cselect_b32 {sidx}, 0, {sidx}"]
+def rotate(sidx, role, regs, stride):
+    """Moves the LDS addresses `regs` to the next of the NBUF buffers (buffers are `stride` bytes apart); sidx holds
+    the current buffer index."""
+    t = SROT[role]
+    ops = [f"s_cmp_eq_u32 {sidx}, {NBUF - 1}", f"s_cselect_b32 {t}, {(-NBUF * stride) & 0xFFFFFFFF:#x}, 0",
+           f"s_add_u32 {t}, {t}, {stride:#x}"]
+    ops += [f"v_add_u32 {r}, {t}, {r}" for r in regs]
+    ops += [f"s_add_u32 {sidx}, {sidx}, 1", f"s_cmp_eq_u32 {sidx}, {NBUF}", f"s_cselect_b32 {sidx}, 0, {sidx}"]
     return ops
 
 
-WREGS = [("%[kw]", K_TILE), ("%[vwx]", V_TILE)]
-KREGS = [("%[kr]", K_TILE)]
-VREGS = [(f"%[vr{i}]", V_TILE) for i in range(4)]
+KREGS = ["%[kr]"]
+VREGS = [f"%[vr{i}]" for i in range(4)]
 
 
-def stage_loads(st):
-    """Staging set st gets the thread's four K rows (voffset %[st]) and four V rows (%[stv]), 16 bytes each, of the
-    next tile to load; both offsets then move on by a tile. Rows past the workgroup's keys lie outside the buffers
-    and load as zeros."""
-    ops = [f"buffer_load_dwordx4 {KST(i, st)}, %[st], %[krs], 0 offen offset:{256 * i}" for i in range(4)]
-    ops += [f"buffer_load_dwordx4 {VSTQ(i, st)}, %[stv], %[vrs], 0 offen offset:{256 * i}" for i in range(4)]
-    ops += ["v_add_u32 %[st], 0x4000, %[st]", "v_add_u32 %[stv], 0x4000, %[stv]"]
+def stage_loads(kregs=KSTG, vregs=VSTG):
+    """Loads the next tile into the staging registers, then moves the sources on by a tile. K: the wave's pieces w,
+    w + 4, w + 8, w + 12 of the 17 KiB padded image (%[kd*]: the byte of K a lane's LDS slot holds) and piece 16
+    (every wave loads it; they write the same bytes to the same place). V^T: the wave's 4 KiB of the tile image, as
+    four 1 KiB loads. Record counts shrink by a tile and stop at zero, so tiles past the keys load zeros."""
+    ops = [f"buffer_load_dwordx4 {kregs(m)}, %[kd{m}], {quad(KRS)}, 0 offen" for m in range(5)]
+    ops += [f"buffer_load_dwordx4 {vregs(i)}, %[vd], {quad(VRS)}, 0 offen offset:{1024 * i}" for i in range(4)]
+    for r in (KRS, VRS):
+        ops += [f"s_add_u32 {r[0]}, {r[0]}, 0x4000", f"s_addc_u32 {r[1]}, {r[1]}, 0",
+                f"s_sub_u32 {r[2]}, {r[2]}, 0x4000", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
     return ops
 
 
-def stage_convert(bf16, st):
-    """V of keys 0..3 (dword p: head dims 2p, 2p + 1) into f16 pairs of consecutive keys for each head dim
-    (bf16 -> f16 rounds toward zero, as the C++ kernels' staging does)."""
+WKREGS = ["%[kwa]", "%[kwb]"]
+WVREGS = ["%[vwa]"]
+
+
+def stage_writes(kregs=KSTG, vregs=VSTG):
+    """The staged tile into LDS buffer SBW (1 KiB a write, conflict-free), then the write addresses move to the next
+    buffer. %[kwa]: this wave's first K piece plus 16 bytes a lane, %[kwb]: piece 16; %[vwa]: its V^T 4 KiB."""
+    ops = [f"ds_write_b128 %[kwa], {kregs(m)} offset:{4096 * m}" for m in range(4)]
+    ops.append(f"ds_write_b128 %[kwb], {kregs(4)}")
+    ops += [f"ds_write_b128 %[vwa], {vregs(i)} offset:{1024 * i}" for i in range(4)]
+    wk, wv = SROT["wk"], SROT["wv"]
+    ops += [f"s_cmp_eq_u32 {SBW}, {NBUF - 1}",
+            f"s_cselect_b32 {wk}, {(-NBUF * K_TILE) & 0xFFFFFFFF:#x}, 0",
+            f"s_cselect_b32 {wv}, {(-NBUF * V_TILE) & 0xFFFFFFFF:#x}, 0",
+            f"s_add_u32 {wk}, {wk}, {K_TILE:#x}", f"s_add_u32 {wv}, {wv}, {V_TILE:#x}"]
+    ops += [f"v_add_u32 {r}, {wk}, {r}" for r in WKREGS] + [f"v_add_u32 {r}, {wv}, {r}" for r in WVREGS]
+    ops += [f"s_add_u32 {SBW}, {SBW}, 1", f"s_cmp_eq_u32 {SBW}, {NBUF}", f"s_cselect_b32 {SBW}, 0, {SBW}"]
+    return ops
+
+
+def dma_issue():
+    """LDS DMA loads of the next tile into buffer SBW (lane l of a load writes 16 bytes at M0 + offset + 16 l), then
+    the sources move on by a tile and the destinations to the next buffer. K: pieces w, w + 4, w + 8, w + 12 of the
+    17 KiB image at M0 = their LDS address, and piece 16 (every wave; the same bytes to the same place). V^T: the
+    wave's 4 KiB of the tile image, as four 1 KiB loads whose offset moves source and destination alike. A write of
+    M0 is read by an LDS load after one wait state. Record counts shrink by a tile and stop at zero."""
     ops = []
-    for p in range(4):
-        for lohi in range(2):
-            e = 2 * p + lohi
-            for half in range(2):
-                a, b = VST(2 * half, p, st), VST(2 * half + 1, p, st)
-                dst = VTO(e, half)
-                if bf16:
-                    if lohi == 0:
-                        ops += [f"v_lshlrev_b32 {TMP[12]}, 16, {a}", f"v_lshlrev_b32 {TMP[13]}, 16, {b}"]
-                    else:
-                        ops += [f"v_and_b32 {TMP[12]}, {SHIMASK}, {a}", f"v_and_b32 {TMP[13]}, {SHIMASK}, {b}"]
-                    ops.append(f"v_cvt_pkrtz_f16_f32 {dst}, {TMP[12]}, {TMP[13]}")
-                else:
-                    ops.append(f"v_perm_b32 {dst}, {b}, {a}, {SPHI if lohi else SPLO}")
+    for m in range(4):
+        ops += [f"s_add_u32 m0, {SKWW}, {4096 * m}" if m else f"s_mov_b32 m0, {SKWW}", "s_nop 0",
+                f"buffer_load_dwordx4 %[kd{m}], {quad(KRS)}, 0 offen lds"]
+    ops += [f"s_add_u32 m0, {SKW}, {16 * 1024}", "s_nop 0", f"buffer_load_dwordx4 %[kd4], {quad(KRS)}, 0 offen lds"]
+    ops += [f"s_mov_b32 m0, {SVWW}", "s_nop 0"]
+    ops += [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds" for i in range(4)]
+    for r in (KRS, VRS):
+        ops += [f"s_add_u32 {r[0]}, {r[0]}, 0x4000", f"s_addc_u32 {r[1]}, {r[1]}, 0",
+                f"s_sub_u32 {r[2]}, {r[2]}, 0x4000", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
+    wk, wv = SROT["wk"], SROT["wv"]
+    ops += [f"s_cmp_eq_u32 {SBW}, {NBUF - 1}",
+            f"s_cselect_b32 {wk}, {(-NBUF * K_TILE) & 0xFFFFFFFF:#x}, 0",
+            f"s_cselect_b32 {wv}, {(-NBUF * V_TILE) & 0xFFFFFFFF:#x}, 0",
+            f"s_add_u32 {wk}, {wk}, {K_TILE:#x}", f"s_add_u32 {wv}, {wv}, {V_TILE:#x}",
+            f"s_add_u32 {SKW}, {SKW}, {wk}", f"s_add_u32 {SKWW}, {SKWW}, {wk}", f"s_add_u32 {SVWW}, {SVWW}, {wv}",
+            f"s_add_u32 {SBW}, {SBW}, 1", f"s_cmp_eq_u32 {SBW}, {NBUF}", f"s_cselect_b32 {SBW}, 0, {SBW}"]
     return ops
 
 
-def stage_writes(st):
-    """K rows to their LDS rows; V^T: head dim 8 c + e of the thread's keys at %[vwx] ^ 16 e (the chunk swizzle of
-    row d is (d % 8) ^ (d / 8 % 4), here e ^ a per-lane constant folded into %[vwx]) plus the row, 128 e."""
-    ops = [f"ds_write_b128 %[kw], {KST(i, st)} offset:{K_ROW * i}" for i in range(4)]
-    for e in range(8):
-        t = TMP[8 + (e % 4)]
-        ops.append(f"v_xor_b32 {t}, {16 * e}, %[vwx]")
-        ops.append(f"ds_write_b64 {t}, {VTO2(e)} offset:{128 * e}")
-    return ops
+def staging():
+    """A tile's staging in the loop. DMA: load tile j + 3 (waited for before barrier j + 2). Registers: wait for the
+    staged tile j + 2 (loaded an iteration ago), write it, load tile j + 3."""
+    if STAGING == "dma":
+        return dma_issue()
+    return ["s_waitcnt vmcnt(0)"] + stage_writes() + stage_loads()
 
 
-def staging(bf16, st):
-    """A tile's staging in the loop (staging set st): wait for its loads (the next tile's stay in flight), convert,
-    write to LDS and rotate the write addresses; then load the tile two ahead into the same set."""
-    return (["s_waitcnt vmcnt(8)"] + stage_convert(bf16, st) + stage_writes(st) + rotate(SBW, "w", WREGS))
+def barrier():
+    """The wave's LDS writes and reads are done (the buffer read last is written after the barrier); then the
+    barrier."""
+    if STAGING == "dma":
+        return [f"s_waitcnt vmcnt({DMA_PER_TILE}) lgkmcnt(0)", "s_barrier"]
+    return ["s_waitcnt lgkmcnt(0)", "s_barrier"]
 
 
 def k_reads(addr):
@@ -309,9 +332,11 @@ def exps(sbuf):
 
 
 def pack_and_sum(sbuf):
-    """P[rb] = f16 pairs of tile S(sbuf)'s exponentials, and the sum a row block of the f16 values (v_dot2 against
-    (1, 1), four chains) into TMP[0] (rb 0) and TMP[4] (rb 1)."""
-    ops = [f"v_mov_b32 {TMP[q]}, 0" for q in range(8)]
+    """P[rb] = f16 pairs of tile S(sbuf)'s exponentials, and the sum a row block of those f16 values, exactly in f32
+    (v_dot2 against (1, 1), four chains a row block, the first of each with a zero addend), into TMP[0] (rb 0) and
+    TMP[4] (rb 1). A dot instruction reads a vector register written by the instruction before it after one wait
+    state, and its result is read by other vector instructions after three."""
+    ops = []
     for rb in range(2):
         for cc in range(4):
             t, r0 = cc // 2, 8 * (cc % 2)
@@ -322,7 +347,8 @@ def pack_and_sum(sbuf):
         for rb in range(2):
             for i in range(4):
                 acc = TMP[4 * rb + i]
-                ops.append(f"v_dot2_f32_f16 {acc}, {P(rb, cc, i)}, {SONES}, {acc}")
+                ops.append(f"v_dot2_f32_f16 {acc}, {P(rb, cc, i)}, {SONES}, {acc if cc else 0}")
+    ops.append("s_nop 2")
     for rb in range(2):
         a = TMP[4 * rb: 4 * rb + 4]
         ops += [f"v_add_f32 {a[0]}, {a[0]}, {a[1]}", f"v_add_f32 {a[2]}, {a[2]}, {a[3]}",
@@ -335,10 +361,11 @@ def wait_mfma():
     return ["s_nop 7", "s_nop 7", "s_nop 4"]
 
 
-def exact_tile(e, dtype, sbuf, kaddr, j0):
+def exact_tile(e, dtype, sbuf, kaddr, j0, first=False):
     """The exact path for a tile (K at LDS address kaddr, first key in scalar j0): its raw scores into S(sbuf), the
     mask, each row's maximum, the reference's rule for moving the running maximum (outputs and sums rescaled when it
-    moves), the exponentials, P and the sums (TMP[0], TMP[4])."""
+    moves), the exponentials, P and the sums (TMP[0], TMP[4]). first: the wave's first tile, where the outputs and
+    sums are still zero and need no rescaling."""
     interleave(e, k_reads(kaddr), qk_mfmas(dtype, sbuf), [])
     for op in wait_mfma() + mask(sbuf, j0):
         e(op)
@@ -371,9 +398,10 @@ def exact_tile(e, dtype, sbuf, kaddr, j0):
         e(f"v_cndmask_b32 {MAXV[rb]}, {MAXV[rb]}, {mx}, vcc")
         e(f"v_sub_f32 {TMP[7]}, 0, {mx}")
         e(f"v_cndmask_b32 {NEGMU[rb]}, {NEGMU[rb]}, {TMP[7]}, vcc")
-        e(f"v_mul_f32 {LSUM[rb]}, {LSUM[rb]}, {f}")
+        if not first:
+            e(f"v_mul_f32 {LSUM[rb]}, {LSUM[rb]}, {f}")
     # rescale the outputs (the MFMAs that wrote them were issued before the last barrier)
-    for rb in range(2):
+    for rb in range(2 if not first else 0):
         f = TMP[8 + rb]
         for i in range(64):
             a, tv = f"a{64 * rb + i}", TMP[10 + (i % 4)]
@@ -439,64 +467,86 @@ def epilogue(e, out_dtype):
 # ---- the kernel body ----------------------------------------------------------------------------------------------
 
 def body(in_dtype, out_dtype):
-    bf16 = in_dtype == "bf16"
     e = Emit()
     e(f"s_mov_b32 {S256}, 0x43800000")
     e(f"s_mov_b32 {SONES}, 0x3c003c00")
-    e(f"s_mov_b32 {SHIMASK}, 0xffff0000")
-    e(f"s_mov_b32 {SPLO}, 0x05040100")
-    e(f"s_mov_b32 {SPHI}, 0x07060302")
-    for st, (step, wrap) in SINC.items():
-        e(f"s_mov_b32 {step}, {st:#x}")
-        e(f"s_mov_b32 {wrap}, {(-2 * st) & 0xFFFFFFFF:#x}")
     e(f"v_mov_b32 {NINF}, 0xff800000")
     e(f"v_mov_b32 {ZERO}, 0")
     for rb in range(2):
         e(f"v_mov_b32 {NEGMU[rb]}, 0")
         e(f"v_mov_b32 {LSUM[rb]}, 0")
         e(f"v_mov_b32 {MAXV[rb]}, {NINF}")
-    # Q into the accumulator registers (rows past n_q load as zeros); outputs zeroed
+    # load sources of tile 0
+    for r, pre in ((KRS, "k"), (VRS, "v")):
+        e(f"s_mov_b32 {r[0]}, %[{pre}b0]")
+        e(f"s_mov_b32 {r[1]}, %[{pre}b1]")
+        e(f"s_mov_b32 {r[2]}, %[{pre}n]")
+        e(f"s_mov_b32 {r[3]}, 0x20000")
+    e(f"s_mov_b32 {SBW}, 0")
+    # Q into the accumulator registers (rows past n_q load as zeros)
     e(f"v_add_u32 {TMP[0]}, 0x2000, %[qo]")
     for rb in range(2):
         for kk in range(8):
             e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen offset:{32 * kk}")
-    # tiles 0 and 1 through the two staging sets, then tiles 2 and 3 in flight
-    for op in stage_loads(0) + stage_loads(1):
+    if STAGING == "dma":
+        # tiles 0, 1, 2 into buffers 0, 1, 2; outputs zeroed meanwhile; the barrier waits for tiles 0 and 1
+        e(f"s_mov_b32 {SKW}, %[skw]")
+        e(f"s_mov_b32 {SKWW}, %[skww]")
+        e(f"s_mov_b32 {SVWW}, %[svww]")
+        for _ in range(3):
+            for op in dma_issue():
+                e(op)
+        for i in range(128):
+            e(f"v_accvgpr_write_b32 a{i}, 0")
+    else:
+        # tiles 0 and 1 into the (still free) score registers, tile 2 into the staging registers; outputs zeroed
+        # meanwhile; tiles 0 and 1 written to buffers 0, 1
+        early_staging(e)
+    body_rest(e, in_dtype, out_dtype)
+    return e.out
+
+
+def early_staging(e):
+
+    def early(t):
+        return (lambda m: f"v[{36 * t + 4 * m}:{36 * t + 4 * m + 3}]",
+                lambda i: f"v[{36 * t + 20 + 4 * i}:{36 * t + 23 + 4 * i}]")
+    for t in range(2):
+        for op in stage_loads(*early(t)):
+            e(op)
+    for op in stage_loads():
         e(op)
     for i in range(128):
         e(f"v_accvgpr_write_b32 a{i}, 0")
-    e(f"s_mov_b32 {SBW}, 0")
-    e("s_waitcnt vmcnt(0)")
-    for op in stage_convert(bf16, 0) + stage_writes(0) + rotate(SBW, "w", WREGS):
-        e(op)
-    for op in stage_convert(bf16, 1) + stage_writes(1) + rotate(SBW, "w", WREGS):
-        e(op)
-    for op in stage_loads(0) + stage_loads(1):
-        e(op)
+    e("s_waitcnt vmcnt(9)")
+    for t in range(2):
+        for op in stage_writes(*early(t)):
+            e(op)
+
+
+def body_rest(e, in_dtype, out_dtype):
     e(f"s_mov_b32 {SJ}, 0")
     e(f"s_mov_b32 {SBK}, 0")
     e(f"s_mov_b32 {SBV}, 0")
-    e("s_waitcnt lgkmcnt(0)")
-    e("s_barrier")
+    for op in barrier():
+        e(op)
     e("s_cmp_eq_u32 %[ntw], 0")
     e(f"s_cbranch_scc1 {lbl('L_tail')}")
     # tile 0 by the exact path
     e(f"s_mov_b32 {SJX}, 0")
-    exact_tile(e, in_dtype, 0, "%[kr]", SJX)
+    exact_tile(e, in_dtype, 0, "%[kr]", SJX, first=True)
     e(f"v_add_f32 {LSUM[0]}, {LSUM[0]}, {TMP[0]}")
     e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
 
-    def iteration(par, variant):
+    def iteration(par, variant, masked_next=False):
         """Iteration j with S_cur = S(par), S_nxt = S(1 - par). variant: 'plain' (tile j + 1 fully seen by the
         wave's rows), 'masked', 'last' (no tile j + 1), 'first' (j = 0: tile 0's P and sums came from the exact
-        path)."""
+        path; masked_next: tile 1 needs the mask)."""
         cur, nxt = par, 1 - par
         tag = f"{variant}{par}"
-        # phase QK (tile j's staging set is j % 2 = par)
-        valu = staging(bf16, par)
+        valu = staging()
         if variant != "first":
             valu += pack_and_sum(cur)
-        valu += stage_loads(par)
         if variant != "last":
             interleave(e, k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu)
         else:
@@ -512,14 +562,14 @@ def body(in_dtype, out_dtype):
             e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
             e.label(f"L_back_{tag}")
         if variant != "last":
-            for op in rotate(SBK, "k", KREGS):
+            for op in rotate(SBK, "k", KREGS, K_TILE):
                 e(op)
         # phase PV
         valu = []
         if variant != "last":
-            valu = ["s_nop 7", "s_nop 7"] + (mask(nxt, SJ0) if variant == "masked" else []) + exps(nxt)
+            valu = ["s_nop 7", "s_nop 7"] + (mask(nxt, SJ0) if variant == "masked" or masked_next else []) + exps(nxt)
         interleave(e, v_reads(), pv_mfmas(), valu)
-        for op in rotate(SBV, "v", VREGS):
+        for op in rotate(SBV, "v", VREGS, V_TILE):
             e(op)
 
     def exact_block(par, variant):
@@ -538,8 +588,8 @@ def body(in_dtype, out_dtype):
         """Barrier, then the variant of iteration SJ: this wave's last, one whose next tile needs the mask, plain."""
         name = "first" if first else f"iter{par}"
         e.label(f"L_{name}")
-        e("s_waitcnt lgkmcnt(0)")
-        e("s_barrier")
+        for op in barrier():
+            e(op)
         e(f"s_add_u32 {ST[1]}, {SJ}, 1")
         e(f"s_cmp_ge_u32 {ST[1]}, %[ntw]")
         e(f"s_cbranch_scc1 {lbl(f'L_last_{name}')}")
@@ -551,24 +601,13 @@ def body(in_dtype, out_dtype):
         e(f"s_branch {lbl(f'L_next_{name}')}")
         e.label(f"L_masked_{name}")
         if first:
-            iteration_first_masked()
+            iteration(0, "first", masked_next=True)
         else:
             iteration(par, "masked")
         e.label(f"L_next_{name}")
         e(f"s_add_u32 {SJ}, {SJ}, 1")
 
-    def iteration_first_masked():
-        # as iteration(0, 'first') with the next tile masked
-        valu = staging(bf16, 0) + stage_loads(0)
-        interleave(e, k_reads("%[kr]"), qk_mfmas(in_dtype, 1), valu)
-        for op in rotate(SBK, "k", KREGS):
-            e(op)
-        valu = ["s_nop 7", "s_nop 7"] + mask(1, SJ0) + exps(1)
-        interleave(e, v_reads(), pv_mfmas(), valu)
-        for op in rotate(SBV, "v", VREGS):
-            e(op)
-
-    for op in rotate(SBK, "k", KREGS):
+    for op in rotate(SBK, "k", KREGS, K_TILE):
         e(op)
     dispatch(0, first=True)
     dispatch(1)
@@ -576,11 +615,10 @@ def body(in_dtype, out_dtype):
     e(f"s_branch {lbl('L_iter1')}")
     # the last iteration of the wave, by entry point
     e.label("L_last_first")
-    valu = staging(bf16, 0) + stage_loads(0)
-    for op in valu:
+    for op in staging():
         e(op)
     interleave(e, v_reads(), pv_mfmas(), [])
-    for op in rotate(SBV, "v", VREGS):
+    for op in rotate(SBV, "v", VREGS, V_TILE):
         e(op)
     e(f"s_add_u32 {SJ}, {SJ}, 1")
     e(f"s_branch {lbl('L_tail')}")
@@ -592,24 +630,16 @@ def body(in_dtype, out_dtype):
     for par in (0, 1):
         for variant in ("plain", "masked", "last"):
             exact_block(par, variant)
-    # staging-only iterations for the tiles the workgroup's other waves still compute (staging set j % 2)
+    # load-only iterations for the tiles the workgroup's other waves still compute
     e.label("L_tail")
-    e(f"s_and_b32 {ST[3]}, {SJ}, 1")
-    e(f"s_cmp_eq_u32 {ST[3]}, 1")
-    e(f"s_cbranch_scc1 {lbl('L_tail1')}")
-    for par in (0, 1):
-        e.label(f"L_tail{par}")
-        e("s_cmp_ge_u32 %s, %%[nt]" % SJ)
-        e(f"s_cbranch_scc1 {lbl('L_epi')}")
-        e("s_waitcnt lgkmcnt(0)")
-        e("s_barrier")
-        for op in staging(bf16, par) + stage_loads(par):
-            e(op)
-        e(f"s_add_u32 {SJ}, {SJ}, 1")
-    e(f"s_branch {lbl('L_tail0')}")
+    e("s_cmp_ge_u32 %s, %%[nt]" % SJ)
+    e(f"s_cbranch_scc1 {lbl('L_epi')}")
+    for op in barrier() + staging():
+        e(op)
+    e(f"s_add_u32 {SJ}, {SJ}, 1")
+    e(f"s_branch {lbl('L_tail')}")
     e.label("L_epi")
     epilogue(e, out_dtype)
-    return e.out
 
 
 def clobbers():
@@ -643,6 +673,8 @@ def main():
             out.append('    ""')
             out.append("")
     out.append(f"#define MAKO_FWD64_CLOBBERS {clobbers()}")
+    out.append(f"#define MAKO_FWD64_DMA {1 if STAGING == 'dma' else 0}")
+    out.append(f"#define MAKO_FWD64_NBUF {NBUF}")
     out.append("")
     with open(os.path.join(HERE, "attn_fwd64_asm.inc"), "w") as f:
         f.write("\n".join(out))

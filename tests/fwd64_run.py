@@ -1,0 +1,202 @@
+"""Runs flash_fwd_r64's generated stream on the emulator (fwd64_emu.py) for a small case, with the per-lane operands
+attn_fwd64.hip computes restated here, and compares the outputs and LSE with the oracle's."""
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(os.path.dirname(HERE), "mako-common_amd", "csrc"))
+import fwd64_emu as E  # noqa: E402
+import gen_attn_fwd64 as G  # noqa: E402
+import oracle as O  # noqa: E402
+
+VOPS = ['kr', 'vr0', 'vr1', 'vr2', 'vr3'] + ([] if G.STAGING == 'dma' else ['kwa', 'kwb', 'vwa']) + [
+    'kd0', 'kd1', 'kd2', 'kd3', 'kd4', 'vd', 'lim0', 'lim1', 'kr0', 'qo', 'oo', 'lo0', 'lo1', 'swp']
+SOPS = {'qrs': 's[0:3]', 'ors': 's[12:15]', 'lrs': 's[16:19]', 'c': 's20',
+        'nt': 's21', 'ntw': 's22', 'lmin': 's23', 'has_lse': 's24', 'so1': 's25', 'kb0': 's26', 'kb1': 's27',
+        'kn': 's28', 'vb0': 's29', 'vb1': 's30', 'vn': 's31', 'skw': 's32', 'skww': 's33', 'svww': 's34'}
+VREG = {n: f'v{G.CLOBBER_V + i}' for i, n in enumerate(VOPS)}
+
+
+def program(ind, outd):
+    lines = G.body(ind, outd)
+    out = []
+    for ln in lines:
+        ln = ln.replace('%=', '0')
+        for n, r in VREG.items():
+            ln = ln.replace(f'%[{n}]', r)
+        for n, r in SOPS.items():
+            ln = ln.replace(f'%[{n}]', r)
+        out.append(ln)
+    return E.parse(out)
+
+
+def slot_of(r):
+    return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1)
+
+
+def lim_of(pos, n_k, block):
+    return n_k if pos >= block else min(n_k, pos + 1)
+
+
+def vt_swz(d):
+    return (d & 7) ^ ((d >> 3) & 3)
+
+
+def vt_images(vb, kv, n_k, k_pad, ind):
+    """The f16 V^T tile images: [kv][tile][d 128][slot 8][8 keys], slot s of row d holding keys 8 (s ^ vt_swz(d))."""
+    nti = (n_k + 63) // 64
+    if ind == 'bf16':
+        f = vb.astype(np.uint32) << 16
+        vals = f.view(np.float32)
+        h = E.f16_rtz(vals).view(np.uint16).reshape(kv, k_pad, 128)
+    else:
+        h = vb.reshape(kv, k_pad, 128).astype(np.uint16)
+    img = np.zeros((kv, nti, 128, 8, 8), np.uint16)
+    for t in range(nti):
+        for d in range(128):
+            for sl in range(8):
+                c = sl ^ vt_swz(d)
+                keys = t * 64 + 8 * c + np.arange(8)
+                ok = keys < n_k
+                img[:, t, d, sl, ok] = h[:, keys[ok], d]
+    return img, nti
+
+
+def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verbose=True, kgrow=0.0):
+    rng = np.random.default_rng(seed)
+    dt = O.BF16 if ind == 'bf16' else O.F16
+    q_pad = (S_q + 63) // 64 * 64
+    k_pad = (S_k + 127) // 128 * 128
+    conv = O.to_bf16_bits if ind == 'bf16' else O.to_f16_bits
+    qb = conv(rng.standard_normal((heads, q_pad, 128), dtype=np.float32))
+    kf = rng.standard_normal((kv, k_pad, 128), dtype=np.float32)
+    if kgrow:
+        kf *= (1 + kgrow * (np.arange(k_pad) // 64))[None, :, None].astype(np.float32)
+    kb = conv(kf)
+    vb = conv(rng.standard_normal((kv, k_pad, 128), dtype=np.float32))
+    width = heads * 128
+    so = 4 if outd == 'f32' else 2
+    # global memory
+    img, nti = vt_images(vb, kv, S_k, k_pad, ind)
+    sizes = [qb.nbytes, kb.nbytes, vb.nbytes, S_q * width * so + 4096, heads * S_q * 4 + 4096, img.nbytes + 4096]
+    offs = np.cumsum([4096] + [((x + 4095) // 4096) * 4096 for x in sizes])
+    Q0, K0, V0, O0, L0, I0 = [int(x) for x in offs[:6]]
+    mem = E.Mem(int(offs[-1]) + 4096)
+    mem.b[Q0:Q0 + qb.nbytes] = qb.view(np.uint8).ravel()
+    mem.b[K0:K0 + kb.nbytes] = kb.view(np.uint8).ravel()
+    mem.b[V0:V0 + vb.nbytes] = vb.view(np.uint8).ravel()
+    mem.b[I0:I0 + img.nbytes] = img.view(np.uint8).ravel()
+    fill = np.full(S_q * width, np.nan, np.float32) if so == 4 else None
+    if so == 4:
+        mem.b[O0:O0 + fill.nbytes] = fill.view(np.uint8)
+    prog, labels = program(ind, outd)
+    group = heads // kv
+    hq = 4 if group % 4 == 0 else 2 if group % 2 == 0 else 1
+    rows_wg = 256 // hq
+    n_qblk = (S_q + rows_wg - 1) // rows_wg
+    n_hg = heads // hq
+    c = np.float32(1.0 / np.sqrt(128.0)) * np.float32(1.4426950408889634)
+    lane = np.arange(64)
+    g, c32 = lane >> 5, lane & 31
+    lbase = 0
+    vbase = lbase + G.NBUF * G.K_TILE
+    t0 = time.time()
+    n_instr = 0
+    worst = {}
+    for wid in range(n_hg * n_qblk):
+        if n_hg % 8 == 0:
+            x, kx, per = wid % 8, wid // 8, n_hg // 8
+            if block == 0:
+                hg, qbk = x + 8 * (kx // n_qblk), kx % n_qblk
+            else:
+                hg, qbk = x + 8 * (kx % per), n_qblk - 1 - kx // per
+        else:
+            hg, qbk = wid % n_hg, n_qblk - 1 - wid // n_hg
+        emu = E.Emu(prog, labels, mem, G.NBUF * (G.K_TILE + G.V_TILE))
+        waves = []
+        for w in range(4):
+            W = E.Wave(w)
+            tid = 64 * w + lane
+            h = hg * hq + w % hq
+            kvh = hg * hq // group
+            wg_q0 = qbk * rows_wg
+            q0 = wg_q0 + (w // hq) * 64
+            wg_last = q_pos0 + min(wg_q0 + rows_wg, S_q) - 1
+            n_keys = S_k if wg_last >= block else min(S_k, wg_last + 1)
+            live = q0 < S_q
+            w_last = q_pos0 + min(q0 + 64, S_q) - 1
+            w_keys = 0 if not live else (S_k if w_last >= block else min(S_k, w_last + 1))
+            nt, ntw = (n_keys + 63) // 64, (w_keys + 63) // 64
+            p0 = q_pos0 + q0
+            lmin = lim_of(p0, S_k, block)
+            lim0 = np.array([lim_of(p0 + cc, S_k, block) for cc in c32]) - 8 * g
+            lim1 = np.array([lim_of(p0 + 32 + cc, S_k, block) for cc in c32]) - 8 * g
+            kr = lbase + c32 * G.K_ROW + 16 * g
+            sw = np.array([vt_swz(x) for x in c32])
+            vr = [vbase + c32 * 128 + ((((2 * cc + g) ^ sw) & 7) << 4) for cc in range(4)]
+
+            def kd_of(i):
+                b = 1024 * i + 16 * lane
+                R, c = b // G.K_ROW, (b % G.K_ROW) // 16
+                return np.array([slot_of(int(r)) for r in R]) * 256 + 16 * np.where(c < 16, c, 0)
+            kds = [kd_of(w + 4 * m) for m in range(4)] + [kd_of(16)]
+            vd = 4096 * w + 16 * lane
+            qo = ((q0 + c32) * 128 + 8 * g) * 2
+            oo = (q0 + c32) * width * so + (h * 128 + 4 * g) * so
+            so1 = 32 * width * so
+            lo0 = np.where(q0 + c32 < S_q, (h * S_q + q0 + c32) * 4, 0xffffffff)
+            lo1 = np.where(q0 + 32 + c32 < S_q, (h * S_q + q0 + 32 + c32) * 4, 0xffffffff)
+            swp = (lane ^ 32) * 4
+            vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], vr2=vr[2], vr3=vr[3], kd0=kds[0], kd1=kds[1], kd2=kds[2],
+                        kd3=kds[3], kd4=kds[4], vd=vd, lim0=lim0, lim1=lim1, kr0=kr, qo=qo, oo=oo, lo0=lo0, lo1=lo1,
+                        swp=swp)
+            if G.STAGING != 'dma':
+                vals.update(kwa=lbase + 1024 * w + 16 * lane, kwb=lbase + 16384 + 16 * lane,
+                            vwa=vbase + 4096 * w + 16 * lane)
+            for n, arr in vals.items():
+                W.v[int(VREG[n][1:])] = np.asarray(arr, np.int64).astype(np.uint32) if np.ndim(arr) else \
+                    np.full(64, int(arr) & 0xFFFFFFFF, np.uint32)
+
+            def rs(sidx, base, nbytes):
+                W.s[sidx] = base & 0xFFFFFFFF
+                W.s[sidx + 1] = (base >> 32) & 0xFFFF
+                W.s[sidx + 2] = nbytes & 0xFFFFFFFF
+                W.s[sidx + 3] = 0x00020000
+            rs(0, Q0 + h * q_pad * 256, S_q * 256)
+            kbase = K0 + kvh * k_pad * 256
+            ibase = I0 + kvh * nti * 16384
+            W.s[26], W.s[27], W.s[28] = kbase & 0xFFFFFFFF, (kbase >> 32) & 0xFFFF, n_keys * 256
+            W.s[29], W.s[30], W.s[31] = ibase & 0xFFFFFFFF, (ibase >> 32) & 0xFFFF, nt * 16384
+            W.s[32], W.s[33], W.s[34] = lbase, lbase + 1024 * w, vbase + 4096 * w
+            rs(12, O0, S_q * width * so)
+            rs(16, L0, heads * S_q * 4)
+            W.s[20] = int(np.float32(c).view(np.uint32))
+            W.s[21], W.s[22], W.s[23], W.s[24], W.s[25] = nt, ntw, lmin, 1, so1
+            waves.append(W)
+        emu.run_wg(waves)
+        n_instr += emu.count
+        for k_, v_ in emu.conflicts.items():
+            worst[k_] = max(worst.get(k_, 1), v_)
+    if verbose:
+        print(f'emulated {n_instr} wave-instructions in {time.time() - t0:.1f} s; LDS worst multiplicity {worst}')
+    if so == 4:
+        o = mem.b[O0:O0 + S_q * width * 4].view(np.float32).reshape(S_q, width).astype(np.float64)
+    else:
+        bitsv = mem.b[O0:O0 + S_q * width * 2].view(np.uint16)
+        o = O.bits_to_f32(bitsv, dt).reshape(S_q, width).astype(np.float64)
+    lse = mem.b[L0:L0 + heads * S_q * 4].view(np.float32).reshape(heads, S_q).astype(np.float64)
+    want_o, want_l = O.attn_dense(qb, kb, vb, n_q=S_q, q_pad=q_pad, n_k=S_k, k_pad=k_pad, heads=heads, kv_heads=kv,
+                                  q_pos0=q_pos0, block=block, dim=128, dtype=dt)
+    err = np.abs(o - want_o)
+    bad = ~(err <= 2e-3 + 1e-2 * np.abs(want_o))
+    lerr = np.abs(lse - want_l)
+    lbad = ~(lerr <= 1e-3) & np.isfinite(want_l)
+    if verbose:
+        print(f'h{heads} kv{kv} q{S_q} k{S_k} p{q_pos0} b{block}: out bad {bad.sum()} / {bad.size} (max err {np.nanmax(err):.3g}), '
+          f'lse bad {lbad.sum()} (max {np.nanmax(np.where(np.isfinite(want_l), lerr, 0)):.3g})')
+    return dict(out_bad=int(bad.sum()), lse_bad=int(lbad.sum()), lds_worst=worst, max_err=float(np.nanmax(err)))
+
+
