@@ -24,8 +24,8 @@ the writes, but on this part it holds the shader clock near 1.9 GHz where regist
 
 Iteration j, with S_cur holding tile j's exponentials (f32, made against the running maximum known when they were
 made) and S_nxt receiving tile j + 1's scores:
-  phase QK: 32 MFMAs, S_nxt = K(j + 1) Q^T, beside the staging (the writes of tile j + 2, the loads of tile
-            j + 3), P = f16(S_cur) and the row sums of those f16 values. Then the check: when some lane's sum over its 32 keys exceeds 256 (a score above the
+  phase QK: 32 MFMAs, S_nxt = K(j + 1) Q^T, beside the staging of tile j + 3, P = f16(S_cur) and the row sums
+            of S_cur (f32, as the reference sums them). Then the check: when some lane's sum over its 32 keys exceeds 256 (a score above the
             running maximum by more than 8, base 2) or is not a number, the wave takes the exact path, which
             recomputes tile j's scores from LDS, masks them, moves the running maximum by the reference's rule (only
             when a score passes it by more than 8), rescales the outputs and sums, and makes the exponentials, P and
@@ -96,7 +96,6 @@ SBK = "s61"       # buffer of the tile whose K is read next
 SBV = "s62"       # buffer of the tile whose V^T is read next
 SBW = "s63"       # buffer written next
 S256 = "s64"      # 256.0f
-SONES = "s65"     # f16 pair (1, 1)
 KRS = ("s68", "s69", "s70", "s71")   # buffer descriptor of K from the tile loaded next (4-aligned)
 VRS = ("s72", "s73", "s74", "s75")   # buffer descriptor of the V^T tile images from the tile loaded next
 ST = ["s76", "s77", "s78", "s79"]
@@ -332,10 +331,9 @@ def exps(sbuf):
 
 
 def pack_and_sum(sbuf):
-    """P[rb] = f16 pairs of tile S(sbuf)'s exponentials, and the sum a row block of those f16 values, exactly in f32
-    (v_dot2 against (1, 1), four chains a row block, the first of each with a zero addend), into TMP[0] (rb 0) and
-    TMP[4] (rb 1). A dot instruction reads a vector register written by the instruction before it after one wait
-    state, and its result is read by other vector instructions after three."""
+    """P[rb] = f16 pairs of tile S(sbuf)'s exponentials, and the sum a row block of the f32 exponentials (as the
+    reference sums them, ops.metal:326-331; P V multiplies their f16 roundings) into TMP[0] (rb 0) and TMP[4] (rb 1):
+    four chains of adds a row block, interleaved, so no add waits on the one before it."""
     ops = []
     for rb in range(2):
         for cc in range(4):
@@ -343,12 +341,13 @@ def pack_and_sum(sbuf):
             for i in range(4):
                 ops.append(f"v_cvt_pk_f16_f32 {P(rb, cc, i)}, {S(sbuf, rb, t, r0 + 2 * i)}, "
                            f"{S(sbuf, rb, t, r0 + 2 * i + 1)}")
-    for cc in range(4):
+    vals = {rb: [S(sbuf, rb, t, r) for t in range(2) for r in range(16)] for rb in range(2)}
+    for k in range(1, 8):       # chain c of row block rb sums values c, c + 4, c + 8, ...
         for rb in range(2):
-            for i in range(4):
-                acc = TMP[4 * rb + i]
-                ops.append(f"v_dot2_f32_f16 {acc}, {P(rb, cc, i)}, {SONES}, {acc if cc else 0}")
-    ops.append("s_nop 2")
+            for c in range(4):
+                acc = TMP[4 * rb + c]
+                first = vals[rb][c] if k == 1 else acc
+                ops.append(f"v_add_f32 {acc}, {first}, {vals[rb][4 * k + c]}")
     for rb in range(2):
         a = TMP[4 * rb: 4 * rb + 4]
         ops += [f"v_add_f32 {a[0]}, {a[0]}, {a[1]}", f"v_add_f32 {a[2]}, {a[2]}, {a[3]}",
@@ -413,45 +412,28 @@ def exact_tile(e, dtype, sbuf, kaddr, j0, first=False):
 
 
 def epilogue(e, out_dtype):
-    """Normalise and store this wave's rows of O (rows past n_q fall outside the output buffer and are dropped),
-    then the LSE (offsets of rows past n_q are outside its buffer)."""
+    """Normalise and store this wave's rows of O, then the LSE. The rows go through LDS (free once every wave has
+    passed the barrier here with its loads landed): each lane writes its 4-dim pieces of rows c32 and c32 + 32 into
+    the wave's region (row-major, 16-byte chunk c of row R at c ^ (R % 8), so the writes of a row group hit distinct
+    banks), then reads back whole-row chunks, so each global store writes 1 KiB of contiguous row segments (4 rows of
+    bf16 / f16, 2 of f32) instead of 16 bytes of each of 32 rows. Rows past n_q fall outside the output buffer and
+    are dropped; LSE offsets of rows past n_q are outside its buffer."""
     e("s_waitcnt vmcnt(0) lgkmcnt(0)")
+    e("s_barrier")
     for op in wait_mfma():
         e(op)
     sz = {"f32": 4, "bf16": 2, "f16": 2}[out_dtype]
+    row = 128 * sz
+    inv = (TMP[1], TMP[2])
     for rb in range(2):
-        lt, inv, addr = TMP[0], TMP[1], TMP[2]
+        lt = TMP[0]
         e(f"ds_bpermute_b32 {lt}, %[swp], {LSUM[rb]}")
         e("s_waitcnt lgkmcnt(0)")
         e(f"v_add_f32 {lt}, {lt}, {LSUM[rb]}")
-        e(f"v_rcp_f32 {inv}, {lt}")
+        e(f"v_rcp_f32 {inv[rb]}, {lt}")
         e(f"v_cmp_lt_f32 vcc, 0, {lt}")
         e("s_nop 1")
-        e(f"v_cndmask_b32 {inv}, {ZERO}, {inv}, vcc")
-        if rb == 0:
-            e(f"v_mov_b32 {addr}, %[oo]")
-        else:
-            e(f"v_add_u32 {addr}, %[so1], %[oo]")
-        # store data alternates between two register sets: a store of more than 8 bytes reads its data after
-        # issue, so the next group must not overwrite it right away
-        for db in range(4):
-            for r4 in range(4):
-                alt = 4 * ((4 * db + r4) % 2)
-                vals = [TMP[4 + alt + i] for i in range(4)]  # v220..v223 or v224..v227
-                for i in range(4):
-                    e(f"v_accvgpr_read_b32 {vals[i]}, {O(rb, db, 4 * r4 + i)}")
-                for i in range(4):
-                    e(f"v_mul_f32 {vals[i]}, {vals[i]}, {inv}")
-                off = (32 * db + 8 * r4) * sz
-                first = int(vals[0][1:])
-                if out_dtype == "f32":
-                    e(f"buffer_store_dwordx4 v[{first}:{first + 3}], {addr}, %[ors], 0 offen offset:{off}")
-                else:
-                    cvt = "v_cvt_pk_bf16_f32" if out_dtype == "bf16" else "v_cvt_pk_f16_f32"
-                    e(f"{cvt} {vals[0]}, {vals[0]}, {vals[1]}")
-                    e(f"{cvt} {vals[1]}, {vals[2]}, {vals[3]}")
-                    e(f"buffer_store_dwordx2 v[{first}:{first + 1}], {addr}, %[ors], 0 offen offset:{off}")
-        e("s_nop 1")
+        e(f"v_cndmask_b32 {inv[rb]}, {ZERO}, {inv[rb]}, vcc")
         # lse = (m + log2 l) ln 2 with m the maximum the exponentials are relative to (-negmu); -inf when l = 0
         e("s_cmp_eq_u32 %[has_lse], 0")
         e(f"s_cbranch_scc1 {lbl(f'L_nolse{rb}')}")
@@ -462,6 +444,50 @@ def epilogue(e, out_dtype):
         e(f"v_cndmask_b32 {TMP[3]}, {NINF}, {TMP[3]}, vcc")
         e(f"buffer_store_dword {TMP[3]}, %[lo{rb}], %[lrs], 0 offen")
         e.label(f"L_nolse{rb}")
+    # writes: piece (rb, db, r4) is head dims 32 db + 8 r4 + 4 g .. + 3 of row 32 rb + c32; its address is
+    # %[ew] ^ (16 x its chunk without the lane's part), %[ew] holding the row, the lane's part and the swizzle
+    n = 0
+    for rb in range(2):
+        for db in range(4):
+            for r4 in range(4):
+                vals = [f"v{4 * n + i}" for i in range(4)]
+                addr = f"v{128 + n}"
+                for i in range(4):
+                    e(f"v_accvgpr_read_b32 {vals[i]}, {O(rb, db, 4 * r4 + i)}")
+                for i in range(4):
+                    e(f"v_mul_f32 {vals[i]}, {vals[i]}, {inv[rb]}")
+                chunk = 4 * db + r4 if sz == 2 else 8 * db + 2 * r4
+                e(f"v_xor_b32 {addr}, {16 * chunk}, %[ew]")
+                if sz == 4:
+                    e(f"ds_write_b128 {addr}, v[{4 * n}:{4 * n + 3}] offset:{32 * row * rb}")
+                else:
+                    cvt = "v_cvt_pk_bf16_f32" if out_dtype == "bf16" else "v_cvt_pk_f16_f32"
+                    e(f"{cvt} {vals[0]}, {vals[0]}, {vals[1]}")
+                    e(f"{cvt} {vals[1]}, {vals[2]}, {vals[3]}")
+                    e(f"ds_write_b64 {addr}, v[{4 * n}:{4 * n + 1}] offset:{32 * row * rb}")
+                n += 1
+    e("s_waitcnt lgkmcnt(0)")
+    # reads: load i covers rows (rows_i) i .. of the wave's 64 (16 lanes a row for 2-byte outputs, 32 for f32); the
+    # lane's chunk swizzle depends on the row through i, folded in by an xor of %[er]
+    rows_i = 1024 // row
+    n_ld = 64 // rows_i
+    for i in range(n_ld):
+        swz = ((rows_i * i) & 7) * 16
+        addr = f"v{128 + i}"
+        e(f"v_xor_b32 {addr}, {swz}, %[er]")
+        e(f"ds_read_b128 v[{4 * i}:{4 * i + 3}], {addr} offset:{1024 * i}")
+    # global addresses alternate between two registers, each moved on by two loads' rows after its store
+    ga = (TMP[4], TMP[5])
+    e(f"v_mov_b32 {ga[0]}, %[og]")
+    e(f"v_add_u32 {ga[1]}, %[ogs], %[og]")
+    e(f"s_lshl_b32 {ST[0]}, %[ogs], 1")
+    e("s_waitcnt lgkmcnt(0)")
+    for i in range(n_ld):
+        a = ga[i % 2]
+        e(f"buffer_store_dwordx4 v[{4 * i}:{4 * i + 3}], {a}, %[ors], 0 offen")
+        if i + 2 < n_ld:
+            e("s_nop 1")
+            e(f"v_add_u32 {a}, {ST[0]}, {a}")
 
 
 # ---- the kernel body ----------------------------------------------------------------------------------------------
@@ -469,7 +495,6 @@ def epilogue(e, out_dtype):
 def body(in_dtype, out_dtype):
     e = Emit()
     e(f"s_mov_b32 {S256}, 0x43800000")
-    e(f"s_mov_b32 {SONES}, 0x3c003c00")
     e(f"v_mov_b32 {NINF}, 0xff800000")
     e(f"v_mov_b32 {ZERO}, 0")
     for rb in range(2):

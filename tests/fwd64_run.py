@@ -13,9 +13,9 @@ import gen_attn_fwd64 as G  # noqa: E402
 import oracle as O  # noqa: E402
 
 VOPS = ['kr', 'vr0', 'vr1', 'vr2', 'vr3'] + ([] if G.STAGING == 'dma' else ['kwa', 'kwb', 'vwa']) + [
-    'kd0', 'kd1', 'kd2', 'kd3', 'kd4', 'vd', 'lim0', 'lim1', 'kr0', 'qo', 'oo', 'lo0', 'lo1', 'swp']
+    'kd0', 'kd1', 'kd2', 'kd3', 'kd4', 'vd', 'lim0', 'lim1', 'kr0', 'qo', 'lo0', 'lo1', 'swp', 'ew', 'er', 'og']
 SOPS = {'qrs': 's[0:3]', 'ors': 's[12:15]', 'lrs': 's[16:19]', 'c': 's20',
-        'nt': 's21', 'ntw': 's22', 'lmin': 's23', 'has_lse': 's24', 'so1': 's25', 'kb0': 's26', 'kb1': 's27',
+        'nt': 's21', 'ntw': 's22', 'lmin': 's23', 'has_lse': 's24', 'ogs': 's25', 'kb0': 's26', 'kb1': 's27',
         'kn': 's28', 'vb0': 's29', 'vb1': 's30', 'vn': 's31', 'skw': 's32', 'skww': 's33', 'svww': 's34'}
 VREG = {n: f'v{G.CLOBBER_V + i}' for i, n in enumerate(VOPS)}
 
@@ -145,13 +145,21 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
             kds = [kd_of(w + 4 * m) for m in range(4)] + [kd_of(16)]
             vd = 4096 * w + 16 * lane
             qo = ((q0 + c32) * 128 + 8 * g) * 2
-            oo = (q0 + c32) * width * so + (h * 128 + 4 * g) * so
-            so1 = 32 * width * so
+            orow = 128 * so
+            lpr = orow // 16
+            obase = lbase + w * 64 * orow
+            if so == 4:
+                ew = obase + c32 * orow + 16 * ((c32 & 7) ^ g)
+            else:
+                ew = obase + c32 * orow + 8 * g + 16 * (c32 & 7)
+            er = obase + (lane // lpr) * orow + 16 * ((lane % lpr) ^ (lane // lpr))
+            og = (q0 + lane // lpr) * width * so + h * orow + 16 * (lane % lpr)
+            ogs = (64 // lpr) * width * so
             lo0 = np.where(q0 + c32 < S_q, (h * S_q + q0 + c32) * 4, 0xffffffff)
             lo1 = np.where(q0 + 32 + c32 < S_q, (h * S_q + q0 + 32 + c32) * 4, 0xffffffff)
             swp = (lane ^ 32) * 4
             vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], vr2=vr[2], vr3=vr[3], kd0=kds[0], kd1=kds[1], kd2=kds[2],
-                        kd3=kds[3], kd4=kds[4], vd=vd, lim0=lim0, lim1=lim1, kr0=kr, qo=qo, oo=oo, lo0=lo0, lo1=lo1,
+                        kd3=kds[3], kd4=kds[4], vd=vd, lim0=lim0, lim1=lim1, kr0=kr, qo=qo, lo0=lo0, lo1=lo1, ew=ew, er=er, og=og,
                         swp=swp)
             if G.STAGING != 'dma':
                 vals.update(kwa=lbase + 1024 * w + 16 * lane, kwb=lbase + 16384 + 16 * lane,
@@ -174,7 +182,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
             rs(12, O0, S_q * width * so)
             rs(16, L0, heads * S_q * 4)
             W.s[20] = int(np.float32(c).view(np.uint32))
-            W.s[21], W.s[22], W.s[23], W.s[24], W.s[25] = nt, ntw, lmin, 1, so1
+            W.s[21], W.s[22], W.s[23], W.s[24], W.s[25] = nt, ntw, lmin, 1, ogs
             waves.append(W)
         emu.run_wg(waves)
         n_instr += emu.count

@@ -44,7 +44,9 @@ def test_stream_matches_oracle(case):
     taken = E.EXACT_COUNT[0]
     r = R.run(**case, verbose=False)
     assert r["out_bad"] == 0 and r["lse_bad"] == 0, r
-    assert all(m == 1 for m in r["lds_worst"].values()), r["lds_worst"]
+    # the epilogue's 8-byte writes (2-byte outputs) meet 2-way: sixteen lanes of one write cover rows with eight
+    # distinct chunk slots; every other LDS access is conflict-free
+    assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
     if case.get("kgrow"):
         assert E.EXACT_COUNT[0] > taken  # the exact path ran
 
