@@ -100,7 +100,8 @@ int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dty
  * q [heads][q_pad][128], k [heads][k_pad][128] (f16 or bf16), cnt u32 [n_cubes]; writes sel u16
  * [heads][n_cubes][min(topk, n_cubes)] and nsel u16 [heads][n_cubes]. workspace: at least
  * mako_cube_select_workspace(heads, n_cubes) bytes of device memory. Refuses (MAKO_EINVAL) what the reference
- * refuses: n_cubes > 4096, topk == 0, local not 0, 1 or 3.
+ * refuses: n_cubes > 4096, topk == 0, local not 0, 1 or 3. The selection is exact: means and scores in double,
+ * in the order of the reference test's double check (tests/sparse_attn_test.cpp:98-129), ties to the smaller index.
  */
 size_t mako_cube_select_workspace(uint32_t heads, uint32_t n_cubes);
 int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_cubes, uint32_t topk,

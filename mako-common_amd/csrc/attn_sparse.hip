@@ -3,7 +3,11 @@
 // Semantics (the reference's, src/kernels/ops.metal:914-1185; host checks src/models/runtime.cpp:286-317):
 // * cube_pool: the mean of a cube's 64 rows of q or k over its cnt[c] valid rows (0 when cnt is 0; the padding
 //   rows are zero by the tiles' construction) (ops.metal:926-939).
-// * cube_scores: sc[h][qc][kc] = qp[h][qc] . kp[h][kc] in fp32 (:941-955).
+// * cube_scores: sc[h][qc][kc] = qp[h][qc] . kp[h][kc] (:941-955).
+//   The selection is index work, so it is exact: pooling and scores run in double, in the order of the double CPU
+//   check the reference's own test sorts by (tests/sparse_attn_test.cpp:98-129; the rows summed in order, the mean
+//   by one correctly rounded division, the dot products as a sequential sum of separately rounded products, no
+//   fused multiply-add), so the scores, and with them every comparison the top-k makes, are the check's bit for bit.
 // * cube_topk: the `local` cubes {qc, qc - stride, qc + stride} (those in range) first, their scores taken out of
 //   the running, then repeated argmax, the larger score first and the smaller index on ties; nsel = min(topk, n)
 //   (:957-1027).
@@ -272,55 +276,54 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_sparse(const SparseParams p)
 // q (rows q_pad apart per head), z = 1 pools k (k_pad). 128 threads, one per head dimension.
 template <class T>
 __global__ __launch_bounds__(kD) void cube_pool(const T* __restrict__ q, const T* __restrict__ k,
-                                                 const uint32_t* __restrict__ cnt, float* __restrict__ qp,
-                                                 float* __restrict__ kp, uint32_t n_cubes, uint32_t q_pad,
+                                                 const uint32_t* __restrict__ cnt, double* __restrict__ qp,
+                                                 double* __restrict__ kp, uint32_t n_cubes, uint32_t q_pad,
                                                  uint32_t k_pad)
 {
     const uint32_t cb = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
     const bool is_k = blockIdx.z == 1;
     const T* x = (is_k ? k + (size_t)h * k_pad * kD : q + (size_t)h * q_pad * kD) + (size_t)cb * kCube * kD + d;
-    float s = 0.0f;
+    double s = 0.0;
 #pragma unroll 16
     for (uint32_t r = 0; r < kCube; ++r)
-        s += to_float(x[(size_t)r * kD]);
+        s += (double)to_float(x[(size_t)r * kD]);
     const uint32_t n = cnt[cb];
-    (is_k ? kp : qp)[((size_t)h * n_cubes + cb) * kD + d] = n ? s / (float)n : 0.0f;
+    (is_k ? kp : qp)[((size_t)h * n_cubes + cb) * kD + d] = n ? s / (double)n : 0.0;
 }
 
 // sc[h][qc][kc] = qp[h][qc] . kp[h][kc]: 16 x 16 output tiles through LDS. Grid (ceil(n / 16), ceil(n / 16),
 // heads), 256 threads.
-__global__ __launch_bounds__(256) void cube_scores(const float* __restrict__ qp, const float* __restrict__ kp,
-                                                   float* __restrict__ sc, uint32_t n)
+__global__ __launch_bounds__(256) void cube_scores(const double* __restrict__ qp, const double* __restrict__ kp,
+                                                   double* __restrict__ sc, uint32_t n)
 {
-    __shared__ float qs[16][kD + 1], kt[16][kD + 1];
+    __shared__ double qs[16][kD + 1], kt[16][kD + 1];
     const uint32_t kc0 = blockIdx.x * 16, qc0 = blockIdx.y * 16, h = blockIdx.z, t = threadIdx.x;
     for (uint32_t i = t; i < 16 * kD; i += 256) {
         const uint32_t r = i / kD, d = i % kD;
-        qs[r][d] = qc0 + r < n ? qp[((size_t)h * n + qc0 + r) * kD + d] : 0.0f;
-        kt[r][d] = kc0 + r < n ? kp[((size_t)h * n + kc0 + r) * kD + d] : 0.0f;
+        qs[r][d] = qc0 + r < n ? qp[((size_t)h * n + qc0 + r) * kD + d] : 0.0;
+        kt[r][d] = kc0 + r < n ? kp[((size_t)h * n + kc0 + r) * kD + d] : 0.0;
     }
     __syncthreads();
     const uint32_t qr = t / 16, kr = t % 16;
-    float s = 0.0f;
-#pragma unroll 8
+    double s = 0.0;
     for (uint32_t d = 0; d < kD; ++d)
-        s = fmaf(qs[qr][d], kt[kr][d], s);
+        s = __dadd_rn(s, __dmul_rn(qs[qr][d], kt[kr][d]));  // separately rounded, in order: no contraction
     if (qc0 + qr < n && kc0 + kr < n)
         sc[((size_t)h * n + qc0 + qr) * n + kc0 + kr] = s;
 }
 
 // sel[h][qc][0 .. kk) (kk = min(topk, n)): the local cubes first, then repeated argmax (the larger score, the
 // smaller index on ties); nsel[h][qc] = kk. One workgroup of 256 threads per (qc, h); n <= 4096.
-__global__ __launch_bounds__(256) void cube_topk(const float* __restrict__ sc, uint16_t* __restrict__ sel,
+__global__ __launch_bounds__(256) void cube_topk(const double* __restrict__ sc, uint16_t* __restrict__ sel,
                                                  uint16_t* __restrict__ nsel, uint32_t n, uint32_t kk,
                                                  uint32_t local, uint32_t stride)
 {
-    __shared__ float scores[4096];
-    __shared__ float best_v[4];
+    __shared__ double scores[4096];
+    __shared__ double best_v[4];
     __shared__ uint32_t best_i[4];
     __shared__ uint32_t n_local;
     const uint32_t qc = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float* rowp = sc + ((size_t)h * n + qc) * n;
+    const double* rowp = sc + ((size_t)h * n + qc) * n;
     for (uint32_t i = tid; i < n; i += 256)
         scores[i] = rowp[i];
     uint16_t* out = sel + ((size_t)h * n + qc) * kk;
@@ -339,7 +342,7 @@ __global__ __launch_bounds__(256) void cube_topk(const float* __restrict__ sc, u
     }
     __syncthreads();
     for (uint32_t it = n_local; it < kk; ++it) {
-        float v = -INFINITY;
+        double v = -INFINITY;
         uint32_t idx = 0;
         for (uint32_t i = tid; i < n; i += 256)
             if (scores[i] > v) {
@@ -348,7 +351,7 @@ __global__ __launch_bounds__(256) void cube_topk(const float* __restrict__ sc, u
             }
 #pragma unroll
         for (uint32_t o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(v, o);
+            const double ov = __shfl_xor(v, o);
             const uint32_t oi = __shfl_xor(idx, o);
             if (ov > v || (ov == v && oi < idx)) {
                 v = ov;
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(256) void cube_topk(const float* __restrict__ sc, u
         }
         __syncthreads();
         if (tid == 0) {
-            float bv = best_v[0];
+            double bv = best_v[0];
             uint32_t bi = best_i[0];
             for (uint32_t j = 1; j < 4; ++j)
                 if (best_v[j] > bv || (best_v[j] == bv && best_i[j] < bi)) {
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(256) void cube_topk(const float* __restrict__ sc, u
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-size_t pooled_bytes(uint32_t heads, uint32_t n) { return ((size_t)heads * n * kD * sizeof(float) + 255) / 256 * 256; }
+size_t pooled_bytes(uint32_t heads, uint32_t n) { return ((size_t)heads * n * kD * sizeof(double) + 255) / 256 * 256; }
 
 constexpr int kWaves8 = 8;
 
@@ -726,7 +729,7 @@ using namespace mako;
 
 extern "C" size_t mako_cube_select_workspace(uint32_t heads, uint32_t n_cubes)
 {
-    return 2 * pooled_bytes(heads, n_cubes) + (size_t)heads * n_cubes * n_cubes * sizeof(float);
+    return 2 * pooled_bytes(heads, n_cubes) + (size_t)heads * n_cubes * n_cubes * sizeof(double);
 }
 
 extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_cubes, uint32_t topk,
@@ -748,9 +751,9 @@ extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, 
                     workspace_bytes, mako_cube_select_workspace(heads, n_cubes));
     if (!heads || !n_cubes)
         return ok();
-    float* qp = static_cast<float*>(workspace);
-    float* kp = reinterpret_cast<float*>(static_cast<char*>(workspace) + pooled_bytes(heads, n_cubes));
-    float* sc = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * pooled_bytes(heads, n_cubes));
+    double* qp = static_cast<double*>(workspace);
+    double* kp = reinterpret_cast<double*>(static_cast<char*>(workspace) + pooled_bytes(heads, n_cubes));
+    double* sc = reinterpret_cast<double*>(static_cast<char*>(workspace) + 2 * pooled_bytes(heads, n_cubes));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 pgrid(n_cubes, heads, 2), sgrid((n_cubes + 15) / 16, (n_cubes + 15) / 16, heads), tgrid(n_cubes, heads);
     if (in == MAKO_BF16)
