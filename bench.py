@@ -302,6 +302,56 @@ def bench_decode(torch, M, steps, warmup, with_cpu):
     return out
 
 
+def bench_few_rows(torch, M, steps, warmup, with_cpu):
+    """attention() with a few query rows (the reference's decode is attention(n_q = 1, q_pos0 = ctx - 1)): n_q 1, 4
+    and 16 at ctx 32768, 32 query heads over 8 kv heads, bf16, through mako_attn_fwd (its split-K route). HBM-bound:
+    each call reads K + V once, 8 x 32768 x 256 bytes each."""
+    import numpy as np
+
+    H, KV, D, n = 32, 8, 128, 32768
+    gen = torch.Generator(device="cuda").manual_seed(32768)
+    k = torch.randn((KV, n, D), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((KV, n, D), generator=gen, device="cuda").to(torch.bfloat16)
+    nbytes = 2.0 * KV * n * D * 2
+    out = {}
+    for nq in (1, 4, 16):
+        q = torch.randn((H, nq, D), generator=gen, device="cuda").to(torch.bfloat16)
+        o = torch.empty((nq, H * D), dtype=torch.bfloat16, device="cuda")
+        lse = torch.empty((H, nq), dtype=torch.float32, device="cuda")
+        args = dict(n_q=nq, q_pad=nq, n_k=n, k_pad=n, heads=H, kv_heads=KV, q_pos0=n - nq, block=U32_MAX, dim=D)
+        ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
+        kg = nbytes / (kms * 1e-3) / 1e9
+        leg = {"ms": round(ms, 5), "kernel_ms": round(kms, 5), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+               "roofline": {"bound": "hbm", "achieved": kg, "peak": PEAK_GBPS, "unit": "GB/s",
+                            "frac": kg / PEAK_GBPS, "traffic": traffic(f"few_rows_nq{nq}"),
+                            "kernel": "decode_split<bf16,%d> + decode_merge<bf16> (one call, both kernels)"
+                                      % (1 if nq * H // KV <= 32 else 2), "kernel_ms": kms}}
+        if with_cpu:
+            import oracle as O
+
+            qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
+            rng = np.random.default_rng(nq)
+            gpu_o, gpu_l = o.float().cpu().numpy(), lse.cpu().numpy()
+            state = {}
+
+            def run(m):
+                hr = np.stack([rng.integers(0, H, m), rng.integers(0, nq, m)], 1).astype(np.uint32)
+                want, wl = O.attn_dense_rows(qb, kb, vb, hr, dtype=O.BF16, nthreads=cpu_threads(), **args)
+                state["hr"], state["want"], state["wl"] = hr, want, wl
+
+            m, dt = cpu_sample(run, 8, CPU_SECONDS / 3)
+            hr = state["hr"]
+            got = np.stack([gpu_o[r, h * D:(h + 1) * D] for h, r in hr])
+            leg["cpu_baseline"] = {"value": m * nbytes / (H * nq) / dt / 1e9, "unit": "GB/s", "kind": "port",
+                                   "extrapolated": True,
+                                   "sample": f"{m} random (head, row) pairs, double precision, {dt:.2f} s wall; each "
+                                             f"pair credited its share of the K + V bytes"}
+            leg["cpu_baseline"].update(cpu_info())
+            leg["parity"] = parity_of(got, state["want"], D, np.array([gpu_l[h, r] for h, r in hr]), state["wl"])
+        out[f"n_q={nq}"] = leg
+    return out
+
+
 def bench_bidir(torch, M, steps, warmup, with_cpu):
     S, H, D = 16384, 24, 128
     gen = torch.Generator(device="cuda").manual_seed(16384)
@@ -539,7 +589,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline and parity legs")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs to run alone (no CPU legs unless --cpu): prefill, s512, decode, "
-                         "bidir, sparse, heads, gather, proj, scan, copy")
+                         "few_rows, bidir, sparse, heads, gather, proj, scan, copy")
     ap.add_argument("--cpu", action="store_true", help="with --only: run the legs' CPU-baseline and parity parts")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -560,6 +610,7 @@ def main():
         fn = {"prefill": lambda: bench_prefill(torch, M, args.steps, args.warmup, c),
               "s512": lambda: bench_s512(torch, M, args.steps, args.warmup, c),
               "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, c),
+              "few_rows": lambda: bench_few_rows(torch, M, args.steps, args.warmup, c),
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup, c),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup, c),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
@@ -576,6 +627,7 @@ def main():
     pre = bench_prefill(torch, M, args.steps, args.warmup, with_cpu)
     s512 = bench_s512(torch, M, args.steps, args.warmup, with_cpu)
     dec = bench_decode(torch, M, args.steps, args.warmup, with_cpu)
+    few = bench_few_rows(torch, M, args.steps, args.warmup, with_cpu)
     bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup), with_cpu)
     spa = bench_sparse(torch, M, args.steps, args.warmup, with_cpu)
     hds = bench_heads(torch, M, args.steps, args.warmup)
@@ -605,6 +657,12 @@ def main():
                                                           "contexts U[1024, 32768] seed 2026, f16 cache",
                                               "sum_ctx": dec["sum_ctx"]},
                    "roofline": dec["roofline"]},
+        "few_rows": {"value": few["n_q=1"]["gbps"], "unit": "GB/s", "dtype": "bf16",
+                     "roofline": few["n_q=1"]["roofline"],
+                     "per_n_q": few,
+                     "config": {"workload": "attention() with n_q 1, 4, 16 rows at q_pos0 = ctx - n_q, ctx 32768, "
+                                            "32 query heads / 8 kv heads, D 128, bf16 in/out, LSE (split-K route)",
+                                "bytes": 2 * 8 * 32768 * 256}},
         "bidirectional": bid,
         "block_sparse": spa,
         "head_tiles": {"value": round(hds["gbps"], 1), "unit": "GB/s", "ms_per_step": round(hds["ms"], 4),

@@ -88,7 +88,11 @@ const char* mako_last_error(void);
  * launch. Replaces TransformerRuntime::attention (src/models/runtime.hpp:90-95; src/models/runtime.cpp:262-273)
  * and the kernels it dispatches, flash_attn_coop_{64,128}_32 and flash_attn_sg_256_16x32_4
  * (src/kernels/ops.metal:106-214, 230-369). dim 64, 128 or 256; heads a multiple of kv_heads. Keys past n_k
- * are masked (their rows need not be zero); fully masked rows give 0 and lse = -inf.
+ * are masked (their rows need not be zero); fully masked rows give 0 and lse = -inf. Heads of 128 take one of two
+ * routes: a few query rows (n_q x heads / kv_heads <= 64, as the reference's decode, attention with n_q = 1)
+ * split-K over the keys; more rows, the prefill kernel, after a pass that writes V as f16 V^T tiles. Both keep a
+ * workspace per (device, stream), allocated stream-ordered the first time a call needs it (or more of it), so
+ * such a call allocates; later calls on the stream reuse it.
  */
 int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
                   const void* k, const void* v, void* o, float* lse, void* stream);

@@ -1,7 +1,10 @@
-// Batched single-token decode for gfx950: split-K over each sequence's context, fp32 partials merged by LSE.
+// Split-K attention for gfx950 over each sequence's context, fp32 partials merged by LSE: batched single-token decode
+// (one query row a sequence), and the reference's attention() with a few query rows (mako_attn_fwd routes n_q rows
+// x the GQA group <= 64 columns here; the prefill kernels would leave the GPU nearly empty).
 //
-// Semantics: sequence b's one query row sits at position ctx[b] - 1 and sees keys [0, ctx[b]) (the reference's
-// mask rule, src/kernels/ops.metal:289, with n_q = 1 and q_pos0 = ctx - 1); head h reads kv head
+// Semantics: decode: sequence b's one query row sits at position ctx[b] - 1 and sees keys [0, ctx[b]) (the
+// reference's mask rule, src/kernels/ops.metal:289, with n_q = 1 and q_pos0 = ctx - 1); attention: one sequence, row r
+// at position q_pos0 + r sees key j < n_k when j <= q_pos0 + r or both are >= block (:289); head h reads kv head
 // h / (heads / kv_heads) (:242); the running maximum moves only when a score passes it by 8 (base 2, :303-316);
 // an empty context gives 0 and lse = -inf (:355); P and V meet in f16 for the P V product (V converted from
 // bf16 as it is staged). The reference splits the P V product over keys (attn_pv, src/kernels/gemm.metal:688-730)
@@ -17,12 +20,16 @@
 // * Each wave stages 32-key K / V tiles in its own LDS slice (buffer loads that return zeros past the piece's
 //   end, four whole 256-byte rows an instruction; the next tile's loads are in flight while the current one is
 //   used), so the four waves of a workgroup never wait on each other.
-// * The group's query heads are the columns of S^T = K Q^T on v_mfma_f32_32x32x16 (4 of 32 columns used at
-//   GQA 4): the matrix unit has ~20x the rate this needs, and it keeps the VALU free of per-key dot products and
-//   cross-lane reductions. K rows are stored with bits 2 and 3 of the row swapped so the exponentiated scores are
+// * The columns of S^T = K Q^T on v_mfma_f32_32x32x16 are (query row, head of the group) pairs, col = r group + hg
+//   (decode at GQA 4 uses 4 of the 32): the matrix unit has ~20x the rate this needs, and it keeps the VALU free of
+//   per-key dot products and cross-lane reductions. More than 32 columns (up to 64) make each kv head two segments,
+//   one a column group, which read the same K / V at the same time (the second read mostly hits the cache), so a
+//   wave never needs a second block of accumulators. A column masks the keys its row does not see (only tiles past
+//   the first row's limit need it). K rows are stored with bits 2 and 3 of the row swapped so the exponentiated scores are
 //   already the B operand of O^T = V^T P^T; V is transposed into LDS through registers.
 // * Partials: the unnormalised O^T columns, the running maximum and the row sum; the merge rescales a
-//   segment's pieces to their common maximum and divides once.
+//   segment's pieces to their common maximum and divides once. With many columns a wave takes more keys (at least
+//   8 a column), so the partials stay a small share of the K / V bytes.
 #include <algorithm>
 #include <mutex>
 
@@ -41,17 +48,82 @@ struct DecParams {
     const void* q;
     const void* k;
     const void* v;
-    const uint32_t* ctx;
-    float* part_o;   // [pieces][group][kD]
-    float* part_ml;  // [pieces][group][2]: maximum (base 2), sum
+    const uint32_t* ctx;  // keys of each sequence's segment; null: every sequence has max_ctx
+    float* part_o;   // [pieces][nc][kD]
+    float* part_ml;  // [pieces][nc][2]: maximum (base 2), sum
     uint32_t batch, heads, kv_heads, group, cap, max_ctx, n_waves;
     float scale_log2;
+    uint32_t nq;          // query rows a sequence; nc = nq * group columns (<= 64)
+    uint32_t ncg, ncs;    // column groups a kv head (segments a kv head), columns a segment (<= 32)
+    uint32_t q_pos0;      // position of row 0 (UINT32_MAX: ctx - nq, the decode case)
+    uint32_t block, n_k;  // the visibility rule's block and key count
+    uint32_t qs_b, qs_h, qs_r;  // q element strides: sequence, head, row
+    uint32_t os_b, os_r;        // o element strides: sequence, row (head h at h * kD)
+    uint32_t ls_b, ls_h, ls_r;  // lse strides
 };
 
 // A sequence's context, clamped to max_ctx so no index can leave the cache.
 __device__ __forceinline__ uint32_t ctx_of(const uint32_t* ctx, uint32_t b, uint32_t max_ctx)
 {
-    return min(ctx[b], max_ctx);
+    return ctx ? min(ctx[b], max_ctx) : max_ctx;
+}
+
+// The sum of the contexts of sequences [0, n) (every lane gets it), read 64 at a time: lane-parallel loads and a
+// wave reduction, not n dependent steps.
+__device__ __forceinline__ uint32_t ctx_sum(const DecParams& p, uint32_t n, uint32_t lane)
+{
+    if (!p.ctx)
+        return n * p.max_ctx;
+    uint32_t s = 0;
+    for (uint32_t i0 = 0; i0 < n; i0 += 64) {
+        uint32_t v = i0 + lane < n ? min(p.ctx[i0 + lane], p.max_ctx) : 0u;
+        #pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            v += __shfl_xor(v, o);
+        s += v;
+    }
+    return s;
+}
+
+// The sequence b whose rows (laid end to end, kv_heads x ncg rows a key) hold row r, and the first row of its segments;
+// b = batch when r is past them all. Lane-parallel as ctx_sum: an inclusive prefix over 64 sequences at a time, the
+// first lane whose end passes r.
+__device__ __forceinline__ void seq_of(const DecParams& p, uint32_t r, uint32_t lane, uint32_t& b, uint32_t& seg0)
+{
+    if (!p.ctx) {
+        const uint32_t per = p.max_ctx * p.kv_heads * p.ncg;
+        b = per ? min(r / per, p.batch) : p.batch;
+        seg0 = b * per;
+        return;
+    }
+    uint32_t base = 0;
+    for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
+        const uint32_t i = i0 + lane;
+        const uint32_t len = i < p.batch ? min(p.ctx[i], p.max_ctx) * p.kv_heads * p.ncg : 0u;
+        uint32_t inc = len;
+        #pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(inc, o);
+            inc += lane >= (uint32_t)o ? t : 0u;
+        }
+        const uint64_t hit = __ballot(i < p.batch && r < base + inc);
+        if (hit) {
+            const uint32_t first = (uint32_t)__builtin_ctzll(hit);
+            b = i0 + first;
+            seg0 = base + __shfl(inc - len, first);
+            return;
+        }
+        base += __shfl(inc, 63);
+    }
+    b = p.batch;
+    seg0 = base;
+}
+
+// The keys row r of a sequence with context ctx sees: [0, lim).
+__device__ __forceinline__ uint32_t lim_of(const DecParams& p, uint32_t ctx, uint32_t r)
+{
+    const uint32_t pos = (p.q_pos0 == 0xffffffffu ? ctx - p.nq : p.q_pos0) + r;
+    return pos >= p.block ? ctx : min(ctx, pos + 1);
 }
 
 // The rows of all segments laid end to end, cut into n equal ranges: range w starts at floor(w T / n), computed
@@ -97,48 +169,50 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
     const uint32_t wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane >> 5, c32 = lane & 31;
     const uint32_t wave = blockIdx.x * kWaves + wl;
+    const uint32_t nc = p.nq * p.group, nseg = p.kv_heads * p.ncg;
     T* ks = ks_all[wl];
     _Float16* vt = vt_all[wl];
 
-    // The rows laid end to end: segment (b, kvh) = b * kv_heads + kvh holds ctx[b] rows.
-    uint32_t total = 0;
-    for (uint32_t b = 0; b < p.batch; ++b)
-        total += ctx_of(p.ctx, b, p.max_ctx);
-    total *= p.kv_heads;
+    // The rows laid end to end: segment (b, sh) = b * nseg + sh (kv head sh / ncg, column group sh % ncg) holds
+    // ctx[b] rows.
+    const uint32_t total = ctx_sum(p, p.batch, lane) * nseg;
     if (total == 0)
         return;
     const Ranges rg(total, p.n_waves);
     const uint32_t r0 = rg.start(wave), r1 = rg.start(wave + 1);
     if (r0 >= r1)
         return;
-    // The segment holding r0.
-    uint32_t b = 0, seg0 = 0;  // seg0: first row of sequence b's segments
-    for (; b < p.batch; ++b) {
-        const uint32_t len = ctx_of(p.ctx, b, p.max_ctx) * p.kv_heads;
-        if (r0 < seg0 + len)
-            break;
-        seg0 += len;
-    }
+    // The segment holding r0 (seg0: the first row of sequence b's segments).
+    uint32_t b, seg0;
+    seq_of(p, r0, lane, b, seg0);
     uint32_t ctx = ctx_of(p.ctx, b, p.max_ctx);
-    uint32_t kvh = (r0 - seg0) / ctx;
+    uint32_t sh = (r0 - seg0) / ctx;
     uint32_t row = r0;
 
     const uint32_t cc = lane % 16, kg = lane / 16;
     while (row < r1) {
-        // One piece: segment (b, kvh), keys [k_begin, k_end).
-        const uint32_t s_start = seg0 + kvh * ctx;
+        // One piece: segment (b, sh), keys [k_begin, k_end).
+        const uint32_t s_start = seg0 + sh * ctx;
         const uint32_t k_begin = row - s_start;
         const uint32_t k_end = min(ctx, r1 - s_start);
-        const uint32_t seg = b * p.kv_heads + kvh;
+        const uint32_t seg = b * nseg + sh;
+        const uint32_t kvh = sh / p.ncg;
+        // Column of the lane: col = 32 (sh % ncg) + c32, row col / group, head kvh * group + col % group; its keys
+        // [0, lim) (none past the segment's columns). Tiles below lim_all need no mask: every column sees them.
+        const uint32_t col = 32 * (sh % p.ncg) + c32;
+        const bool has_col = c32 < p.ncs && col < nc;
+        const uint32_t lim = has_col ? lim_of(p, ctx, col / p.group) : 0u;
+        const uint32_t lim_all = lim_of(p, ctx, 0);
 
-        // Q: the B operand; column c32 is query head kvh * group + c32 (zero past the group).
+        // Q: the B operand (zero past the segment's columns).
         V8 qreg[kD / 16];
         {
-            const uint32_t hq = kvh * p.group + c32;
-            const T* src = static_cast<const T*>(p.q) + ((size_t)b * p.heads + hq) * kD + 8 * g;
+            const uint32_t r = col / p.group, hq = kvh * p.group + col % p.group;
+            const T* src = static_cast<const T*>(p.q) + (size_t)b * p.qs_b + (size_t)hq * p.qs_h +
+                           (size_t)r * p.qs_r + 8 * g;
             #pragma unroll
             for (int kk = 0; kk < kD / 16; ++kk)
-                qreg[kk] = c32 < p.group ? *reinterpret_cast<const V8*>(src + 16 * kk) : V8{};
+                qreg[kk] = has_col ? *reinterpret_cast<const V8*>(src + 16 * kk) : V8{};
             #pragma unroll
             for (int kk = 0; kk < kD / 16; ++kk)
                 settle(qreg[kk]);
@@ -189,13 +263,16 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
                 for (int kk = 0; kk < kD / 16; ++kk)
                     s = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s);
             }
-            // Register r holds key j0 + 16 (r / 8) + 8 g + r % 8.
-            if (j0 + kTK > k_end)
+            // Register r holds key j0 + 16 (r / 8) + 8 g + r % 8; keys past the piece or the column's row are
+            // masked.
+            if (j0 + kTK > min(k_end, lim_all)) {
+                const uint32_t end = min(k_end, lim);
                 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t j = j0 + 16 * (r >> 3) + 8 * g + (r & 7);
-                    s[r] = j < k_end ? s[r] : -INFINITY;
+                    s[r] = j < end ? s[r] : -INFINITY;
                 }
+            }
             float mx = -INFINITY;
             #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -237,11 +314,11 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
                 }
             asm volatile("" ::: "memory");
         }
-        // The piece's partial at index wave + segment: unnormalised O^T column c32 (head dims
+        // The piece's partial at index wave + segment: unnormalised O^T column c32 of the segment (head dims
         // 32 db + 8 (r / 4) + 4 g + r % 4), maximum and sum.
         const float lt = l + swap_halves(l);
-        if (c32 < p.group) {
-            const size_t prow = ((size_t)wave + seg) * p.group + c32;
+        if (has_col) {
+            const size_t prow = ((size_t)wave + seg) * p.ncs + c32;
             float* po = p.part_o + prow * kD;
             #pragma unroll
             for (int db = 0; db < kD / 32; ++db)
@@ -254,9 +331,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
         }
         // The next segment (sequences with an empty context hold no rows and are skipped).
         row = s_start + k_end;
-        if (++kvh == p.kv_heads) {
-            kvh = 0;
-            seg0 += ctx * p.kv_heads;
+        if (++sh == nseg) {
+            sh = 0;
+            seg0 += ctx * nseg;
             do {
                 ++b;
             } while (b < p.batch && ctx_of(p.ctx, b, p.max_ctx) == 0);
@@ -267,39 +344,43 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
     }
 }
 
-// One workgroup of 128 threads per (head, sequence): one pass over the segment's pieces with a running maximum
-// (up to 32 pieces' loads in flight at a time), then one division; lse = (max + log2 sum) ln 2.
+// One workgroup of 1024 threads per (head, sequence, row), as kMergeGroups groups of 32 lanes (a lane holds 4 head
+// dims): group gi takes every kMergeGroups-th of the segment's pieces, one pass with a running maximum (all of its
+// pieces' loads in flight at once for up to 8 each), then the groups' (maximum, sum, output) meet in LDS and group 0
+// divides once; lse = (max + log2 sum) ln 2.
+constexpr int kMergeGroups = 32;
+
 template <class TO>
-__global__ __launch_bounds__(kD) void decode_merge(const DecParams p, TO* __restrict__ o, float* __restrict__ lse)
+__global__ __launch_bounds__(1024) void decode_merge(const DecParams p, TO* __restrict__ o, float* __restrict__ lse)
 {
-    const uint32_t h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const uint32_t kvh = h / p.group, hg = h % p.group;
-    uint32_t total = 0, seq0 = 0;
-    for (uint32_t i = 0; i < p.batch; ++i) {
-        const uint32_t n = ctx_of(p.ctx, i, p.max_ctx);
-        seq0 += i < b ? n : 0u;
-        total += n;
-    }
-    total *= p.kv_heads;
+    __shared__ float s_ml[kMergeGroups][2];
+    __shared__ f32x4 s_acc[kMergeGroups][kD / 4];
+    const uint32_t h = blockIdx.x, b = blockIdx.y, rq = blockIdx.z, gi = threadIdx.x / 32, d4 = threadIdx.x % 32;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t kvh = h / p.group, col = rq * p.group + h % p.group, nseg = p.kv_heads * p.ncg;
+    const uint32_t sh = kvh * p.ncg + col / 32, cs = col % 32;  // the column's segment and place in it
+    const uint32_t total = ctx_sum(p, p.batch, lane) * nseg;
+    const uint32_t seq0 = ctx_sum(p, b, lane);
     const uint32_t ctx = ctx_of(p.ctx, b, p.max_ctx);
-    float mx = -INFINITY, sum = 0.0f, acc = 0.0f;
+    float mx = -INFINITY, sum = 0.0f;
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (ctx > 0) {
         const Ranges rg(total, p.n_waves);
-        const uint32_t s_start = seq0 * p.kv_heads + kvh * ctx;
+        const uint32_t s_start = seq0 * nseg + sh * ctx;
         const uint32_t w_lo = rg.wave_of(s_start), w_hi = rg.wave_of(s_start + ctx - 1);
-        const uint32_t seg = b * p.kv_heads + kvh;
-        constexpr int U = 32;
-        for (uint32_t w0 = w_lo; w0 <= w_hi; w0 += U) {
+        const uint32_t seg = b * nseg + sh;
+        constexpr int U = 8;
+        for (uint32_t w0 = w_lo + gi; w0 <= w_hi; w0 += U * kMergeGroups) {
             float2 ml[U];
-            float ov[U];
+            f32x4 ov[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const uint32_t w = w0 + u;
-                // waves with an empty range (fewer rows than waves) wrote nothing
-                const bool live = w <= w_hi && !rg.empty(w);
-                const size_t prow = ((size_t)(live ? w : w_lo) + seg) * p.group + hg;
+                const uint32_t w = w0 + u * kMergeGroups;
+                // waves with an empty range wrote nothing (only possible with fewer rows than waves, q = 0)
+                const bool live = w <= w_hi && (rg.q > 0 || !rg.empty(w));
+                const size_t prow = ((size_t)(live ? w : w_lo) + seg) * p.ncs + cs;
                 ml[u] = live ? *reinterpret_cast<const float2*>(p.part_ml + prow * 2) : float2{-INFINITY, 0.0f};
-                ov[u] = live ? p.part_o[prow * kD + d] : 0.0f;
+                ov[u] = live ? *reinterpret_cast<const f32x4*>(p.part_o + prow * kD + 4 * d4) : f32x4{};
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -313,10 +394,31 @@ __global__ __launch_bounds__(kD) void decode_merge(const DecParams p, TO* __rest
             }
         }
     }
-    const float r = sum > 0.0f ? acc / sum : 0.0f;
-    o[((size_t)b * p.heads + h) * kD + d] = (TO)r;
-    if (lse && d == 0)
-        lse[(size_t)b * p.heads + h] = sum > 0.0f ? (mx + __log2f(sum)) * kLn2 : -INFINITY;
+    if (d4 == 0) {
+        s_ml[gi][0] = mx;
+        s_ml[gi][1] = sum;
+    }
+    s_acc[gi][d4] = acc;
+    __syncthreads();
+    if (gi != 0)
+        return;
+    for (uint32_t j = 1; j < kMergeGroups; ++j) {
+        const float jm = s_ml[j][0];
+        const float nm = fmaxf(mx, jm);
+        if (nm == -INFINITY)
+            continue;
+        const float a = exp2_fast(mx - nm), wgt = exp2_fast(jm - nm);
+        sum = sum * a + s_ml[j][1] * wgt;
+        acc = acc * a + s_acc[j][d4] * wgt;
+        mx = nm;
+    }
+    TO* orow = o + (size_t)b * p.os_b + (size_t)rq * p.os_r + (size_t)h * kD + 4 * d4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        orow[i] = (TO)(sum > 0.0f ? acc[i] / sum : 0.0f);
+    if (lse && d4 == 0)
+        lse[(size_t)b * p.ls_b + (size_t)h * p.ls_h + (size_t)rq * p.ls_r] =
+            sum > 0.0f ? (mx + __log2f(sum)) * kLn2 : -INFINITY;
 }
 
 // Resident waves: kWgPerCu workgroups of kWaves waves on every CU of the current device (0: no device).
@@ -332,16 +434,31 @@ uint32_t waves_for(const mako_decode_args* a, uint32_t resident)
     return (uint32_t)((n + kWaves - 1) / kWaves * kWaves);
 }
 
-size_t pieces_of(uint32_t n_waves, const mako_decode_args* a) { return (size_t)n_waves + (size_t)a->batch * a->kv_heads; }
+// Partials: one a piece (at most n_waves + segments pieces) and column (nc = rows x group).
+size_t part_o_bytes(size_t pieces, uint32_t nc) { return (pieces * nc * kD * sizeof(float) + 255) / 256 * 256; }
+size_t partials_bytes(size_t pieces, uint32_t nc) { return part_o_bytes(pieces, nc) + pieces * nc * 2 * sizeof(float); }
 
-size_t part_o_bytes(uint32_t n_waves, const mako_decode_args* a)
-{
-    return (pieces_of(n_waves, a) * (a->heads / a->kv_heads) * kD * sizeof(float) + 255) / 256 * 256;
-}
+size_t pieces_of(uint32_t n_waves, const mako_decode_args* a) { return (size_t)n_waves + (size_t)a->batch * a->kv_heads; }
+// (the decode's group is at most 32 columns: one segment a kv head)
 
 size_t workspace_for(uint32_t n_waves, const mako_decode_args* a)
 {
-    return part_o_bytes(n_waves, a) + pieces_of(n_waves, a) * (a->heads / a->kv_heads) * 2 * sizeof(float);
+    return partials_bytes(pieces_of(n_waves, a), a->heads / a->kv_heads);
+}
+
+// The split kernel and the merge on stream s.
+template <class T>
+void launch_split_merge(const DecParams& p, mako_dtype out, void* o, float* lse, hipStream_t s)
+{
+    const dim3 grid(p.n_waves / kWaves), mgrid(p.heads, p.batch, p.nq);
+    hipLaunchKernelGGL((decode_split<T>), grid, dim3(kWaves * 64), 0, s, p);
+    const dim3 mblock(1024);
+    if (out == MAKO_F32)
+        hipLaunchKernelGGL(decode_merge<float>, mgrid, mblock, 0, s, p, static_cast<float*>(o), lse);
+    else if (out == MAKO_BF16)
+        hipLaunchKernelGGL(decode_merge<__bf16>, mgrid, mblock, 0, s, p, static_cast<__bf16*>(o), lse);
+    else
+        hipLaunchKernelGGL(decode_merge<_Float16>, mgrid, mblock, 0, s, p, static_cast<_Float16*>(o), lse);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -428,26 +545,62 @@ int launch_decode(const mako_decode_args* a, uint32_t n_waves, mako_dtype in, ma
                   const void* k, const void* v, const uint32_t* ctx_len, void* o, float* lse, void* ws, void* stream,
                   const char* what)
 {
+    const uint32_t group = a->heads / a->kv_heads;
     float* part_o = static_cast<float*>(ws);
-    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + part_o_bytes(n_waves, a));
-    const DecParams p{q, k, v, ctx_len, part_o, part_ml, a->batch, a->heads, a->kv_heads, a->heads / a->kv_heads,
-                      a->cap, a->max_ctx, n_waves, a->scale * kLog2e};
+    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + part_o_bytes(pieces_of(n_waves, a), group));
+    // one query row a sequence at position ctx - 1: q [batch][heads][kD], o likewise, lse [batch][heads]
+    const DecParams p{q, k, v, ctx_len, part_o, part_ml, a->batch, a->heads, a->kv_heads, group, a->cap,
+                      a->max_ctx, n_waves, a->scale * kLog2e, 1u, 1u, group, 0xffffffffu, 0xffffffffu, 0u,
+                      a->heads * kD, kD, 0u, a->heads * kD, 0u, a->heads, 1u, 0u};
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(n_waves / kWaves), mgrid(a->heads, a->batch);
     if (in == MAKO_BF16)
-        hipLaunchKernelGGL(decode_split<__bf16>, grid, dim3(kWaves * 64), 0, s, p);
+        launch_split_merge<__bf16>(p, out, o, lse, s);
     else
-        hipLaunchKernelGGL(decode_split<_Float16>, grid, dim3(kWaves * 64), 0, s, p);
-    if (out == MAKO_F32)
-        hipLaunchKernelGGL(decode_merge<float>, mgrid, dim3(kD), 0, s, p, static_cast<float*>(o), lse);
-    else if (out == MAKO_BF16)
-        hipLaunchKernelGGL(decode_merge<__bf16>, mgrid, dim3(kD), 0, s, p, static_cast<__bf16*>(o), lse);
-    else
-        hipLaunchKernelGGL(decode_merge<_Float16>, mgrid, dim3(kD), 0, s, p, static_cast<_Float16*>(o), lse);
+        launch_split_merge<_Float16>(p, out, o, lse, s);
     return check_launch(what);
 }
 
 }  // namespace
+
+namespace mako {
+
+// mako_attn_fwd's route for a few query rows (heads of 128): when the columns (n_q rows x the GQA group) are at most
+// 64, the split kernel over each kv head's keys (those the last row sees; a segment per 32 columns), partials in the
+// stream's cached workspace, and the merge into o [n_q][width] and lse [heads][n_q]. A wave takes at least 256 keys.
+// Returns 1 when launched, 0 when the case does not take this route, -1 when the workspace could not be had.
+int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                       const void* v, void* o, float* lse, hipStream_t s)
+{
+    const uint32_t group = a->heads / a->kv_heads, nc = a->n_q * group;
+    if (nc > 64 || a->n_q == 0 || (uint64_t)a->q_pos0 + a->n_q >= 0xffffffffull)
+        return 0;
+    const uint32_t last = a->q_pos0 + a->n_q - 1;  // the last row's position: it sees the most keys
+    const uint32_t n_keys = last >= a->block ? a->n_k : std::min(a->n_k, last + 1);
+    const uint32_t ncg = (nc + 31) / 32, ncs = std::min(nc, 32u);
+    const uint32_t resident = resident_waves();
+    if (!resident)
+        return -1;
+    const uint64_t rows = (uint64_t)a->kv_heads * ncg * n_keys;
+    const uint64_t want = std::min<uint64_t>(std::max<uint64_t>((rows + 255) / 256, 1), resident);
+    const uint32_t n_waves = (uint32_t)((want + kWaves - 1) / kWaves * kWaves);
+    const size_t pieces = (size_t)n_waves + (size_t)a->kv_heads * ncg;
+    void* ws = stream_workspace(kWsSplitK, partials_bytes(pieces, ncs), s);
+    if (!ws)
+        return -1;
+    float* part_o = static_cast<float*>(ws);
+    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + part_o_bytes(pieces, ncs));
+    // one sequence of n_keys keys a kv head: q [heads][q_pad][kD], o [n_q][width], lse [heads][n_q]
+    const DecParams p{q, k, v, nullptr, part_o, part_ml, 1u, a->heads, a->kv_heads, group, a->k_pad, n_keys,
+                      n_waves, a->scale * kLog2e, a->n_q, ncg, ncs, a->q_pos0, a->block, a->n_k,
+                      0u, a->q_pad * kD, kD, 0u, a->width, 0u, a->n_q, 1u};
+    if (in == MAKO_BF16)
+        launch_split_merge<__bf16>(p, out, o, lse, s);
+    else
+        launch_split_merge<_Float16>(p, out, o, lse, s);
+    return 1;
+}
+
+}  // namespace mako
 
 extern "C" int mako_attn_decode(const mako_decode_args* a, mako_dtype in, mako_dtype out, const void* q,
                                 const void* k, const void* v, const uint32_t* ctx_len, void* o, float* lse,

@@ -618,6 +618,11 @@ uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uin
 
 }  // namespace
 
+// The split-K route for a few query rows (attn_decode.hip): 1 launched, 0 when the case does not take it, -1 when
+// its workspace could not be allocated.
+int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                       const void* v, void* o, float* lse, hipStream_t s);
+
 // flash_fwd_r64 (attn_fwd64.hip): heads of 128 with 64 rows a wave; 1 launched, 0 when a size does not fit its
 // offsets, -1 when its workspace could not be allocated.
 template <class T, class TO>
@@ -693,6 +698,14 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
         return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
     const dim3 grid(a->heads / hq, p.n_qblk);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dim == 128) {
+        // a few query rows (the reference's decode is attention with n_q = 1): split-K over the keys
+        const int r = launch_attn_splitk(a, in, out, q, k, v, o, lse, s);
+        if (r < 0)
+            return fail(MAKO_EHIP, "attention: no device memory for the split-K partials (%u rows)", a->n_q);
+        if (r > 0)
+            return check_launch("attention");
+    }
     bool launched;
     if (in == MAKO_BF16)
         launched = out == MAKO_F32 ? launch_d<__bf16, float>(a, dim, p, grid, s)

@@ -185,4 +185,12 @@ int check_launch(const char* what);
 // Compute units of the current device (cached per device and thread); 0 when there is none.
 uint32_t device_cus();
 
+// Workspaces the library keeps for callers that pass none: one buffer per (purpose, device, stream), grown (stream-
+// ordered) when a call needs more. Calls on one stream are ordered by the stream and calls on different streams use
+// different buffers, so no call waits on the host or inserts a GPU-side wait. A stream's buffers stay with its handle
+// (hipStreamDestroy waits for the stream's work, so a handle reused later may take them over). Returns null, with
+// nothing allocated, when the allocation fails.
+enum WorkspacePurpose { kWsVtImages = 0, kWsSplitK = 1 };
+void* stream_workspace(WorkspacePurpose purpose, size_t bytes, hipStream_t s);
+
 }  // namespace mako

@@ -3,8 +3,12 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 
+#include "device.hpp"
 #include "mako_attn.h"
 
 namespace mako {
@@ -53,6 +57,37 @@ uint32_t device_cus()
         dev_cached = dev;
     }
     return cus_cached;
+}
+
+namespace {
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex ws_mu;
+std::map<std::tuple<int, int, hipStream_t>, Workspace> ws_all;
+}  // namespace
+
+void* stream_workspace(WorkspacePurpose purpose, size_t bytes, hipStream_t s)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return nullptr;
+    std::lock_guard<std::mutex> lock(ws_mu);
+    Workspace& ws = ws_all[{(int)purpose, dev, s}];
+    if (ws.bytes < bytes) {
+        if (ws.ptr)
+            (void)hipFreeAsync(ws.ptr, s);  // after the previous use on this stream
+        ws.ptr = nullptr;
+        ws.bytes = 0;
+        if (hipMallocAsync(&ws.ptr, bytes, s) != hipSuccess) {
+            (void)hipGetLastError();
+            ws.ptr = nullptr;
+            return nullptr;
+        }
+        ws.bytes = bytes;
+    }
+    return ws.ptr;
 }
 
 }  // namespace mako
