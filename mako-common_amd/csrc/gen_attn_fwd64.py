@@ -107,6 +107,7 @@ SROT = {"k": "s96", "v": "s97", "wk": "s98", "wv": "s99"}   # rotation increment
 SKW = "s66"       # DMA: LDS address of the K image of buffer SBW
 SKWW = "s67"      # DMA: SKW + 1 KiB x (wave index), this wave's first K piece
 SVWW = "s84"      # DMA: LDS address of this wave's 4 KiB of the V^T image of buffer SBW
+SM0 = "s87"       # DMA: the compiler's M0, restored at the end
 
 
 def KSTG(m):      # staged K piece m (0..3: pieces w + 4 m; 4: piece 16)
@@ -514,6 +515,8 @@ def body(in_dtype, out_dtype):
         for kk in range(8):
             e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen offset:{32 * kk}")
     if STAGING == "dma":
+        # M0 is the compiler's: kept in SM0 while the stream uses it, restored at the end
+        e(f"s_mov_b32 {SM0}, m0")
         # tiles 0, 1, 2 into buffers 0, 1, 2; outputs zeroed meanwhile; the barrier waits for tiles 0 and 1
         e(f"s_mov_b32 {SKW}, %[skw]")
         e(f"s_mov_b32 {SKWW}, %[skww]")
@@ -665,6 +668,8 @@ def body_rest(e, in_dtype, out_dtype):
     e(f"s_branch {lbl('L_tail')}")
     e.label("L_epi")
     epilogue(e, out_dtype)
+    if STAGING == "dma":
+        e(f"s_mov_b32 m0, {SM0}")
 
 
 def clobbers():

@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <stdexcept>
 
 #include "mako_attn.h"
@@ -37,8 +38,29 @@ std::optional<Telemetry> parse_telemetry(std::string_view s)
 
 Runtime::Runtime(Telemetry telemetry, int device) : device_(device), tel_(telemetry)
 {
+    if (const char* r = std::getenv("MAKO_REPEAT")) {  // src/gpu/runtime.cpp:52-59
+        const std::string spec(r);
+        const size_t colon = spec.rfind(':');
+        if (colon == std::string::npos)
+            throw std::runtime_error("MAKO_REPEAT wants <label substring>:<n>");
+        repeat_label_ = spec.substr(0, colon);
+        repeat_n_ = std::max(0, std::atoi(r + colon + 1));
+    }
     hip_check(hipSetDevice(device_), "hipSetDevice");
     hip_check(hipStreamCreateWithFlags(&enc_.stream, hipStreamNonBlocking), "hipStreamCreate");
+}
+
+int Runtime::repeats(std::string_view label) const
+{
+    if (repeat_n_ == 1)
+        return 1;
+    for (size_t p = 0; p <= repeat_label_.size();) {
+        const size_t e = std::min(repeat_label_.find(',', p), repeat_label_.size());
+        if (e > p && label.find(std::string_view(repeat_label_).substr(p, e - p)) != std::string_view::npos)
+            return repeat_n_;
+        p = e + 1;
+    }
+    return 1;
 }
 
 Runtime::~Runtime()
@@ -51,6 +73,12 @@ Runtime::~Runtime()
     }
     for (hipEvent_t e : spare_events_)
         (void)hipEventDestroy(e);
+    for (auto& m : marks_)
+        (void)hipEventDestroy(m.ev);
+    for (auto& p : pending_probes_)
+        (void)hipHostFree(p.host);
+    for (auto& [ptr, n] : spare_host_)
+        (void)hipHostFree(ptr);
     for (auto& [name, b] : scratch_)
         (void)hipFree(b.ptr);
     if (enc_.stream)
@@ -138,6 +166,13 @@ void Runtime::finish(Encoder* enc)
         stats_.encode_ms += std::chrono::duration<double, std::milli>(t0 - step_start_).count();
         encoding_ = false;
     }
+    if (!marks_.empty()) {  // the last section or part ends here
+        Mark end;
+        end.ev = event();
+        end.section = -1;
+        hip_check(hipEventRecord(end.ev, enc->stream), "hipEventRecord");
+        marks_.push_back(std::move(end));
+    }
     const hipError_t e = hipStreamSynchronize(enc->stream);
     stats_.gpu_wait_ms += std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
     if (e != hipSuccess)
@@ -146,6 +181,113 @@ void Runtime::finish(Encoder* enc)
     if (last != hipSuccess)
         throw std::runtime_error(std::string("launch queue failed: ") + hipGetErrorString(last));
     resolve_times();
+    resolve_sections();
+    deliver_probes();
+}
+
+void Runtime::section(Encoder*& enc, uint32_t layer, int section)
+{
+    if (tel_ != Telemetry::layers)
+        return;
+    Mark m;
+    m.ev = event();
+    m.layer = layer;
+    m.section = section;
+    hip_check(hipEventRecord(m.ev, enc->stream), "hipEventRecord");
+    marks_.push_back(std::move(m));
+}
+
+void Runtime::part(Encoder*& enc, std::string_view name)
+{
+    if (!part_timing_ || marks_.empty() || marks_.back().section < 0)
+        return;
+    Mark m;
+    m.ev = event();
+    m.layer = marks_.back().layer;
+    m.section = marks_.back().section;
+    m.part = name;
+    hip_check(hipEventRecord(m.ev, enc->stream), "hipEventRecord");
+    marks_.push_back(std::move(m));
+}
+
+// Each interval between consecutive marks belongs to the section of its first mark, and to that mark's part if it
+// names one.
+void Runtime::resolve_sections()
+{
+    for (size_t i = 0; i + 1 < marks_.size(); ++i) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, marks_[i].ev, marks_[i + 1].ev) != hipSuccess)
+            continue;
+        const Mark& m = marks_[i];
+        auto sec = std::find_if(sections_.begin(), sections_.end(), [&](const SectionTime& t) {
+            return t.layer == m.layer && t.section == m.section;
+        });
+        if (sec == sections_.end())
+            sec = sections_.insert(sections_.end(), SectionTime{m.layer, m.section, 0});
+        sec->ms += ms;
+        if (!m.part.empty()) {
+            auto it = std::find_if(parts_.begin(), parts_.end(), [&](const KernelTime& k) { return k.kernel == m.part; });
+            if (it == parts_.end())
+                it = parts_.insert(parts_.end(), KernelTime{m.part, 0, 0});
+            it->ms += ms;
+            ++it->count;
+        }
+    }
+    for (auto& m : marks_)
+        spare_events_.push_back(m.ev);
+    marks_.clear();
+}
+
+std::vector<Runtime::SectionTime> Runtime::section_times()
+{
+    std::vector<SectionTime> out;
+    out.swap(sections_);
+    return out;
+}
+
+std::vector<KernelTime> Runtime::part_times()
+{
+    std::vector<KernelTime> out;
+    out.swap(parts_);
+    return out;
+}
+
+void Runtime::probe(Encoder*& enc, const std::string& name, int layer, Buffer* buf, size_t n, uint64_t off)
+{
+    if (!probe_)
+        return;
+    if (off + n * sizeof(float) > buf->bytes)
+        throw std::runtime_error("probe " + name + ": " + std::to_string(n) + " values at byte " + std::to_string(off) +
+                                 " run past the buffer's " + std::to_string(buf->bytes));
+    PendingProbe p;
+    p.name = name;
+    p.layer = layer;
+    p.n = n;
+    // a spare pinned buffer large enough, or a new one
+    auto it = std::find_if(spare_host_.begin(), spare_host_.end(), [&](const auto& h) { return h.second >= n; });
+    if (it != spare_host_.end()) {
+        p.host = it->first;
+        p.cap = it->second;
+        spare_host_.erase(it);
+    } else {
+        hip_check(hipHostMalloc(reinterpret_cast<void**>(&p.host), std::max<size_t>(n, 1) * sizeof(float),
+                                hipHostMallocDefault), "probe: hipHostMalloc");
+        p.cap = std::max<size_t>(n, 1);
+    }
+    pending_probes_.push_back(p);
+    hip_check(hipMemcpyAsync(p.host, static_cast<const char*>(buf->ptr) + off, n * sizeof(float),
+                             hipMemcpyDeviceToHost, enc->stream), "probe: hipMemcpyAsync");
+}
+
+void Runtime::deliver_probes()
+{
+    std::vector<PendingProbe> ps;
+    ps.swap(pending_probes_);
+    for (auto& p : ps) {
+        if (probe_)
+            probe_(p.name, p.layer, p.host, p.n);
+        spare_host_.emplace_back(p.host, p.cap);
+    }
 }
 
 void Runtime::resolve_times()
@@ -189,11 +331,13 @@ void Runtime::proj(Encoder*& enc, const Weight& w, Buffer* x, uint64_t x_off, Bu
         throw std::runtime_error(msg);
     }
     const mako_gemm_args a{T, w.k, w.n, 2 * w.k, ldy, 0};
+    const char* label = bf16_split_ && !x_bf16 ? "proj BF16 split" : "proj BF16";
     before(enc);
-    check(mako_proj_bf16(&a, x_bf16 ? MAKO_BF16 : MAKO_F32, bf16_split_ && !x_bf16 ? 1 : 0,
-                         static_cast<const char*>(w.buf->ptr) + w.off, static_cast<const char*>(x->ptr) + x_off,
-                         reinterpret_cast<float*>(static_cast<char*>(y->ptr) + y_off), enc->stream));
-    after(enc, bf16_split_ && !x_bf16 ? "proj BF16 split" : "proj BF16");
+    for (int r = repeats(label); r > 0; --r)
+        check(mako_proj_bf16(&a, x_bf16 ? MAKO_BF16 : MAKO_F32, bf16_split_ && !x_bf16 ? 1 : 0,
+                             static_cast<const char*>(w.buf->ptr) + w.off, static_cast<const char*>(x->ptr) + x_off,
+                             reinterpret_cast<float*>(static_cast<char*>(y->ptr) + y_off), enc->stream));
+    after(enc, label);
 }
 
 }  // namespace mako::gpu

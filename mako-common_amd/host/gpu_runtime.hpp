@@ -1,6 +1,6 @@
 // The launch side of the attention path on HIP: what src/gpu/runtime.hpp gives the reference's engines, for the
 // parts the attention path uses (named scratch buffers, one in-order launch queue, finish() raising device errors,
-// per-kernel telemetry, the step statistics). Kernels are reached through the C ABI of include/mako_attn.h, not
+// per-kernel and per-section telemetry, the probe hook for parity checks, MAKO_REPEAT, the step statistics). Kernels are reached through the C ABI of include/mako_attn.h, not
 // by name: the typed entry points replace the pipeline lookup (src/gpu/runtime.cpp:127-135).
 #pragma once
 
@@ -8,6 +8,7 @@
 
 #include <chrono>
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <optional>
 #include <string>
@@ -16,8 +17,9 @@
 
 namespace mako::gpu {
 
-// How much a step measures (src/gpu/runtime.hpp:21-26): at the kernels level every launch is bracketed by a pair
-// of HIP events and labelled.
+// How much a step measures (src/gpu/runtime.hpp:21-26): at the layers level each section (and, with part timing on,
+// each named part) of a step is timed by HIP events on the queue; at the kernels level every launch is bracketed by
+// a pair of HIP events and labelled.
 enum class Telemetry { off, summary, steps, layers, kernels };
 std::optional<Telemetry> parse_telemetry(std::string_view s);
 
@@ -41,6 +43,11 @@ struct Encoder {
 
 class Runtime {
 public:
+    // Called after each named stage of a step with the fp32 values it produced, for parity checks
+    // (src/gpu/runtime.hpp:45-47). Probes are delivered by finish(), in the order they were taken.
+    using Probe = std::function<void(const std::string& name, int layer, const float* data, size_t n)>;
+    void set_probe(Probe probe) { probe_ = std::move(probe); }
+
     struct Stats {
         double gpu_wait_ms = 0, gpu_exec_ms = 0;  // wait: finish() blocked; exec: timed launches, summed
         double encode_ms = 0, step_ms = 0;        // encode: step start to finish()
@@ -50,6 +57,18 @@ public:
     uint64_t scratch_bytes() const;
     // At the kernels level: the launches' GPU times since the last call, summed per kernel.
     std::vector<KernelTime> kernel_times();
+    // At the layers level: each timed section's GPU time (layer, section, ms) and the named parts' times summed per
+    // name, since the last call (the reference's resolve_times, src/gpu/runtime.hpp:147-152).
+    struct SectionTime {
+        uint32_t layer = 0;
+        int section = 0;
+        double ms = 0;
+    };
+    std::vector<SectionTime> section_times();
+    std::vector<KernelTime> part_times();
+    // MAKO_REPEAT=<label substrings, comma-separated>:<n>: launches whose label holds one of the substrings run n
+    // times (0: not at all), so the extra step time measures their cost in place (src/gpu/runtime.hpp:158-172).
+    int repeats(std::string_view label) const;
 
     Runtime(const Runtime&) = delete;
     Runtime& operator=(const Runtime&) = delete;
@@ -68,9 +87,22 @@ protected:
     // and reopened the encoder, src/gpu/runtime.cpp:362-370).
     void before(Encoder* enc);
     void after(Encoder*& enc, std::string_view kernel);
-    // Waits for every launch of the queue and raises std::runtime_error if one failed
-    // (src/gpu/runtime.cpp:453-475).
+    // Waits for every launch of the queue and raises std::runtime_error if one failed (src/gpu/runtime.cpp:453-475);
+    // then resolves the step's times and delivers its probes.
     void finish(Encoder* enc);
+    // With a probe set: n f32 values of buf at off bytes copied on the queue (after what was launched before) into
+    // host memory, handed to the probe by finish() as (name, layer) (src/gpu/runtime.cpp:502-517).
+    void probe(Encoder*& enc, const std::string& name, int layer, Buffer* buf, size_t n, uint64_t off = 0);
+    // Hands the taken probes to the probe (src/gpu/runtime.cpp:519-524); finish() calls it.
+    void deliver_probes();
+    // At the layers level: the launches from here to the next section() (or finish()) are timed as section
+    // `section` of layer `layer` (the reference's timed encoder of a section).
+    bool timing() const { return tel_ == Telemetry::layers; }
+    void section(Encoder*& enc, uint32_t layer, int section);
+    // At the layers level with part timing on: the launches from here to the next part() or section() (or finish())
+    // are timed as `name` within the current section (src/gpu/runtime.hpp:137-146).
+    void enable_part_timing(bool on) { part_timing_ = on && tel_ == Telemetry::layers; }
+    void part(Encoder*& enc, std::string_view name);
     // Turns a nonzero C ABI status into std::runtime_error carrying the library's message.
     static void check(int status);
 
@@ -101,12 +133,34 @@ private:
         std::string kernel;
     };
     std::vector<Timed> timed_;
+    struct Mark {  // a section or part boundary on the queue
+        hipEvent_t ev = nullptr;
+        uint32_t layer = 0;
+        int section = 0;
+        std::string part;  // empty: the section itself
+    };
+    std::vector<Mark> marks_;
+    std::vector<SectionTime> sections_;
+    std::vector<KernelTime> parts_;
+    bool part_timing_ = false;
+    struct PendingProbe {
+        std::string name;
+        int layer = 0;
+        float* host = nullptr;  // pinned
+        size_t n = 0, cap = 0;
+    };
+    Probe probe_;
+    std::vector<PendingProbe> pending_probes_;
+    std::vector<std::pair<float*, size_t>> spare_host_;  // pinned buffers (values) for later probes
+    std::string repeat_label_;
+    int repeat_n_ = 1;
     std::vector<hipEvent_t> spare_events_;
     std::vector<KernelTime> kernels_;
     std::chrono::steady_clock::time_point step_start_;
     bool encoding_ = false;
     hipEvent_t event();
     void resolve_times();
+    void resolve_sections();
 };
 
 }  // namespace mako::gpu

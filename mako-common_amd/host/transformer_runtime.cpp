@@ -27,8 +27,9 @@ void TransformerRuntime::heads(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t ld, 
     const mako_heads_args a{T, ld, col0, kHeadDim, kHeadDim, n_heads, n_pad, 0, rope, rope ? kHeadDim : 0u, 0.0f,
                             1};
     before(enc);
-    check(mako_heads(&a, out, static_cast<const float*>(x->ptr), cs ? static_cast<const float*>(cs->ptr) : nullptr,
-                     nullptr, nullptr, y->ptr, enc->stream));
+    for (int r = repeats("heads"); r > 0; --r)
+        check(mako_heads(&a, out, static_cast<const float*>(x->ptr), cs ? static_cast<const float*>(cs->ptr) : nullptr,
+                         nullptr, nullptr, y->ptr, enc->stream));
     after(enc, "heads");
 }
 
@@ -40,8 +41,9 @@ void TransformerRuntime::heads_norm(gpu::Encoder*& enc, gpu::Buffer* x, uint32_t
                             0};
     const float* c = cs ? reinterpret_cast<const float*>(static_cast<const char*>(cs->ptr) + cs_off) : nullptr;
     before(enc);
-    check(mako_heads(&a, out, static_cast<const float*>(x->ptr), c, static_cast<const float*>(w->ptr), nullptr,
-                     y->ptr, enc->stream));
+    for (int r = repeats("heads_norm"); r > 0; --r)
+        check(mako_heads(&a, out, static_cast<const float*>(x->ptr), c, static_cast<const float*>(w->ptr), nullptr,
+                         y->ptr, enc->stream));
     after(enc, "heads_norm");
 }
 
@@ -54,9 +56,10 @@ void TransformerRuntime::heads_partial(gpu::Encoder*& enc, gpu::Buffer* x, uint3
         throw std::runtime_error(fmt("heads_partial: heads of %u with %u rotated", dim, rot));
     const mako_heads_args a{T, ld, col0, stride, dim, n_heads, n_pad, 0, rot ? 1u : 0u, rot, w ? eps : 0.0f, 0};
     before(enc);
-    check(mako_heads(&a, out, static_cast<const float*>(x->ptr), cs ? static_cast<const float*>(cs->ptr) : nullptr,
-                     w ? static_cast<const float*>(w->ptr) : nullptr,
-                     map ? static_cast<const int32_t*>(map->ptr) : nullptr, y->ptr, enc->stream));
+    for (int r = repeats("heads_partial"); r > 0; --r)
+        check(mako_heads(&a, out, static_cast<const float*>(x->ptr), cs ? static_cast<const float*>(cs->ptr) : nullptr,
+                         w ? static_cast<const float*>(w->ptr) : nullptr,
+                         map ? static_cast<const int32_t*>(map->ptr) : nullptr, y->ptr, enc->stream));
     after(enc, "heads_partial");
 }
 
@@ -68,7 +71,8 @@ void TransformerRuntime::kda_scan(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffe
     const mako_scan_args a{kHeadDim, T, qkv_stride, inner, n_heads, snap};
     auto f = [](gpu::Buffer* b) { return b ? static_cast<float*>(b->ptr) : nullptr; };
     before(enc);
-    check(mako_kda_scan(&a, f(q), f(k), f(v), f(g), f(beta), f(state), f(o), f(snap_state), enc->stream));
+    for (int r = repeats("kda_scan"); r > 0; --r)
+        check(mako_kda_scan(&a, f(q), f(k), f(v), f(g), f(beta), f(state), f(o), f(snap_state), enc->stream));
     after(enc, "kda_scan");
 }
 
@@ -81,10 +85,12 @@ void TransformerRuntime::attention(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buff
         throw std::runtime_error(fmt("attention: heads of %u", dim));
     const mako_attn_args a{n_q, q_pad, n_k, k_pad, n_heads, kv_heads, q_pos0, block, n_heads * dim,
                            1.0f / std::sqrt(float(dim))};
+    const char* label = dim == 64 ? "flash_fwd_64" : dim == 128 ? "flash_fwd_128" : "flash_fwd_256";
     before(enc);
-    check(mako_attn_fwd(&a, dim, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
-                        opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
-    after(enc, dim == 64 ? "flash_fwd_64" : dim == 128 ? "flash_fwd_128" : "flash_fwd_256");
+    for (int r = repeats(label); r > 0; --r)
+        check(mako_attn_fwd(&a, dim, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
+                            opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
+    after(enc, label);
 }
 
 void TransformerRuntime::cube_select(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, uint32_t heads, uint32_t q_pad,
@@ -99,9 +105,10 @@ void TransformerRuntime::cube_select(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Bu
     sel = scratch("c_sel", uint64_t(heads) * n_cubes * kk * 2);
     nsel = scratch("c_nsel", uint64_t(heads) * n_cubes * 2);
     before(enc);
-    check(mako_cube_select(heads, q_pad, k_pad, n_cubes, topk, local, stride, in, q->ptr, k->ptr,
-                           static_cast<const uint32_t*>(cnt->ptr), static_cast<uint16_t*>(sel->ptr),
-                           static_cast<uint16_t*>(nsel->ptr), ws->ptr, ws->bytes, enc->stream));
+    for (int r = repeats("cube_select"); r > 0; --r)
+        check(mako_cube_select(heads, q_pad, k_pad, n_cubes, topk, local, stride, in, q->ptr, k->ptr,
+                               static_cast<const uint32_t*>(cnt->ptr), static_cast<uint16_t*>(sel->ptr),
+                               static_cast<uint16_t*>(nsel->ptr), ws->ptr, ws->bytes, enc->stream));
     after(enc, "cube_select");
 }
 
@@ -119,11 +126,12 @@ void TransformerRuntime::attention_sparse(gpu::Encoder*& enc, gpu::Buffer* q, gp
                              n_cubes, std::min(topk, n_cubes), dense0, dense1, opt.causal ? 1u : 0u,
                              opt.sel_per_kv_head ? kv_heads : heads};
     before(enc);
-    check(mako_attn_sparse(&a, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
-                           sel ? static_cast<const uint16_t*>(sel->ptr) : nullptr,
-                           nsel ? static_cast<const uint16_t*>(nsel->ptr) : nullptr,
-                           static_cast<const uint8_t*>(valid->ptr), static_cast<const int32_t*>(map->ptr),
-                           opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
+    for (int r = repeats("flash_sparse_128"); r > 0; --r)
+        check(mako_attn_sparse(&a, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
+                               sel ? static_cast<const uint16_t*>(sel->ptr) : nullptr,
+                               nsel ? static_cast<const uint16_t*>(nsel->ptr) : nullptr,
+                               static_cast<const uint8_t*>(valid->ptr), static_cast<const int32_t*>(map->ptr),
+                               opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
     after(enc, "flash_sparse_128");
 }
 
@@ -137,9 +145,10 @@ void TransformerRuntime::attention_decode(gpu::Encoder*& enc, gpu::Buffer* q, gp
         throw std::runtime_error(fmt("attention_decode: %u heads over %u kv heads", heads, kv_heads));
     gpu::Buffer* ws = scratch("attn_decode", need);
     before(enc);
-    check(mako_attn_decode(&a, opt.in, opt.out, q->ptr, k->ptr, v->ptr, static_cast<const uint32_t*>(ctx_len->ptr),
-                           o->ptr, opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, ws->ptr, ws->bytes,
-                           enc->stream));
+    for (int r = repeats("attn_decode"); r > 0; --r)
+        check(mako_attn_decode(&a, opt.in, opt.out, q->ptr, k->ptr, v->ptr, static_cast<const uint32_t*>(ctx_len->ptr),
+                               o->ptr, opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, ws->ptr, ws->bytes,
+                               enc->stream));
     after(enc, "attn_decode");
 }
 

@@ -12,6 +12,10 @@
 // * proj() with BF16 weights after attention (src/models/qwen_text.cpp:312): f32 rows, the bf16 split the Qwen
 //   encoders turn on (src/models/qwen_text.cpp:271), bf16 rows, a y row stride, and the refusal of k = 96
 //   (src/gpu/runtime.cpp:179-180); within the f32 summation bound 2 k 2^-24 sum|terms| (4 k with the split);
+// * the probe hook (src/gpu/runtime.cpp:502-524): the attention output probed after attention(), whole and a slice
+//   at an offset, comes back bit-equal to o, with its name and layer; layer / part timing at the layers level
+//   (src/gpu/runtime.hpp:137-152): two sections and three named parts, each timed; MAKO_REPEAT=flash_fwd:3 runs
+//   attention three times inside one timed launch and leaves its output bit-equal;
 // * kda_scan with the arguments QwenText::linear_layer passes (src/models/qwen_text.cpp:374-382: {128, T, vw, vw, VH,
 //   0}, the state zeroed), 4 heads over 100 tokens; within 2e-5 + 1e-4 |ref| of the oracle.
 // Tolerance: every element within 2e-3 + 1e-2 |ref|; LSE within 1e-3; head tiles within one f16 ulp.
@@ -21,9 +25,11 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "attn_oracle.h"
@@ -33,7 +39,7 @@ namespace {
 
 class Harness final : public mako::models::TransformerRuntime {
 public:
-    Harness() : TransformerRuntime(mako::gpu::Telemetry::kernels) {}
+    explicit Harness(mako::gpu::Telemetry t = mako::gpu::Telemetry::kernels) : TransformerRuntime(t) {}
     using TransformerRuntime::attention;
     using TransformerRuntime::attention_decode;
     using TransformerRuntime::heads;
@@ -45,6 +51,10 @@ public:
     using TransformerRuntime::encoder;
     using TransformerRuntime::finish;
     using TransformerRuntime::scratch;
+    using TransformerRuntime::probe;
+    using TransformerRuntime::section;
+    using TransformerRuntime::part;
+    using TransformerRuntime::enable_part_timing;
 };
 
 int failures = 0;
@@ -192,6 +202,93 @@ int main()
         const double le = lse_err(get<float>(lb, want_l.size()), want_l);
         check(bad == 0 && le <= 1e-3, "attention_decode, 4 sequences: " + std::to_string(bad) +
                                           " elements out of tolerance, LSE error " + std::to_string(le));
+    }
+    // The probe hook: attention's output probed whole and as one head of one row (at a byte offset).
+    {
+        const uint32_t heads = 8, kv = 2, D = 128, S = 256;
+        const auto q = random_tile(size_t(heads) * S * D, ORACLE_F16), k = random_tile(size_t(kv) * S * D, ORACLE_F16),
+                   v = random_tile(size_t(kv) * S * D, ORACLE_F16);
+        auto qb = put(h, "q", q), kb = put(h, "k", k), vb = put(h, "v", v);
+        const size_t n = size_t(S) * heads * D;
+        auto ob = h.scratch("o", n * 4);
+        std::vector<std::tuple<std::string, int, std::vector<float>>> got;
+        h.set_probe([&](const std::string& name, int layer, const float* data, size_t cnt) {
+            got.emplace_back(name, layer, std::vector<float>(data, data + cnt));
+        });
+        auto* enc = h.encoder();
+        h.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX);
+        h.probe(enc, "attn_out", 7, ob, n);
+        const uint64_t off = (5ull * heads * D + 2 * D) * 4;  // row 5, head 2
+        h.probe(enc, "attn_row5_head2", 7, ob, D, off);
+        h.finish(enc);
+        h.set_probe(nullptr);
+        const auto o = get<float>(ob, n);
+        bool same = got.size() == 2 && std::get<0>(got[0]) == "attn_out" && std::get<1>(got[0]) == 7 &&
+                    std::get<2>(got[0]).size() == n && std::get<0>(got[1]) == "attn_row5_head2" &&
+                    std::get<2>(got[1]).size() == D;
+        same = same && std::memcmp(std::get<2>(got[0]).data(), o.data(), n * 4) == 0 &&
+               std::memcmp(std::get<2>(got[1]).data(), o.data() + off / 4, size_t(D) * 4) == 0;
+        check(same, "probe after attention: the f32 rows come back bit-equal to o, with name and layer");
+    }
+    // Layer / part timing at the layers level, and MAKO_REPEAT.
+    {
+        const uint32_t heads = 8, kv = 2, D = 128, S = 512;
+        const auto q = random_tile(size_t(heads) * S * D, ORACLE_BF16),
+                   k = random_tile(size_t(kv) * S * D, ORACLE_BF16), v = random_tile(size_t(kv) * S * D, ORACLE_BF16);
+        mako::models::AttnOptions opt;
+        opt.in = MAKO_BF16;
+        const size_t n = size_t(S) * heads * D;
+        std::vector<float> once;
+        {
+            Harness ht(mako::gpu::Telemetry::layers);
+            auto qb = put(ht, "q", q), kb = put(ht, "k", k), vb = put(ht, "v", v);
+            auto ob = ht.scratch("o", n * 4);
+            ht.enable_part_timing(true);
+            auto* enc = ht.encoder();
+            ht.section(enc, 3, 0);
+            ht.part(enc, "attention causal");
+            ht.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX, D, opt);
+            ht.part(enc, "attention bidirectional");
+            ht.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, 0, D, opt);
+            ht.section(enc, 4, 1);
+            ht.part(enc, "attention causal");
+            ht.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX, D, opt);
+            ht.finish(enc);
+            once = get<float>(ob, n);
+            const auto secs = ht.section_times();
+            const auto parts = ht.part_times();
+            bool ok = secs.size() == 2 && secs[0].layer == 3 && secs[0].section == 0 && secs[1].layer == 4 &&
+                      secs[1].section == 1 && secs[0].ms > 0 && secs[1].ms > 0;
+            double causal = 0, bidir = 0;
+            uint32_t causal_n = 0;
+            for (const auto& p : parts) {
+                if (p.kernel == "attention causal") {
+                    causal = p.ms;
+                    causal_n = p.count;
+                } else if (p.kernel == "attention bidirectional") {
+                    bidir = p.ms;
+                }
+            }
+            ok = ok && parts.size() == 2 && causal_n == 2 && causal > 0 && bidir > 0 &&
+                 secs[0].ms + 1e-6 >= bidir && ht.section_times().empty();
+            check(ok, "layers timing: 2 sections (" + std::to_string(secs.size()) + "), parts causal x" +
+                          std::to_string(causal_n) + " and bidirectional, each timed");
+        }
+        {
+            setenv("MAKO_REPEAT", "flash_fwd:3", 1);
+            Harness hr;
+            unsetenv("MAKO_REPEAT");
+            auto qb = put(hr, "q", q), kb = put(hr, "k", k), vb = put(hr, "v", v);
+            auto ob = hr.scratch("o", n * 4);
+            auto* enc = hr.encoder();
+            hr.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX, D, opt);
+            hr.finish(enc);
+            const auto kt = hr.kernel_times();
+            const auto o = get<float>(ob, n);
+            check(hr.repeats("flash_fwd_128") == 3 && hr.repeats("proj BF16") == 1 && kt.size() == 1 &&
+                      kt[0].count == 1 && std::memcmp(o.data(), once.data(), n * 4) == 0,
+                  "MAKO_REPEAT=flash_fwd:3: attention repeated inside one timed launch, output bit-equal");
+        }
     }
     // A head width the reference refuses.
     {
