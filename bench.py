@@ -376,6 +376,48 @@ def bench_bidir(torch, M, steps, warmup, with_cpu):
     return out
 
 
+def bench_other_dims(torch, M, steps, warmup, with_cpu):
+    """The attention path's other head widths, each against the MFMA roof: heads of 256 causal (the Qwen3.5 gated
+    attention layers, qwen_text.cpp:418, at a Qwen3-Next-style shape: 16 query heads over 2 kv heads, S 4096) on
+    flash_fwd_wide, and heads of 64 bidirectional (the H3 VAE decoder's ViT attention, h3_vae.cpp:219: MHA, 16
+    heads, 4096 tokens) on flash_fwd. bf16 in and out, LSE."""
+    legs = {
+        "d256_causal": dict(H=16, KV=2, D=256, S=4096, block=U32_MAX, seed=256,
+                            kernel="flash_fwd_wide<bf16,bf16,256>",
+                            workload="causal GQA, 16 query heads / 2 kv heads, D 256, S 4096, bf16 in/out, LSE "
+                                     "(Qwen3.5 gated attention)"),
+        "d64_bidir": dict(H=16, KV=16, D=64, S=4096, block=0, seed=64, kernel="flash_fwd<bf16,bf16,64>",
+                          workload="bidirectional MHA, 16 heads, D 64, S 4096, bf16 in/out, LSE (H3 VAE ViT)"),
+    }
+    out = {}
+    for name, c in legs.items():
+        H, KV, D, S = c["H"], c["KV"], c["D"], c["S"]
+        gen = torch.Generator(device="cuda").manual_seed(c["seed"])
+        q = torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+        k = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+        v = torch.randn((KV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+        o = torch.empty((S, H * D), dtype=torch.bfloat16, device="cuda")
+        lse = torch.empty((H, S), dtype=torch.float32, device="cuda")
+        args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=H, kv_heads=KV, q_pos0=0, block=c["block"], dim=D)
+        ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, lse=lse, **args), steps, warmup)
+        pairs = S * (S + 1) / 2 if c["block"] == U32_MAX else S * S
+        flop = 4.0 * D * pairs * H
+        kt = flop / (kms * 1e-3) / 1e12
+        leg = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+               "kernel_ms": round(kms, 4), "frac": round(kt / PEAK_TFLOPS, 4), "dtype": "bf16",
+               "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": kt / PEAK_TFLOPS, "traffic": traffic(name), "kernel": c["kernel"],
+                            "kernel_ms": kms},
+               "config": {"workload": c["workload"], "flop": flop}}
+        if with_cpu:
+            import oracle as O
+
+            leg["cpu_baseline"], leg["parity"], _ = dense_cpu_leg(torch, M, O, q, k, v, o, lse, args, O.BF16,
+                                                                  c["seed"], 16, f"the {name} case")
+        out[name] = leg
+    return out
+
+
 def bench_sparse(torch, M, steps, warmup, with_cpu):
     """Block-sparse causal attention, S16384, 32 query heads over 8 kv heads, 64x64 blocks: each block attends
     itself (causal), the 8 before it and 8 random earlier ones (seed 16384, one list per kv head). MFMA-bound: the
@@ -589,7 +631,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline and parity legs")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs to run alone (no CPU legs unless --cpu): prefill, s512, decode, "
-                         "few_rows, bidir, sparse, heads, gather, proj, scan, copy")
+                         "few_rows, bidir, dims, sparse, heads, gather, proj, scan, copy")
     ap.add_argument("--cpu", action="store_true", help="with --only: run the legs' CPU-baseline and parity parts")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -612,6 +654,7 @@ def main():
               "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, c),
               "few_rows": lambda: bench_few_rows(torch, M, args.steps, args.warmup, c),
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup, c),
+              "dims": lambda: bench_other_dims(torch, M, args.steps, args.warmup, c),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup, c),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
@@ -629,6 +672,7 @@ def main():
     dec = bench_decode(torch, M, args.steps, args.warmup, with_cpu)
     few = bench_few_rows(torch, M, args.steps, args.warmup, with_cpu)
     bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup), with_cpu)
+    dims = bench_other_dims(torch, M, max(1, args.steps // 2), args.warmup, with_cpu)
     spa = bench_sparse(torch, M, args.steps, args.warmup, with_cpu)
     hds = bench_heads(torch, M, args.steps, args.warmup)
     gat = bench_gather(torch, M, args.steps, args.warmup)
@@ -664,6 +708,7 @@ def main():
                                             "32 query heads / 8 kv heads, D 128, bf16 in/out, LSE (split-K route)",
                                 "bytes": 2 * 8 * 32768 * 256}},
         "bidirectional": bid,
+        "other_head_widths": dims,
         "block_sparse": spa,
         "head_tiles": {"value": round(hds["gbps"], 1), "unit": "GB/s", "ms_per_step": round(hds["ms"], 4),
                        "kernel_ms": round(hds["kernel_ms"], 4), "bound": "hbm", "frac": round(hds["frac"], 4),
