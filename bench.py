@@ -302,7 +302,7 @@ def bench_decode(torch, M, steps, warmup, with_cpu):
     return out
 
 
-def bench_few_rows(torch, M, steps, warmup, with_cpu):
+def bench_few_rows(torch, M, steps, warmup, with_cpu, nqs=(1, 4, 16)):
     """attention() with a few query rows (the reference's decode is attention(n_q = 1, q_pos0 = ctx - 1)): n_q 1, 4
     and 16 at ctx 32768, 32 query heads over 8 kv heads, bf16, through mako_attn_fwd (its split-K route). HBM-bound:
     each call reads K + V once, 8 x 32768 x 256 bytes each."""
@@ -316,6 +316,8 @@ def bench_few_rows(torch, M, steps, warmup, with_cpu):
     out = {}
     for nq in (1, 4, 16):
         q = torch.randn((H, nq, D), generator=gen, device="cuda").to(torch.bfloat16)
+        if nq not in nqs:
+            continue
         o = torch.empty((nq, H * D), dtype=torch.bfloat16, device="cuda")
         lse = torch.empty((H, nq), dtype=torch.float32, device="cuda")
         args = dict(n_q=nq, q_pad=nq, n_k=n, k_pad=n, heads=H, kv_heads=KV, q_pos0=n - nq, block=U32_MAX, dim=D)
@@ -376,7 +378,7 @@ def bench_bidir(torch, M, steps, warmup, with_cpu):
     return out
 
 
-def bench_other_dims(torch, M, steps, warmup, with_cpu):
+def bench_other_dims(torch, M, steps, warmup, with_cpu, names=None):
     """The attention path's other head widths, each against the MFMA roof: heads of 256 causal (the Qwen3.5 gated
     attention layers, qwen_text.cpp:418, at a Qwen3-Next-style shape: 16 query heads over 2 kv heads, S 4096) on
     flash_fwd_wide, and heads of 64 bidirectional (the H3 VAE decoder's ViT attention, h3_vae.cpp:219: MHA, 16
@@ -391,6 +393,8 @@ def bench_other_dims(torch, M, steps, warmup, with_cpu):
     }
     out = {}
     for name, c in legs.items():
+        if names is not None and name not in names:
+            continue
         H, KV, D, S = c["H"], c["KV"], c["D"], c["S"]
         gen = torch.Generator(device="cuda").manual_seed(c["seed"])
         q = torch.randn((H, S, D), generator=gen, device="cuda").to(torch.bfloat16)
@@ -631,7 +635,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline and parity legs")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs to run alone (no CPU legs unless --cpu): prefill, s512, decode, "
-                         "few_rows, bidir, dims, sparse, heads, gather, proj, scan, copy")
+                         "few_rows, bidir, dims, sparse, heads, gather, proj, scan, copy; few_rows:N runs the n_q = N "
+                         "case alone, dims:NAME one head width (d256_causal, d64_bidir)")
     ap.add_argument("--cpu", action="store_true", help="with --only: run the legs' CPU-baseline and parity parts")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -649,19 +654,25 @@ def main():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     if args.only:
         c = args.cpu
+        sub = {}
+        for leg in args.only.split(","):
+            name, _, case = leg.partition(":")
+            if case:
+                sub.setdefault(name, []).append(int(case) if name == "few_rows" else case)
         fn = {"prefill": lambda: bench_prefill(torch, M, args.steps, args.warmup, c),
               "s512": lambda: bench_s512(torch, M, args.steps, args.warmup, c),
               "decode": lambda: bench_decode(torch, M, args.steps, args.warmup, c),
-              "few_rows": lambda: bench_few_rows(torch, M, args.steps, args.warmup, c),
+              "few_rows": lambda: bench_few_rows(torch, M, args.steps, args.warmup, c,
+                                                 tuple(sub.get("few_rows", (1, 4, 16)))),
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup, c),
-              "dims": lambda: bench_other_dims(torch, M, args.steps, args.warmup, c),
+              "dims": lambda: bench_other_dims(torch, M, args.steps, args.warmup, c, sub.get("dims")),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup, c),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
               "proj": lambda: bench_proj(torch, M, args.steps, args.warmup),
               "scan": lambda: bench_scan(torch, M, args.steps, args.warmup),
               "copy": lambda: bench_copy(torch, args.steps, args.warmup)}
-        for leg in args.only.split(","):
+        for leg in dict.fromkeys(x.partition(":")[0] for x in args.only.split(",")):
             if leg not in fn:
                 ap.error(f"--only: unknown leg {leg!r}")
             print(json.dumps({leg: fn[leg]()}), flush=True)
