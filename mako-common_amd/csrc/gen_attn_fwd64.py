@@ -13,25 +13,28 @@ LDS as the A operand, Q from the accumulator registers as B), so each lane holds
 of each 32-key half; P V is O^T += V^T P^T with V^T from LDS (f16) and the f16 probabilities as B. Every K / V^T
 operand read from LDS feeds both row blocks' MFMAs.
 
-Keys go by tiles of 64 through three LDS buffers (a padded K image and a V^T image each). Staging is straight
-copies, 16 bytes a lane, with no conversion: the K image from K as it lies in memory (five 1 KiB pieces a wave, each
-lane loading the 16 bytes its LDS slot holds), the V^T image from the f16 V^T tile images that vt_image
-(attn_fwd64.hip) writes before the kernel runs (four contiguous 1 KiB pieces a wave). In iteration j the wave reads
-K(j + 1) and V^T(j), writes tile j + 2 (loaded into its staging registers during iteration j - 1) into the buffer
-of tile j - 1 and loads tile j + 3 into the staging registers; one workgroup barrier a tile. Loads past the
-workgroup's keys lie outside the buffer descriptors and load zeros. (LDS DMA would save the staging registers and
-the writes, but on this part it holds the shader clock near 1.9 GHz where register staging runs at 2.33 GHz.)
+Keys go by tiles of 64 through four LDS buffers (a padded K image and a V^T image each). Staging is straight
+copies by LDS DMA, 16 bytes a lane, with no conversion: the K image from K as it lies in memory (five 1 KiB pieces a
+wave, each lane loading the 16 bytes its LDS slot holds), the V^T image from the f16 V^T tile images that vt_image
+(attn_fwd64.hip) writes before the kernel runs (four contiguous 1 KiB pieces a wave). Iteration j loads tile j + 3
+into the buffer of tile j - 1. Loads past the workgroup's keys lie outside the buffer descriptors and load zeros.
+(MAKO_FWD64_STAGING=reg stages through registers and three buffers instead: load tile j + 3, write tile j + 2.)
 
 Iteration j, with S_cur holding tile j's exponentials (f32, made against the running maximum known when they were
 made) and S_nxt receiving tile j + 1's scores:
   phase QK: 32 MFMAs, S_nxt = K(j + 1) Q^T, beside the staging of tile j + 3, P = f16(S_cur) and the row sums
-            of S_cur (f32, as the reference sums them). Then the check: when some lane's sum over its 32 keys exceeds 256 (a score above the
-            running maximum by more than 8, base 2) or is not a number, the wave takes the exact path, which
-            recomputes tile j's scores from LDS, masks them, moves the running maximum by the reference's rule (only
-            when a score passes it by more than 8), rescales the outputs and sums, and makes the exponentials, P and
-            sums again. Tile 0 always takes that path.
+            of S_cur (f32, as the reference sums them); its last fragments' time reads the first V^T(j) operands.
+            Then the check: when some lane's sum over its 32 keys exceeds 256 (a score above the running maximum by
+            more than 8, base 2) or is not a number, the wave takes the exact path, which recomputes tile j's scores
+            from LDS, masks them, moves the running maximum by the reference's rule (only when a score passes it by
+            more than 8), rescales the outputs and sums, and makes the exponentials, P and sums again. Tile 0 always
+            takes that path.
   phase PV: 32 MFMAs, O += V^T(j) P^T, beside the exponentials of tile j + 1 (masked first when some row of the
-            wave does not see all of its keys).
+            wave does not see all of its keys). Barrier j sits after its fragment BAR_AT, once the wave's V^T(j)
+            reads have landed: past it, every wave's loads of tile j + 2 are in LDS (so the first K(j + 2) operands
+            of the next phase QK are read from there on) and no wave reads the buffer of tile j any more (so the
+            next iteration's staging may overwrite it).
+Operand reads thus run across the phase boundaries, and no MFMA waits for an LDS read issued at its phase's start.
 The loop is unrolled twice so that S_cur and S_nxt swap registers statically.
 
 Register map: a0..a127 the outputs O[rb][db] (32 head dims a block), a128..a191 Q[rb][kk], a192..a223 the LDS
@@ -53,6 +56,8 @@ DMA_PER_TILE = 9        # LDS DMA loads a wave issues a tile (5 K pieces, 4 V^T 
 RING = 8                # LDS operand ring slots
 AHEAD = 6               # operand reads in flight ahead of their MFMAs (a slot is refilled two fragments after its
                         # last MFMA was issued)
+BAR_AT = 12             # phase PV's fragment after whose MFMAs the tile's barrier sits (its V^T reads landed by then)
+N_K_AHEAD = 6           # K reads of the next phase QK that go out in phase PV's tail, after the barrier
 
 # ---- registers ---------------------------------------------------------------------------------------------------
 
@@ -227,8 +232,8 @@ def staging():
 
 
 def barrier():
-    """The wave's LDS writes and reads are done (the buffer read last is written after the barrier); then the
-    barrier."""
+    """The wave's staging of the tile before the last is in LDS and its LDS writes and reads are done (the buffer it
+    read last is written after the barrier); then the barrier."""
     if STAGING == "dma":
         return [f"s_waitcnt vmcnt({DMA_PER_TILE}) lgkmcnt(0)", "s_barrier"]
     return ["s_waitcnt lgkmcnt(0)", "s_barrier"]
@@ -264,22 +269,38 @@ def pv_mfmas():
     return out
 
 
-def interleave(e, reads, mfmas, valu):
-    """Emits the MFMAs, each tagged with the fragment it reads, fed by a ring of RING LDS reads (a fragment is read
-    into its slot once the previous occupant's last MFMA is issued), with the instructions of `valu` spread evenly
-    between them. LDS instructions inside `valu` are counted for the lgkmcnt waits (LDS returns in order)."""
-    issued = []
-    slot = {}
+def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=()):
+    """Emits the MFMAs of a phase, each tagged with the fragment it reads, fed by a ring of RING LDS reads, with the
+    instructions of `valu` spread evenly between them. Fragment f lives in ring slot f % RING; its read goes out AHEAD
+    fragments before its MFMAs (a slot is refilled two fragments after its previous occupant's last MFMA). The first
+    `pre` reads were issued before the phase began, as the last LDS instructions before it. nxt = (kind, reads) of
+    the next phase: its read m goes out after fragment len(reads) + m - AHEAD of this phase, and not before `gate`,
+    the instructions emitted after fragment gate_at's MFMAs. Returns how many of the next phase's reads went out.
+    LDS returns in order, so the wait for a read is lgkmcnt(LDS instructions issued after it); LDS instructions inside
+    `valu` are counted too."""
+    issued = [(kind, f) for f in range(pre)]
+    nfr = len(reads)
 
-    def issue(f):
-        slot[f] = f % RING
-        e(reads[f].format(ring=RINGR(slot[f])))
-        issued.append(f"R{f}")
+    def issue(k, f, text):
+        e(text.format(ring=RINGR(f % RING)))
+        issued.append((k, f))
 
-    nxt = 0
-    while nxt < min(AHEAD, len(reads)):
-        issue(nxt)
-        nxt += 1
+    after = {}
+    for f in range(max(pre, AHEAD), nfr):
+        after.setdefault(f - AHEAD, []).append((kind, f, reads[f]))
+    n_next = 0
+    if nxt:
+        nkind, nreads = nxt
+        for m in range(len(nreads)):
+            at = nfr + m - AHEAD
+            if at > nfr - 1:
+                break
+            if gate_at is not None:
+                at = max(at, gate_at)
+            after.setdefault(at, []).append((nkind, m, nreads[m]))
+            n_next += 1
+    for f in range(pre, min(AHEAD, nfr)):
+        issue(kind, f, reads[f])
     n = len(mfmas)
     per = [0] * n
     for i in range(len(valu)):
@@ -287,19 +308,29 @@ def interleave(e, reads, mfmas, valu):
     vi = 0
     for i, (f, text) in enumerate(mfmas):
         if i == 0 or mfmas[i - 1][0] != f:
-            after = len(issued) - 1 - issued.index(f"R{f}")
-            e(f"s_waitcnt lgkmcnt({min(after, 15)})")
-        e(text.format(ring=RINGR(slot[f])))
-        if (i + 1 == n or mfmas[i + 1][0] != f) and nxt < len(reads):
-            issue(nxt)
-            nxt += 1
+            pos = issued.index((kind, f))
+            e(f"s_waitcnt lgkmcnt({min(len(issued) - 1 - pos, 15)})")
+        e(text.format(ring=RINGR(f % RING)))
+        if i + 1 == n or mfmas[i + 1][0] != f:
+            if gate_at == f:
+                for op in gate:
+                    e(op)
+            for k, g, t in after.get(f, []):
+                issue(k, g, t)
         for _ in range(per[i]):
             op = valu[vi]
             vi += 1
             e(op)
             if op.startswith("ds_"):
-                issued.append("W")
+                issued.append(None)
     assert vi == len(valu)
+    assert gate_at is None or gate_at in {f for f, _ in mfmas}
+    return n_next
+
+
+def interleave(e, reads, mfmas, valu):
+    """A phase with nothing in flight before it and nothing read ahead for the next."""
+    phase(e, "X", reads, mfmas, valu)
 
 
 def mask(sbuf, j0):
@@ -569,14 +600,18 @@ def body_rest(e, in_dtype, out_dtype):
     def iteration(par, variant, masked_next=False):
         """Iteration j with S_cur = S(par), S_nxt = S(1 - par). variant: 'plain' (tile j + 1 fully seen by the
         wave's rows), 'masked', 'last' (no tile j + 1), 'first' (j = 0: tile 0's P and sums came from the exact
-        path; masked_next: tile 1 needs the mask)."""
+        path; masked_next: tile 1 needs the mask). Reads run across the phases: V^T(j)'s first reads go out in phase
+        QK's tail, and phase PV holds barrier j (after its V^T reads have landed) and then the first reads of
+        K(j + 2) for the next iteration's phase QK."""
         cur, nxt = par, 1 - par
         tag = f"{variant}{par}"
         valu = staging()
         if variant != "first":
             valu += pack_and_sum(cur)
+        n_v = 0
         if variant != "last":
-            interleave(e, k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu)
+            n_v = phase(e, "K", k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu, pre=0 if variant == "first" else N_K_AHEAD,
+                        nxt=("V", v_reads()))
         else:
             for op in valu:
                 e(op)
@@ -589,16 +624,21 @@ def body_rest(e, in_dtype, out_dtype):
             e(f"v_add_f32 {LSUM[0]}, {LSUM[0]}, {TMP[0]}")
             e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
             e.label(f"L_back_{tag}")
+            exact_v[tag] = n_v
         if variant != "last":
             for op in rotate(SBK, "k", KREGS, K_TILE):
                 e(op)
-        # phase PV
+        # phase PV, with barrier j
         valu = []
         if variant != "last":
             valu = ["s_nop 7", "s_nop 7"] + (mask(nxt, SJ0) if variant == "masked" or masked_next else []) + exps(nxt)
-        interleave(e, v_reads(), pv_mfmas(), valu)
+        n_k = phase(e, "V", v_reads(), pv_mfmas(), valu, pre=n_v, nxt=None if variant == "last" else ("K", k_reads("%[kr]")),
+                    gate_at=BAR_AT, gate=barrier())
+        assert variant == "last" or n_k == N_K_AHEAD
         for op in rotate(SBV, "v", VREGS, V_TILE):
             e(op)
+
+    exact_v = {}
 
     def exact_block(par, variant):
         tag = f"{variant}{par}"
@@ -610,14 +650,16 @@ def body_rest(e, in_dtype, out_dtype):
         exact_tile(e, in_dtype, par, TMP[15], SJX)
         e(f"v_add_f32 {LSUM[0]}, {LSUM[0]}, {TMP[0]}")
         e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
+        # the V^T reads phase QK sent ahead (their ring slots were reused here), again, as the last LDS instructions
+        reads = v_reads()
+        for f in range(exact_v[tag]):
+            e(reads[f].format(ring=RINGR(f % RING)))
         e(f"s_branch {lbl('L_back_' + tag)}")
 
     def dispatch(par, first=False):
-        """Barrier, then the variant of iteration SJ: this wave's last, one whose next tile needs the mask, plain."""
+        """The variant of iteration SJ: this wave's last, one whose next tile needs the mask, plain."""
         name = "first" if first else f"iter{par}"
         e.label(f"L_{name}")
-        for op in barrier():
-            e(op)
         e(f"s_add_u32 {ST[1]}, {SJ}, 1")
         e(f"s_cmp_ge_u32 {ST[1]}, %[ntw]")
         e(f"s_cbranch_scc1 {lbl(f'L_last_{name}')}")
@@ -645,7 +687,7 @@ def body_rest(e, in_dtype, out_dtype):
     e.label("L_last_first")
     for op in staging():
         e(op)
-    interleave(e, v_reads(), pv_mfmas(), [])
+    phase(e, "V", v_reads(), pv_mfmas(), [], gate_at=BAR_AT, gate=barrier())
     for op in rotate(SBV, "v", VREGS, V_TILE):
         e(op)
     e(f"s_add_u32 {SJ}, {SJ}, 1")
@@ -658,11 +700,12 @@ def body_rest(e, in_dtype, out_dtype):
     for par in (0, 1):
         for variant in ("plain", "masked", "last"):
             exact_block(par, variant)
-    # load-only iterations for the tiles the workgroup's other waves still compute
+    # load-only iterations for the tiles the workgroup's other waves still compute: the staging of iteration SJ,
+    # then its barrier
     e.label("L_tail")
     e("s_cmp_ge_u32 %s, %%[nt]" % SJ)
     e(f"s_cbranch_scc1 {lbl('L_epi')}")
-    for op in barrier() + staging():
+    for op in staging() + barrier():
         e(op)
     e(f"s_add_u32 {SJ}, {SJ}, 1")
     e(f"s_branch {lbl('L_tail')}")

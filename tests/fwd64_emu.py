@@ -1,7 +1,10 @@
 """CPU emulator of the instruction subset gen_attn_fwd64.py emits (flash_fwd_r64's stream), so the stream's logic is
 checked without a GPU: register-exact ALU, MFMA and LDS semantics in program order, one workgroup at a time with its
-barriers. Vector-memory loads land only at the s_waitcnt vmcnt that retires them (their destinations hold all-ones
-until then), so a read that does not wait, or a load into an LDS buffer still being read, shows in the results. It
+barriers. Vector-memory loads land only at the s_waitcnt vmcnt that retires them, and LDS reads (and lane permutes)
+only at the s_waitcnt lgkmcnt that retires them, reading LDS then (their destinations hold all-ones until they land),
+so a read that does not wait, a read into a register an earlier instruction still needs, a load into an LDS buffer
+still being read, or an LDS read left in flight across a barrier, shows in the results. The waves of the workgroup run
+one at a time from barrier to barrier, starting with a different wave each time. It
 reports LDS bank-conflict multiplicities too. Wait states (hardware hazards) are checked by fwd64_hazards.py."""
 import re
 
@@ -107,6 +110,7 @@ class Wave:
         self.done = False
         self.wid = wid
         self.vmq = []       # outstanding vector-memory loads: callables that land their data
+        self.lq = []        # outstanding LDS instructions, in issue order (LDS returns in order)
 
 
 def parse_reg(x):
@@ -219,6 +223,9 @@ class Emu:
             m = re.search(r'vmcnt\((\d+)\)', ' '.join(A))
             if m:
                 self.retire(w, int(m.group(1)))
+            m = re.search(r'lgkmcnt\((\d+)\)', ' '.join(A))
+            if m:
+                self.retire_lds(w, int(m.group(1)))
             return
         if mn == 's_nop':
             return
@@ -353,9 +360,15 @@ class Emu:
             kind, i, n, _ = parse_reg(A[0])
             addr = self.rd(w, A[1]).astype(np.int64) + op.mods.get('offset', 0)
             self.bank(op, addr, 16)
+            dst = w.v if kind == 'v' else w.a
             for q in range(4):
-                vals = np.array([self.lds[x + 4 * q: x + 4 * q + 4].view(np.uint32)[0] if 0 <= x + 4 * q + 4 <= len(self.lds) else 0 for x in addr], np.uint32)
-                (w.v if kind == 'v' else w.a)[i + q] = vals
+                dst[i + q] = 0xFFFFFFFF
+
+            def land(dst=dst, i=i, addr=addr):
+                for q in range(4):
+                    dst[i + q] = np.array([self.lds[x + 4 * q: x + 4 * q + 4].view(np.uint32)[0]
+                                           if 0 <= x + 4 * q + 4 <= len(self.lds) else 0 for x in addr], np.uint32)
+            w.lq.append(land)
         elif mn in ('ds_write_b128', 'ds_write_b64'):
             kind, i, n, _ = parse_reg(A[1])
             addr = self.rd(w, A[0]).astype(np.int64) + op.mods.get('offset', 0)
@@ -366,10 +379,13 @@ class Emu:
                     x = addr[l] + 4 * q
                     if 0 <= x and x + 4 <= len(self.lds):
                         self.lds[x:x + 4] = np.frombuffer(np.uint32(src[i + q][l]).tobytes(), np.uint8)
+            w.lq.append(lambda: None)
         elif mn == 'ds_bpermute_b32':
             addr = self.rd(w, A[1])
             src = self.rd(w, A[2])
-            self.wr(w, A[0], src[(addr // 4) % 64])
+            val = src[(addr // 4) % 64]
+            self.wr(w, A[0], np.full(64, 0xFFFFFFFF, np.uint32))
+            w.lq.append(lambda w=w, d=A[0], val=val: self.wr(w, d, val))
         elif mn == 'buffer_load_dwordx4' and op.mods.get('lds'):
             # LDS DMA: lane l's 16 bytes land at m0 + offset + 16 l when a vmcnt wait retires the load; until then
             # the destination holds garbage (catches reads that do not wait, and loads into buffers still read)
@@ -425,6 +441,10 @@ class Emu:
         while len(w.vmq) > n:
             w.vmq.pop(0)()
 
+    def retire_lds(self, w, n):
+        while len(w.lq) > n:
+            w.lq.pop(0)()
+
     def bank(self, op, addr, size):
         # lanes are served 128 bytes at a time: groups of 128 / size consecutive lanes must hit distinct
         # (addr / size) % (128 / size) slots
@@ -478,15 +498,19 @@ class Emu:
             dst[di + r] = vals
 
     def run_wg(self, waves):
+        rnd = 0
         while True:
             progressed = False
             at_barrier = []
-            for w in waves:
+            k = rnd % len(waves)
+            rnd += 1
+            for w in waves[k:] + waves[:k]:
                 if w.done:
                     continue
                 while True:
                     if w.pc >= len(self.prog):
                         self.retire(w, 0)
+                        self.retire_lds(w, 0)
                         w.done = True
                         break
                     r = self.step(w)

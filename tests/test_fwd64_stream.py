@@ -58,6 +58,16 @@ def test_planted_missing_wait_state_is_found():
     assert Hz.check(lines[:i + 1] + lines[i + 2:], "planted") > 0
 
 
+def test_planted_barrier_without_lds_wait_is_found(monkeypatch):
+    """Phase PV's barrier must follow the landing of its V^T reads: without the lgkmcnt(0), another wave's staging
+    after the barrier overwrites the buffer those reads still sample."""
+    if G.STAGING != "dma":
+        pytest.skip("the staging in use has no DMA wait")
+    monkeypatch.setattr(G, "barrier", lambda: [f"s_waitcnt vmcnt({G.DMA_PER_TILE})", "s_barrier"])
+    r = R.run(4, 1, 64, 448, 0, 0, seed=9, verbose=False)
+    assert r["out_bad"] > 0
+
+
 def test_planted_short_barrier_wait_is_found(monkeypatch):
     if G.STAGING != "dma":
         pytest.skip("the staging in use has no DMA wait")
