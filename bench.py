@@ -456,7 +456,8 @@ def bench_sparse(torch, M, steps, warmup, with_cpu):
            "kernel_ms": round(kms, 4), "dtype": "bf16", "blocks": blocks,
            "gathered_gbps": round(gathered / (kms * 1e-3) / 1e9, 1),
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": kt / PEAK_TFLOPS, "traffic": hbm, "kernel": "flash_sparse8<bf16,bf16>",
+                        "frac": kt / PEAK_TFLOPS, "traffic": hbm,
+                        "kernel": "sparse_prep<bf16> + flash_sparse_r64<bf16,bf16> (one call, both kernels)",
                         "kernel_ms": kms,
                         "hbm_frac": None if hbm is None else hbm / (kms * 1e-3) / 1e9 / PEAK_GBPS,
                         "note": "gathered K + V (1.105 GB) is L2 traffic; HBM moves the counted bytes"},

@@ -120,7 +120,10 @@ int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_
  * dense rows [dense0, dense1); a later tile attends [0, n_k); keys with valid[j] == 0 are masked; query row r's
  * output goes to o row map[r] (dropped when map[r] < 0). Requires q_pad % 64 == 0, k_pad % 128 == 0,
  * dense0 % 32 == 0 (the reference's checks) and n_cubes * 64 <= k_pad. lse [heads][q_pad] by tile row (may be
- * NULL).
+ * NULL). Lists shared by a kv head's query heads (sel_heads == kv_heads) in groups of 4, with dense0 % 64 == 0
+ * and valid 16-byte aligned, take a route that first writes f16 V^T tile images and a pass table into a workspace
+ * per (device, stream), allocated stream-ordered the first time a call needs it (or more of it); other calls
+ * allocate nothing.
  */
 int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
                      const void* v, void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,

@@ -26,6 +26,14 @@
 #include "device.hpp"
 
 namespace mako {
+
+// attn_sparse64.hip: the r64 route for lists shared in groups of 4.
+bool sparse64_fits(const mako_sparse_args* a, const void* valid);
+template <class T, class TO>
+int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+                    const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map, float* lse,
+                    hipStream_t s);
+
 namespace {
 
 constexpr int kD = 128;
@@ -809,6 +817,19 @@ extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_d
     if (p.n_qt > 65535)
         return fail(MAKO_EINVAL, "attention_sparse: %u query tiles exceed the grid", p.n_qt);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (sparse64_fits(a, valid)) {
+        const float sl = a->scale * kLog2e;
+        int r;
+        if (in == MAKO_BF16)
+            r = out == MAKO_F32 ? launch_sparse64<__bf16, float>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s)
+                                : launch_sparse64<__bf16, __bf16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s);
+        else
+            r = out == MAKO_F32 ? launch_sparse64<_Float16, float>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s)
+                                : launch_sparse64<_Float16, _Float16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s);
+        if (r < 0)
+            return fail(MAKO_EHIP, "attention_sparse: no device memory for the V^T images and the pass table");
+        return check_launch("attention_sparse");
+    }
     if (in == MAKO_BF16) {
         if (out == MAKO_F32)
             launch_sparse<__bf16, float>(p, s);

@@ -1,0 +1,88 @@
+// Pieces the r64 attention kernels share (attn_fwd64.hip: dense, attn_sparse64.hip: block-sparse): the LDS tile
+// geometry their generated stream assumes (gen_attn_fwd64.py), the K slot order, and the f16 V^T tile images they
+// stage from. Internal linkage: each file gets its own copies.
+#pragma once
+
+#include "attn_fwd64_asm.inc"
+#include "device.hpp"
+
+namespace mako {
+namespace {
+
+constexpr uint32_t kKRow = 272;            // LDS bytes of a K row: 256 + 16 of padding
+constexpr uint32_t kKTile = 64 * kKRow;    // a K tile of 64 keys
+constexpr uint32_t kVTile = 128 * 64 * 2;  // a V^T tile: 128 head dims x 64 keys in f16
+constexpr uint32_t kNBuf = MAKO_FWD64_NBUF; // LDS tile buffers
+constexpr uint32_t kLdsBytes = kNBuf * (kKTile + kVTile);
+
+__device__ __forceinline__ uint32_t slot_of(uint32_t row)
+{
+    return (row & ~12u) | ((row & 4u) << 1) | ((row & 8u) >> 1);
+}
+
+// XOR swizzle of the 16-byte key chunks in row d of a V^T tile: a bijection on d mod 8 (eight consecutive rows read
+// one chunk column from eight distinct bank groups) that depends on d mod 32 only (the four 32-row blocks of a
+// fragment read differ by an immediate offset).
+__device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d & 7u) ^ ((d >> 3) & 3u); }
+
+// The V^T tile images: tile t of kv head h is 16 KiB, row d (head dim) of 128 bytes holding keys 64 t .. 64 t + 63 in
+// f16, the 16-byte chunk of keys 64 t + 8 c .. + 7 at slot c ^ vt_swz(d): the LDS layout the kernel reads, so its
+// staging copies tiles unchanged. Keys >= n_k are zero. bf16 becomes f16 rounding toward zero (v_cvt_pkrtz), as the
+// staging of the other attention kernels does. 128 threads make a tile: thread (c, e) loads keys 8 c .. 8 c + 7,
+// head dims 8 e .. 8 e + 7 (eight 16-byte loads; 16 threads cover a 256-byte key row), transposes the 8 x 8 block
+// in registers and stores the eight 16-byte chunks of its head dims.
+// vt_image_tiles: the two tiles 2 bx, 2 bx + 1 of kv head kvh (a workgroup of 256 threads).
+template <class T>
+__device__ __forceinline__ void vt_image_tiles(const T* v, uint32_t* img, uint32_t n_k, uint32_t k_pad, uint32_t n_vt,
+                                               uint32_t bx, uint32_t kvh)
+{
+    const uint32_t tile = bx * 2 + (threadIdx.x >> 7);
+    if (tile >= n_vt)
+        return;
+    const uint32_t t = threadIdx.x & 127, e = t & 15, c = t >> 4;
+    const u32x4* src = reinterpret_cast<const u32x4*>(v + ((size_t)kvh * k_pad + (size_t)tile * 64 + 8 * c) * 128) + e;
+    uint32_t x[8][4];  // x[i][m]: head dims 8 e + 2 m, + 1 of key 8 c + i (f16 pairs)
+    #pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        u32x4 r = u32x4{0u, 0u, 0u, 0u};
+        if (tile * 64 + 8 * c + i < n_k)
+            r = __builtin_nontemporal_load(src + 16 * i);
+        #pragma unroll
+        for (uint32_t m = 0; m < 4; ++m) {
+            if constexpr (__is_same(T, __bf16)) {
+                const float lo = __builtin_bit_cast(float, r[m] << 16);
+                const float hi = __builtin_bit_cast(float, r[m] & 0xffff0000u);
+                x[i][m] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+            } else {
+                x[i][m] = r[m];
+            }
+        }
+    }
+    uint32_t* dst = img + ((size_t)kvh * n_vt + tile) * 4096;
+    #pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {  // head dim d = 8 e + j: keys 8 c + 2 q, + 1 in dword q
+        const uint32_t d = 8 * e + j, m = j >> 1, sh = 16 * (j & 1);
+        u32x4 out;
+        #pragma unroll
+        for (uint32_t q = 0; q < 4; ++q)
+            out[q] = ((x[2 * q][m] >> sh) & 0xffffu) | (((x[2 * q + 1][m] >> sh) & 0xffffu) << 16);
+        *reinterpret_cast<u32x4*>(dst + d * 32 + 4 * (c ^ vt_swz(d))) = out;
+    }
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void vt_image(const T* v, uint32_t* img, uint32_t n_k, uint32_t k_pad, uint32_t n_vt)
+{
+    vt_image_tiles<T>(v, img, n_k, k_pad, n_vt, blockIdx.x, blockIdx.y);
+}
+
+// A raw buffer descriptor (gfx9 layout) over `bytes` bytes at `base`: offsets at or past the end load zeros and drop
+// stores.
+__device__ __forceinline__ u32x4 rsrc_of(const void* base, uint32_t bytes)
+{
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+}  // namespace
+}  // namespace mako

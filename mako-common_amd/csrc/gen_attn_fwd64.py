@@ -114,6 +114,16 @@ SKWW = "s67"      # DMA: SKW + 1 KiB x (wave index), this wave's first K piece
 SVWW = "s84"      # DMA: LDS address of this wave's 4 KiB of the V^T image of buffer SBW
 SM0 = "s87"       # DMA: the compiler's M0, restored at the end
 
+# The block-sparse stream (body(..., sparse=True)): each tile's first key, and the validity of its keys, come from the
+# item's pass table (%[ent]: 16 bytes an entry, {first key or -1 for none, 0, W0, W1}; bit 16 t + r of W_g: key
+# 32 t + 16 (r / 8) + 8 g + r % 8 of the tile may be seen), read with scalar loads an iteration ahead.
+SPARSE = False
+SD = "s65"              # first key of the tile the next staging loads (-1: none, loads zeros)
+SEJ = "s86"             # first key of the tile the next phase PV masks (the exact path's is ST[0])
+SEW = "s[94:95]"        # that tile's validity words (the exact path's are s[78:79]); the fourth lane-mask pair,
+SEW_LO, SEW_HI = "s94", "s95"   # which the sparse stream's masks leave alone
+MAPV = "v184"           # the output row map[q0 + lane] (-1: dropped)
+
 
 def KSTG(m):      # staged K piece m (0..3: pieces w + 4 m; 4: piece 16)
     return f"v[{184 + 4 * m}:{187 + 4 * m}]"
@@ -130,6 +140,8 @@ def quad(r):
 CLOBBER_V = 184 if STAGING == "dma" else 220
 CLOBBER_A = 224
 CLOBBER_S = (60, 100)
+CLOBBER_V_SPARSE = 185     # + MAPV
+CLOBBER_S_SPARSE = (60, 100)
 
 
 class Emit:
@@ -202,15 +214,23 @@ def dma_issue():
     the sources move on by a tile and the destinations to the next buffer. K: pieces w, w + 4, w + 8, w + 12 of the
     17 KiB image at M0 = their LDS address, and piece 16 (every wave; the same bytes to the same place). V^T: the
     wave's 4 KiB of the tile image, as four 1 KiB loads whose offset moves source and destination alike. A write of
-    M0 is read by an LDS load after one wait state. Record counts shrink by a tile and stop at zero."""
+    M0 is read by an LDS load after one wait state. Record counts shrink by a tile and stop at zero. Sparse: the
+    sources are set from SD, the tile's first key (K rows and V^T images are both 256 bytes a key), one tile long, or
+    empty when SD is -1."""
     ops = []
+    if SPARSE:
+        t = SROT["k"]
+        ops += [f"s_lshl_b32 {t}, {SD}, 8",
+                f"s_add_u32 {KRS[0]}, %[kb0], {t}", f"s_addc_u32 {KRS[1]}, %[kb1], 0",
+                f"s_add_u32 {VRS[0]}, %[vb0], {t}", f"s_addc_u32 {VRS[1]}, %[vb1], 0",
+                f"s_cmp_eq_u32 {SD}, -1", f"s_cselect_b32 {KRS[2]}, 0, 0x4000", f"s_mov_b32 {VRS[2]}, {KRS[2]}"]
     for m in range(4):
         ops += [f"s_add_u32 m0, {SKWW}, {4096 * m}" if m else f"s_mov_b32 m0, {SKWW}", "s_nop 0",
                 f"buffer_load_dwordx4 %[kd{m}], {quad(KRS)}, 0 offen lds"]
     ops += [f"s_add_u32 m0, {SKW}, {16 * 1024}", "s_nop 0", f"buffer_load_dwordx4 %[kd4], {quad(KRS)}, 0 offen lds"]
     ops += [f"s_mov_b32 m0, {SVWW}", "s_nop 0"]
     ops += [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds" for i in range(4)]
-    for r in (KRS, VRS):
+    for r in (KRS, VRS) if not SPARSE else ():
         ops += [f"s_add_u32 {r[0]}, {r[0]}, 0x4000", f"s_addc_u32 {r[1]}, {r[1]}, 0",
                 f"s_sub_u32 {r[2]}, {r[2]}, 0x4000", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
     wk, wv = SROT["wk"], SROT["wv"]
@@ -338,9 +358,10 @@ def mask(sbuf, j0):
     (the limit: the reference's visibility rule collapsed to `key < lim` for the lane's row)."""
     ops = [f"v_sub_u32 {TMP[rb]}, %[lim{rb}], {j0}" for rb in range(2)]
     elems = [(rb, t, r) for rb in range(2) for t in range(2) for r in range(16)]
-    cmp = [f"v_cmp_lt_i32 {SMASK[i % 4]}, {32 * t + 16 * (r >> 3) + (r & 7)}, {TMP[rb]}"
+    nm = 3 if SPARSE else 4   # the sparse stream keeps the fourth pair for SEW
+    cmp = [f"v_cmp_lt_i32 {SMASK[i % nm]}, {32 * t + 16 * (r >> 3) + (r & 7)}, {TMP[rb]}"
            for i, (rb, t, r) in enumerate(elems)]
-    cnd = [f"v_cndmask_b32 {S(sbuf, rb, t, r)}, {NINF}, {S(sbuf, rb, t, r)}, {SMASK[i % 4]}"
+    cnd = [f"v_cndmask_b32 {S(sbuf, rb, t, r)}, {NINF}, {S(sbuf, rb, t, r)}, {SMASK[i % nm]}"
            for i, (rb, t, r) in enumerate(elems)]
     # a compare's mask is read three instructions later (a VALU-written lane mask needs two wait states)
     ops += cmp[:2]
@@ -349,6 +370,36 @@ def mask(sbuf, j0):
             ops.append(cmp[i + 2])
         ops.append(cnd[i])
     return ops
+
+
+def mask_general(sbuf, j0, w):
+    """Sparse masking of a tile (first key in scalar j0, validity words in the SGPR pair w): the row limit as mask(),
+    then the keys whose validity bit is clear. The lane's word W_g is w shifted right by 32 g (%[g32])."""
+    ops = [f"v_sub_u32 {TMP[rb]}, %[lim{rb}], {j0}" for rb in range(2)]
+    wlo = int(TMP[2][1:])
+    ops.append(f"v_lshrrev_b64 v[{wlo}:{wlo + 1}], %[g32], {w}")
+    for t in range(2):
+        for r in range(16):
+            key = 32 * t + 16 * (r >> 3) + (r & 7)
+            ops += [f"v_cmp_lt_i32 {SMASK[0]}, {key}, {TMP[0]}",
+                    f"v_cmp_lt_i32 {SMASK[1]}, {key}, {TMP[1]}",
+                    f"v_bfe_u32 {TMP[4]}, {TMP[2]}, {16 * t + r}, 1",
+                    f"v_cmp_ne_u32 {SMASK[2]}, 0, {TMP[4]}",
+                    f"v_cndmask_b32 {S(sbuf, 0, t, r)}, {NINF}, {S(sbuf, 0, t, r)}, {SMASK[0]}",
+                    f"v_cndmask_b32 {S(sbuf, 1, t, r)}, {NINF}, {S(sbuf, 1, t, r)}, {SMASK[1]}",
+                    f"v_cndmask_b32 {S(sbuf, 0, t, r)}, {NINF}, {S(sbuf, 0, t, r)}, {SMASK[2]}",
+                    f"v_cndmask_b32 {S(sbuf, 1, t, r)}, {NINF}, {S(sbuf, 1, t, r)}, {SMASK[2]}"]
+    return ops
+
+
+def entry_loads():
+    """Sparse: the scalar loads for iteration SJ + 1, issued in phase PV of iteration SJ (before its barrier, whose
+    lgkmcnt(0) retires them): entry SJ + 2 (the tile it masks) into SEJ / SEW, and the first key of tile SJ + 4 (the
+    tile it stages) into SD."""
+    t = ST[0]
+    return [f"s_lshl_b32 {t}, {SJ}, 4", f"s_add_u32 {t}, {t}, 32", f"s_load_dword {SEJ}, %[ent], {t}",
+            f"s_add_u32 {t}, {t}, 8", f"s_load_dwordx2 {SEW}, %[ent], {t}",
+            f"s_add_u32 {t}, {t}, 24", f"s_load_dword {SD}, %[ent], {t}"]
 
 
 def exps(sbuf):
@@ -392,13 +443,13 @@ def wait_mfma():
     return ["s_nop 7", "s_nop 7", "s_nop 4"]
 
 
-def exact_tile(e, dtype, sbuf, kaddr, j0, first=False):
+def exact_tile(e, dtype, sbuf, kaddr, j0, first=False, w=None):
     """The exact path for a tile (K at LDS address kaddr, first key in scalar j0): its raw scores into S(sbuf), the
     mask, each row's maximum, the reference's rule for moving the running maximum (outputs and sums rescaled when it
     moves), the exponentials, P and the sums (TMP[0], TMP[4]). first: the wave's first tile, where the outputs and
     sums are still zero and need no rescaling."""
     interleave(e, k_reads(kaddr), qk_mfmas(dtype, sbuf), [])
-    for op in wait_mfma() + mask(sbuf, j0):
+    for op in wait_mfma() + (mask_general(sbuf, j0, w) if SPARSE else mask(sbuf, j0)):
         e(op)
     for rb in range(2):
         mx = TMP[2 + rb]
@@ -452,6 +503,11 @@ def epilogue(e, out_dtype):
     are dropped; LSE offsets of rows past n_q are outside its buffer."""
     e("s_waitcnt vmcnt(0) lgkmcnt(0)")
     e("s_barrier")
+    if SPARSE:
+        # rows past n_q are dropped (%[mlive] is 0 for them)
+        e("v_cmp_ne_u32 vcc, 0, %[mlive]")
+        e("s_nop 1")
+        e(f"v_cndmask_b32 {MAPV}, -1, {MAPV}, vcc")
     for op in wait_mfma():
         e(op)
     sz = {"f32": 4, "bf16": 2, "f16": 2}[out_dtype]
@@ -508,6 +564,25 @@ def epilogue(e, out_dtype):
         addr = f"v{128 + i}"
         e(f"v_xor_b32 {addr}, {swz}, %[er]")
         e(f"ds_read_b128 v[{4 * i}:{4 * i + 3}], {addr} offset:{1024 * i}")
+    if SPARSE:
+        # output row map[q0 + row] from the lane holding it (MAPV), as a 64-bit address: row x (width x bytes) +
+        # %[ocol] (o, the head's columns and the lane's chunk); dropped rows (-1) are left out of exec for their store
+        for i in range(n_ld):
+            a = f"v{128 + i}"
+            e(f"v_add_u32 {a}, {4 * rows_i * i}, %[mp]")
+            e(f"ds_bpermute_b32 {a}, {a}, {MAPV}")
+        e("s_waitcnt lgkmcnt(0)")
+        pairs = [(int(TMP[8 + 2 * k][1:]), int(TMP[9 + 2 * k][1:])) for k in range(4)]
+        for i in range(n_ld):
+            a = f"v{128 + i}"
+            lo, hi = pairs[i % 4]
+            e(f"v_mad_u64_u32 v[{lo}:{hi}], {SCMP[1]}, {a}, %[ows], %[ocol]")
+            e(f"v_cmp_le_i32 vcc, 0, {a}")
+            e("s_nop 1")
+            e(f"s_and_saveexec_b64 {SCMP[0]}, vcc")
+            e(f"global_store_dwordx4 v[{lo}:{hi}], v[{4 * i}:{4 * i + 3}], off")
+            e(f"s_mov_b64 exec, {SCMP[0]}")
+        return
     # global addresses alternate between two registers, each moved on by two loads' rows after its store
     ga = (TMP[4], TMP[5])
     e(f"v_mov_b32 {ga[0]}, %[og]")
@@ -524,8 +599,28 @@ def epilogue(e, out_dtype):
 
 # ---- the kernel body ----------------------------------------------------------------------------------------------
 
-def body(in_dtype, out_dtype):
+def body(in_dtype, out_dtype, sparse=False):
+    """The stream for one item (a workgroup's rows); sparse: the block-sparse one (tiles from the pass table)."""
+    global SPARSE
+    SPARSE = sparse
+    try:
+        return body_of(in_dtype, out_dtype)
+    finally:
+        SPARSE = False
+
+
+def body_of(in_dtype, out_dtype):
     e = Emit()
+    if SPARSE:
+        assert STAGING == "dma", "the sparse stream stages by LDS DMA"
+        # the pass table's first entries: the first keys of tiles 0-3, entry 1 (iteration 0 masks tile 1), entry 0
+        # (tile 0's exact path, in ST); and the row map
+        for i, r in enumerate(("s88", "s89", "s90", "s91")):
+            e(f"s_load_dword {r}, %[ent], {16 * i}")
+        e(f"s_load_dword {SEJ}, %[ent], 16")
+        e(f"s_load_dwordx2 {SEW}, %[ent], 24")
+        e(f"s_load_dwordx4 s[76:79], %[ent], 0")
+        e(f"buffer_load_dword {MAPV}, %[mo], %[mrs], 0 offen")
     e(f"s_mov_b32 {S256}, 0x43800000")
     e(f"v_mov_b32 {NINF}, 0xff800000")
     e(f"v_mov_b32 {ZERO}, 0")
@@ -552,9 +647,15 @@ def body(in_dtype, out_dtype):
         e(f"s_mov_b32 {SKW}, %[skw]")
         e(f"s_mov_b32 {SKWW}, %[skww]")
         e(f"s_mov_b32 {SVWW}, %[svww]")
-        for _ in range(3):
+        if SPARSE:
+            e("s_waitcnt lgkmcnt(0)")
+        for i in range(3):
+            if SPARSE:
+                e(f"s_mov_b32 {SD}, s{88 + i}")
             for op in dma_issue():
                 e(op)
+        if SPARSE:
+            e(f"s_mov_b32 {SD}, s91")
         for i in range(128):
             e(f"v_accvgpr_write_b32 a{i}, 0")
     else:
@@ -592,15 +693,19 @@ def body_rest(e, in_dtype, out_dtype):
     e("s_cmp_eq_u32 %[ntw], 0")
     e(f"s_cbranch_scc1 {lbl('L_tail')}")
     # tile 0 by the exact path
-    e(f"s_mov_b32 {SJX}, 0")
-    exact_tile(e, in_dtype, 0, "%[kr]", SJX, first=True)
+    if SPARSE:
+        exact_tile(e, in_dtype, 0, "%[kr]", ST[0], first=True, w="s[78:79]")
+    else:
+        e(f"s_mov_b32 {SJX}, 0")
+        exact_tile(e, in_dtype, 0, "%[kr]", SJX, first=True)
     e(f"v_add_f32 {LSUM[0]}, {LSUM[0]}, {TMP[0]}")
     e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
 
     def iteration(par, variant, masked_next=False):
         """Iteration j with S_cur = S(par), S_nxt = S(1 - par). variant: 'plain' (tile j + 1 fully seen by the
-        wave's rows), 'masked', 'last' (no tile j + 1), 'first' (j = 0: tile 0's P and sums came from the exact
-        path; masked_next: tile 1 needs the mask). Reads run across the phases: V^T(j)'s first reads go out in phase
+        wave's rows), 'masked' (by the row limits), 'general' (sparse: the limits and the validity words), 'last'
+        (no tile j + 1), 'first' (j = 0: tile 0's P and sums came from the exact path; masked_next: tile 1's mask
+        kind). Reads run across the phases: V^T(j)'s first reads go out in phase
         QK's tail, and phase PV holds barrier j (after its V^T reads have landed) and then the first reads of
         K(j + 2) for the next iteration's phase QK."""
         cur, nxt = par, 1 - par
@@ -631,7 +736,13 @@ def body_rest(e, in_dtype, out_dtype):
         # phase PV, with barrier j
         valu = []
         if variant != "last":
-            valu = ["s_nop 7", "s_nop 7"] + (mask(nxt, SJ0) if variant == "masked" or masked_next else []) + exps(nxt)
+            kind = masked_next or variant
+            m = mask(nxt, SJ0) if kind == "masked" else mask_general(nxt, SJ0, SEW) if kind == "general" else []
+            # sparse: the next entries load once this phase has read SEW (the general mask's third instruction)
+            loads = entry_loads() if SPARSE else []
+            valu = ["s_nop 7", "s_nop 7"] + m[:3] + loads + m[3:] + exps(nxt)
+        elif SPARSE:
+            valu = entry_loads()
         n_k = phase(e, "V", v_reads(), pv_mfmas(), valu, pre=n_v, nxt=None if variant == "last" else ("K", k_reads("%[kr]")),
                     gate_at=BAR_AT, gate=barrier())
         assert variant == "last" or n_k == N_K_AHEAD
@@ -646,8 +757,15 @@ def body_rest(e, in_dtype, out_dtype):
         # K of tile j is in buffer SBV (the buffer whose V^T is read next)
         e(f"s_mul_i32 {ST[0]}, {SBV}, {K_TILE}")
         e(f"v_add_u32 {TMP[15]}, {ST[0]}, %[kr0]")
-        e(f"s_lshl_b32 {SJX}, {SJ}, 6")
-        exact_tile(e, in_dtype, par, TMP[15], SJX)
+        if SPARSE:
+            # tile j's entry (its first key and validity words) into ST
+            e(f"s_lshl_b32 {SROT['wk']}, {SJ}, 4")
+            e(f"s_load_dwordx4 s[76:79], %[ent], {SROT['wk']}")
+            e("s_waitcnt lgkmcnt(0)")
+            exact_tile(e, in_dtype, par, TMP[15], ST[0], w="s[78:79]")
+        else:
+            e(f"s_lshl_b32 {SJX}, {SJ}, 6")
+            exact_tile(e, in_dtype, par, TMP[15], SJX)
         e(f"v_add_f32 {LSUM[0]}, {LSUM[0]}, {TMP[0]}")
         e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
         # the V^T reads phase QK sent ahead (their ring slots were reused here), again, as the last LDS instructions
@@ -657,13 +775,20 @@ def body_rest(e, in_dtype, out_dtype):
         e(f"s_branch {lbl('L_back_' + tag)}")
 
     def dispatch(par, first=False):
-        """The variant of iteration SJ: this wave's last, one whose next tile needs the mask, plain."""
+        """The variant of iteration SJ: this wave's last, one whose next tile needs the mask, plain (sparse: also
+        one whose next tile has keys that are not valid)."""
         name = "first" if first else f"iter{par}"
         e.label(f"L_{name}")
         e(f"s_add_u32 {ST[1]}, {SJ}, 1")
         e(f"s_cmp_ge_u32 {ST[1]}, %[ntw]")
         e(f"s_cbranch_scc1 {lbl(f'L_last_{name}')}")
-        e(f"s_lshl_b32 {SJ0}, {ST[1]}, 6")
+        if SPARSE:
+            e(f"s_mov_b32 {SJ0}, {SEJ}")
+            e(f"s_and_b32 {ST[2]}, {SEW_LO}, {SEW_HI}")
+            e(f"s_cmp_eq_u32 {ST[2]}, -1")
+            e(f"s_cbranch_scc0 {lbl(f'L_general_{name}')}")
+        else:
+            e(f"s_lshl_b32 {SJ0}, {ST[1]}, 6")
         e(f"s_add_u32 {ST[2]}, {SJ0}, 64")
         e(f"s_cmp_le_u32 {ST[2]}, %[lmin]")
         e(f"s_cbranch_scc0 {lbl(f'L_masked_{name}')}")
@@ -671,9 +796,16 @@ def body_rest(e, in_dtype, out_dtype):
         e(f"s_branch {lbl(f'L_next_{name}')}")
         e.label(f"L_masked_{name}")
         if first:
-            iteration(0, "first", masked_next=True)
+            iteration(0, "first", masked_next="masked")
         else:
             iteration(par, "masked")
+        if SPARSE:
+            e(f"s_branch {lbl(f'L_next_{name}')}")
+            e.label(f"L_general_{name}")
+            if first:
+                iteration(0, "first", masked_next="general")
+            else:
+                iteration(par, "general")
         e.label(f"L_next_{name}")
         e(f"s_add_u32 {SJ}, {SJ}, 1")
 
@@ -698,13 +830,18 @@ def body_rest(e, in_dtype, out_dtype):
         e(f"s_add_u32 {SJ}, {SJ}, 1")
         e(f"s_branch {lbl('L_tail')}")
     for par in (0, 1):
-        for variant in ("plain", "masked", "last"):
+        for variant in ("plain", "masked", "last") + (("general",) if SPARSE else ()):
             exact_block(par, variant)
     # load-only iterations for the tiles the workgroup's other waves still compute: the staging of iteration SJ,
     # then its barrier
     e.label("L_tail")
     e("s_cmp_ge_u32 %s, %%[nt]" % SJ)
     e(f"s_cbranch_scc1 {lbl('L_epi')}")
+    if SPARSE:
+        e(f"s_lshl_b32 {ST[0]}, {SJ}, 4")
+        e(f"s_add_u32 {ST[0]}, {ST[0]}, 48")
+        e(f"s_load_dword {SD}, %[ent], {ST[0]}")
+        e("s_waitcnt lgkmcnt(0)")
     for op in staging() + barrier():
         e(op)
     e(f"s_add_u32 {SJ}, {SJ}, 1")
@@ -715,37 +852,41 @@ def body_rest(e, in_dtype, out_dtype):
         e(f"s_mov_b32 m0, {SM0}")
 
 
-def clobbers():
-    regs = [f'"v{i}"' for i in range(CLOBBER_V)] + [f'"a{i}"' for i in range(CLOBBER_A)]
-    regs += [f'"s{i}"' for i in range(*CLOBBER_S)]
+def clobbers(sparse=False):
+    regs = [f'"v{i}"' for i in range(CLOBBER_V_SPARSE if sparse else CLOBBER_V)]
+    regs += [f'"a{i}"' for i in range(CLOBBER_A)]
+    regs += [f'"s{i}"' for i in range(*(CLOBBER_S_SPARSE if sparse else CLOBBER_S))]
     return ", ".join(regs)
 
 
-def check_registers(lines):
+def check_registers(lines, sparse=False):
     """Every register the stream names must be one the clobber list reserves (the wave is only given those)."""
     import re
     for ln in lines:
         for kind, one, lo, hi in re.findall(r"\b([vas])(?:(\d+)|\[(\d+):(\d+)\])", ln.split(";")[0]):
             top = int(one) if one else int(hi)
             bot = int(one) if one else int(lo)
-            limit = {"v": (0, CLOBBER_V), "a": (0, CLOBBER_A), "s": CLOBBER_S}[kind]
+            limit = {"v": (0, CLOBBER_V_SPARSE if sparse else CLOBBER_V), "a": (0, CLOBBER_A),
+                     "s": CLOBBER_S_SPARSE if sparse else CLOBBER_S}[kind]
             assert limit[0] <= bot and top < limit[1], f"{kind}{bot}..{top} outside the reserved registers: {ln}"
 
 
 def main():
     out = ["// Generated by gen_attn_fwd64.py (the instruction stream of flash_fwd_r64; the design is described there).",
            "// Do not edit: change the generator and run it.", "#pragma once", ""]
-    for ind in ("bf16", "f16"):
-        for outd in ("f32", ind):
-            lines = body(ind, outd)
-            check_registers(lines)
-            name = f"MAKO_FWD64_ASM_{ind.upper()}_{outd.upper()}"
-            out.append(f"#define {name} \\")
-            for ln in lines:
-                out.append(f'    "{ln}\\n" \\')
-            out.append('    ""')
-            out.append("")
+    for sparse in (False, True) if STAGING == "dma" else (False,):
+        for ind in ("bf16", "f16"):
+            for outd in ("f32", ind):
+                lines = body(ind, outd, sparse)
+                check_registers(lines, sparse)
+                name = f"MAKO_{'SPARSE64' if sparse else 'FWD64'}_ASM_{ind.upper()}_{outd.upper()}"
+                out.append(f"#define {name} \\")
+                for ln in lines:
+                    out.append(f'    "{ln}\\n" \\')
+                out.append('    ""')
+                out.append("")
     out.append(f"#define MAKO_FWD64_CLOBBERS {clobbers()}")
+    out.append(f"#define MAKO_SPARSE64_CLOBBERS {clobbers(True)}")
     out.append(f"#define MAKO_FWD64_DMA {1 if STAGING == 'dma' else 0}")
     out.append(f"#define MAKO_FWD64_NBUF {NBUF}")
     out.append("")

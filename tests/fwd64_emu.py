@@ -99,11 +99,19 @@ class Mem:
         self.b = np.zeros(size, np.uint8)
 
 
+POISON = [False]   # registers start as garbage (as on the GPU) instead of zeros
+
+
 class Wave:
     def __init__(self, wid):
         self.v = np.zeros((256, 64), np.uint32)
         self.a = np.zeros((256, 64), np.uint32)
         self.s = np.zeros(128, np.uint32)
+        if POISON[0]:
+            rng = np.random.default_rng(1000 + wid)
+            self.v = rng.integers(0, 2 ** 32, (256, 64), dtype=np.uint64).astype(np.uint32)
+            self.a = rng.integers(0, 2 ** 32, (256, 64), dtype=np.uint64).astype(np.uint32)
+            self.s = rng.integers(0, 2 ** 32, 128, dtype=np.uint64).astype(np.uint32)
         self.vcc = np.zeros(64, bool)
         self.scc = 0
         self.pc = 0
@@ -111,6 +119,8 @@ class Wave:
         self.wid = wid
         self.vmq = []       # outstanding vector-memory loads: callables that land their data
         self.lq = []        # outstanding LDS instructions, in issue order (LDS returns in order)
+        self.sq = []        # outstanding scalar loads: they return in any order, so they land at lgkmcnt(0) only
+        self.exec = np.ones(64, bool)
 
 
 def parse_reg(x):
@@ -226,6 +236,9 @@ class Emu:
             m = re.search(r'lgkmcnt\((\d+)\)', ' '.join(A))
             if m:
                 self.retire_lds(w, int(m.group(1)))
+                if int(m.group(1)) == 0:
+                    while w.sq:
+                        w.sq.pop(0)()
             return
         if mn == 's_nop':
             return
@@ -253,6 +266,59 @@ class Emu:
             r = self.sread(w, A[1]) & self.sread(w, A[2])
             w.s[parse_reg(A[0])[1]] = r
             w.scc = int(r != 0)
+        elif mn.startswith('s_load_dword'):
+            # scalar load: base pair A[1] + offset A[2] (register or immediate); the destination holds garbage until
+            # an lgkmcnt(0) wait
+            kind, i, n, _ = parse_reg(A[0])
+            _, b, _, _ = parse_reg(A[1])
+            addr = int(w.s[b]) | ((int(w.s[b + 1]) & 0xFFFF) << 32)
+            addr += self.sread(w, A[2])
+            vals = self.g.b[addr:addr + 4 * n].view(np.uint32).copy()
+            for q in range(n):
+                w.s[i + q] = 0xDEADBEEF
+
+            def land(w=w, i=i, vals=vals):
+                for q in range(len(vals)):
+                    w.s[i + q] = vals[q]
+            w.sq.append(land)
+        elif mn == 's_and_saveexec_b64':
+            m = self.mask_of(w, A[1])
+            self.set_mask(w, A[0], w.exec.copy())
+            w.exec = w.exec & m
+            w.scc = int(w.exec.any())
+        elif mn == 's_mov_b64' and A[0] == 'exec':
+            w.exec = self.mask_of(w, A[1])
+        elif mn == 'v_lshrrev_b64':
+            kd, di, _, _ = parse_reg(A[0])
+            sh = self.rd(w, A[1]).astype(np.uint64) & 63
+            _, si, _, _ = parse_reg(A[2])
+            val = np.uint64(int(w.s[si]) | (int(w.s[si + 1]) << 32))
+            r = np.array([int(val) >> int(x) for x in sh], np.uint64)
+            w.v[di] = (r & 0xFFFFFFFF).astype(np.uint32)
+            w.v[di + 1] = (r >> np.uint64(32)).astype(np.uint32)
+        elif mn == 'v_bfe_u32':
+            src, off, wid = self.rd(w, A[1]), self.rd(w, A[2]) & 31, self.rd(w, A[3]) & 31
+            self.wr(w, A[0], ((src >> off) & ((np.uint32(1) << wid) - np.uint32(1))).astype(np.uint32))
+        elif mn == 'v_mad_u64_u32':
+            kd, di, _, _ = parse_reg(A[0])
+            a, b = self.rd(w, A[2]).astype(np.uint64), self.rd(w, A[3]).astype(np.uint64)
+            ck, ci, _, _ = parse_reg(A[4])
+            c = (w.v[ci].astype(np.uint64) | (w.v[ci + 1].astype(np.uint64) << np.uint64(32))) if ck == 'v' else \
+                np.full(64, int(w.s[ci]) | (int(w.s[ci + 1]) << 32), np.uint64)
+            r = a * b + c
+            w.v[di] = (r & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+            w.v[di + 1] = (r >> np.uint64(32)).astype(np.uint32)
+        elif mn == 'global_store_dwordx4':
+            _, ai, _, _ = parse_reg(A[0])
+            _, di, n, _ = parse_reg(A[1])
+            for l in range(64):
+                if not w.exec[l]:
+                    continue
+                addr = int(w.v[ai][l]) | (int(w.v[ai + 1][l]) << 32)
+                assert 0 <= addr and addr + 16 <= len(self.g.b), f'global store at {addr:#x} out of range'
+                for q in range(4):
+                    self.g.b[addr + 4 * q:addr + 4 * q + 4] = np.frombuffer(np.uint32(w.v[di + q][l]).tobytes(),
+                                                                            np.uint8)
         elif mn == 's_mul_i32':
             w.s[parse_reg(A[0])[1]] = (self.sread(w, A[1]) * self.sread(w, A[2])) & 0xFFFFFFFF
         elif mn.startswith('s_cmp_'):
@@ -308,10 +374,13 @@ class Emu:
             _, _, cond, ty = mn.split('_')
             if ty == 'i32':
                 a, b = self.rd(w, A[1]).view(np.int32), self.rd(w, A[2]).view(np.int32)
+            elif ty == 'u32':
+                a, b = self.rd(w, A[1]), self.rd(w, A[2])
             else:
                 a, b = self.rdf(w, A[1]), self.rdf(w, A[2])
             with np.errstate(invalid='ignore'):
-                m = {'lt': a < b, 'gt': a > b, 'nle': ~(a <= b)}[cond]
+                m = {'lt': a < b, 'gt': a > b, 'le': a <= b, 'ne': a != b, 'eq': a == b,
+                     'nle': ~(a <= b)}[cond]
             self.set_mask(w, A[0], m)
         elif mn == 'v_cndmask_b32':
             m = self.mask_of(w, A[3])
@@ -403,13 +472,14 @@ class Emu:
             def land(d0=dst0, flat=flat):
                 self.lds[d0:d0 + 1024] = flat
             w.vmq.append(land)
-        elif mn == 'buffer_load_dwordx4':
+        elif mn in ('buffer_load_dwordx4', 'buffer_load_dword'):
             kind, i, n, _ = parse_reg(A[0])
             base, nrec = self.rsrc(w, A[2])
             off = self.rd(w, A[1]).astype(np.int64) + op.mods.get('offset', 0)
             dst = w.v if kind == 'v' else w.a
             got = []
-            for q in range(4):
+            nq = 4 if mn.endswith('x4') else 1
+            for q in range(nq):
                 vals = np.zeros(64, np.uint32)
                 for l in range(64):
                     o = off[l] + 4 * q
@@ -419,7 +489,7 @@ class Emu:
                 dst[i + q] = 0xFFFFFFFF
 
             def land(dst=dst, i=i, got=got):
-                for q in range(4):
+                for q in range(len(got)):
                     dst[i + q] = got[q]
             w.vmq.append(land)
         elif mn.startswith('buffer_store_dword'):

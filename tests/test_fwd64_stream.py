@@ -5,7 +5,10 @@ with conflict-free LDS access: causal GQA with a query offset and ragged sizes, 
 prefix-causal, f16 in and out, and inputs whose growing scores send most tiles down the exact path. Two planted
 mistakes show the checks have teeth: a dropped wait state after an M0 write, and barriers that let V^T tiles be read
 before their loads land. (Barriers that let only K tiles be read early are healed by the design: the garbage
-scores fail the row-sum check, and the exact path recomputes the tile after the next barrier, when it has landed.)"""
+scores fail the row-sum check, and the exact path recomputes the tile after the next barrier, when it has landed.)
+The block-sparse stream (flash_sparse_r64) gets the same register and hazard checks, and emulated shared-list cases
+(invalid keys, dense rows, rows past n_q, a map that drops rows; causal and not) against the oracle through the pass
+table restated in tests/sparse64_run.py, with a planted mistake in its validity masks."""
 import os
 import sys
 
@@ -73,4 +76,63 @@ def test_planted_short_barrier_wait_is_found(monkeypatch):
         pytest.skip("the staging in use has no DMA wait")
     monkeypatch.setattr(G, "barrier", lambda: [f"s_waitcnt vmcnt({3 * G.DMA_PER_TILE}) lgkmcnt(0)", "s_barrier"])
     r = R.run(4, 1, 64, 448, 0, 0, seed=9, verbose=False)
+    assert r["out_bad"] > 0
+
+
+# ---- the block-sparse stream (flash_sparse_r64: tiles, masks and output rows from the pass table and the row map) ----
+
+@pytest.mark.parametrize("ind,outd", VARIANTS)
+def test_sparse_registers_and_hazards(ind, outd):
+    lines = G.body(ind, outd, sparse=True)
+    G.check_registers(lines, sparse=True)
+    assert Hz.check(lines, f"sparse {ind}->{outd}") == 0
+
+
+def shared_lists_case(causal, seed):
+    """8 query heads over 2 kv heads, 5 cubes (one with 37 valid rows), 40 dense rows, rows past n_q and a map that
+    drops rows (tests/test_gpu_sparse.py's shared-lists case at its small size)."""
+    import numpy as np
+
+    heads, kv, cubes, dense, topk = 8, 2, 5, 40, 3
+    cnt = np.array([64, 64, 37, 64, 64])
+    n = cubes * 64 + dense
+    q_pad, k_pad = (n + 63) // 64 * 64, (n + 127) // 128 * 128
+    n_q = n - 10
+    valid = np.zeros(k_pad, np.uint8)
+    for c in range(cubes):
+        valid[c * 64:c * 64 + cnt[c]] = 1
+    valid[cubes * 64:n] = 1
+    map_ = np.full(q_pad, -1, np.int32)
+    keep = np.nonzero(valid[:n_q])[0]
+    map_[keep] = np.arange(len(keep), dtype=np.int32)
+    map_[keep[::7]] = -1
+    rng = np.random.default_rng(seed)
+    sel = np.zeros((kv, cubes, topk), np.uint16)
+    nsel = np.zeros((kv, cubes), np.uint16)
+    for h in range(kv):
+        for c in range(cubes):
+            ch = rng.permutation(np.arange(c + 1) if causal else np.arange(cubes))[:topk]
+            sel[h, c, :len(ch)] = ch
+            nsel[h, c] = len(ch)
+    return (heads, kv, sel, nsel, valid, map_), dict(n_q=n_q, q_pad=q_pad, n_k=n, k_pad=k_pad, n_cubes=cubes,
+                                                     max_sel=topk, dense0=cubes * 64, dense1=n, causal=causal)
+
+
+@pytest.mark.parametrize("causal,ind,outd", [(0, "bf16", "f32"), (1, "f16", "f16")])
+def test_sparse_stream_matches_oracle(causal, ind, outd):
+    import sparse64_run as SR
+
+    args, kw = shared_lists_case(causal, 41 + causal)
+    r = SR.run(*args, **kw, ind=ind, outd=outd, verbose=False)
+    assert r == dict(out_bad=0, lse_bad=0, untouched=0), r
+
+
+def test_sparse_planted_mask_shift_is_found(monkeypatch):
+    """Validity words shifted by a wrong amount (another operand's register in place of 32 g) mask the wrong keys."""
+    import sparse64_run as SR
+
+    monkeypatch.setattr(G, "mask_general", lambda sbuf, j0, w, f=G.mask_general: [
+        op.replace("%[g32]", "%[mo]") for op in f(sbuf, j0, w)])
+    args, kw = shared_lists_case(0, 41)
+    r = SR.run(*args, **kw, verbose=False)
     assert r["out_bad"] > 0

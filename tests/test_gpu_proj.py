@@ -62,6 +62,10 @@ CASES = [
     (1, 64, 1, O.F32, 0, 0, 0),
     (600, 512, 700, O.F32, 1, 520, 0),      # the split over several 128-row tiles
     (1100, 192, 2048, O.F32, 0, 0, 0),      # more tiles than the 8 XCDs take evenly
+    # bf16 activations with 2, 4 and 6 chunks of 32 (each of the prologue's and the tail's DMA waits), part tiles
+    (200, 64, 130, O.BF16, 0, 0, 0),
+    (129, 128, 200, O.BF16, 0, 136, 0),
+    (70, 192, 257, O.BF16, 0, 0, 260),
 ]
 
 
