@@ -326,8 +326,8 @@ def bench_few_rows(torch, M, steps, warmup, with_cpu, nqs=(1, 4, 16)):
         leg = {"ms": round(ms, 5), "kernel_ms": round(kms, 5), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                "roofline": {"bound": "hbm", "achieved": kg, "peak": PEAK_GBPS, "unit": "GB/s",
                             "frac": kg / PEAK_GBPS, "traffic": traffic(f"few_rows_nq{nq}"),
-                            "kernel": "decode_split<bf16,%d> + decode_merge<bf16> (one call, both kernels)"
-                                      % (1 if nq * H // KV <= 32 else 2), "kernel_ms": kms}}
+                            "kernel": "decode_coop<bf16> (%d column group%s) + decode_merge<bf16> (one call, both "
+                                      "kernels)" % ((1, "") if nq * H // KV <= 32 else (2, "s")), "kernel_ms": kms}}
         if with_cpu:
             import oracle as O
 

@@ -85,13 +85,14 @@ __device__ __forceinline__ uint32_t ctx_sum(const DecParams& p, uint32_t n, uint
     return s;
 }
 
-// The sequence b whose rows (laid end to end, kv_heads x ncg rows a key) hold row r, and the first row of its segments;
+// The sequence b whose rows (laid end to end, nseg rows a key) hold row r, and the first row of its segments;
 // b = batch when r is past them all. Lane-parallel as ctx_sum: an inclusive prefix over 64 sequences at a time, the
 // first lane whose end passes r.
-__device__ __forceinline__ void seq_of(const DecParams& p, uint32_t r, uint32_t lane, uint32_t& b, uint32_t& seg0)
+__device__ __forceinline__ void seq_of(const DecParams& p, uint32_t r, uint32_t lane, uint32_t nseg, uint32_t& b,
+                                       uint32_t& seg0)
 {
     if (!p.ctx) {
-        const uint32_t per = p.max_ctx * p.kv_heads * p.ncg;
+        const uint32_t per = p.max_ctx * nseg;
         b = per ? min(r / per, p.batch) : p.batch;
         seg0 = b * per;
         return;
@@ -99,7 +100,7 @@ __device__ __forceinline__ void seq_of(const DecParams& p, uint32_t r, uint32_t 
     uint32_t base = 0;
     for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
         const uint32_t i = i0 + lane;
-        const uint32_t len = i < p.batch ? min(p.ctx[i], p.max_ctx) * p.kv_heads * p.ncg : 0u;
+        const uint32_t len = i < p.batch ? min(p.ctx[i], p.max_ctx) * nseg : 0u;
         uint32_t inc = len;
         #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -118,6 +119,10 @@ __device__ __forceinline__ void seq_of(const DecParams& p, uint32_t r, uint32_t 
     b = p.batch;
     seg0 = base;
 }
+
+// A value the whole wave holds (the index arithmetic of seq_of goes through lane shuffles, so the compiler cannot
+// prove it uniform; buffer resources built from it would need a waterfall loop around every load).
+__device__ __forceinline__ uint32_t uniform(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane(x); }
 
 // The keys row r of a sequence with context ctx sees: [0, lim).
 __device__ __forceinline__ uint32_t lim_of(const DecParams& p, uint32_t ctx, uint32_t r)
@@ -154,13 +159,154 @@ __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 // XOR swizzle of the four 16-byte key chunks in row d of a transposed 32-key V tile.
 __device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return ((d >> 1) ^ (d >> 3)) & 3u; }
 
+// One wave's keys of a piece: the 32-key tiles at j_first, j_first + step, ... below k_end of one segment (K / V
+// through krs / vrs, rows at or past k_end loading as zeros), against its 32 columns' Q (the B operand, qreg). The
+// wave stages each tile in its own LDS slice (ks: K rows with bits 2 and 3 swapped, so the exponentiated scores are
+// already the B operand of O^T = V^T P^T; vt: V^T in f16, through registers), with the next tile's loads in flight
+// while the current one is used. Keys at or past min(k_end, lim) are masked (tiles below lim_all need no mask).
+// Leaves the unnormalised O^T (register r of block db: head dim 32 db + 8 (r / 4) + 4 g + r % 4 of column c32), the
+// running maximum m (base 2, scaled; the same in both halves; -inf when no key was seen) and this lane's share l of
+// the row sum.
 template <class T>
-__global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p)
+__device__ __forceinline__ void wave_keys(const DecParams& p, T* ks, _Float16* vt, typename Elem<T>::vec8* qreg,
+                                          __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs, uint32_t j_first,
+                                          uint32_t step, uint32_t k_end, uint32_t lim, uint32_t lim_all,
+                                          f32x16 (&oacc)[kD / 32], float& m, float& l)
 {
     using E = Elem<T>;
     using V8 = typename E::vec8;
     using H = Elem<_Float16>;
     using H8 = f16x8;
+    constexpr int KS = kD + 8;
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 5, c32 = lane & 31;
+    // Loads: K chunk i of this lane is row 4 i + lane / 16, head dims 8 (lane % 16) ..; V rows 8 kg + i, the same
+    // head dims.
+    // Streaming (non-temporal) loads, or plain ones when two column groups read each tile (the second read then
+    // hits the L2 line the first brought in).
+    const uint32_t cc = lane % 16, kg = lane / 16;
+    const bool shared = p.ncg > 1;
+    u32x4 kreg[8], vreg[8];
+    auto load16 = [&](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        return shared ? buffer_load16(r, off) : buffer_load16_nt(r, off);
+    };
+    auto load_tile = [&](uint32_t j0) {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+            kreg[i] = load16(krs, ((j0 + 4 * i + kg) * kD + cc * 8) * sizeof(T));
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+            vreg[i] = load16(vrs, ((j0 + 8 * kg + i) * kD + cc * 8) * sizeof(T));
+    };
+    auto store_tile = [&]() {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<u32x4*>(&ks[slot_of(4 * i + kg) * KS + cc * 8]) = kreg[i];
+        #pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t d = cc * 8 + e;
+            *reinterpret_cast<u32x4*>(&vt[d * kTK + ((kg ^ vt_swz(d)) * 8)]) =
+                u32x4{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e),
+                      f16_pair<T>(vreg[4], vreg[5], e), f16_pair<T>(vreg[6], vreg[7], e)};
+        }
+    };
+
+    #pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+        oacc[db] = f32x16{};
+    m = -INFINITY;
+    l = 0.0f;
+    if (j_first >= k_end)
+        return;
+    const float c = p.scale_log2;
+    load_tile(j_first);
+    // Q (loaded by load_q, before the first tile) arrives: waiting here for it does not wait for the tile
+    #pragma unroll
+    for (int kk = 0; kk < kD / 16; ++kk)
+        settle(qreg[kk]);
+    for (uint32_t j0 = j_first; j0 < k_end; j0 += step) {
+        store_tile();
+        if (j0 + step < k_end)
+            load_tile(j0 + step);
+        asm volatile("" ::: "memory");  // LDS writes before other lanes' reads (a wave's LDS ops run in order)
+        f32x16 s = f32x16{};
+        {
+            const T* kr = &ks[c32 * KS + 8 * g];
+            #pragma unroll
+            for (int kk = 0; kk < kD / 16; ++kk)
+                s = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s);
+        }
+        // Register r holds key j0 + 16 (r / 8) + 8 g + r % 8; keys past the piece or the column's row are masked.
+        if (j0 + kTK > min(k_end, lim_all)) {
+            const uint32_t end = min(k_end, lim);
+            #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t j = j0 + 16 * (r >> 3) + 8 * g + (r & 7);
+                s[r] = j < end ? s[r] : -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+        #pragma unroll
+        for (int r = 0; r < 16; ++r)
+            mx = fmaxf(mx, s[r]);
+        mx = fmaxf(mx, swap_halves(mx)) * c;
+        float f = 1.0f;
+        if (mx > m + kRescale) {
+            f = exp2_fast(m - mx);
+            m = mx;
+        }
+        l *= f;
+        if (__any(f != 1.0f))
+            #pragma unroll
+            for (int db = 0; db < kD / 32; ++db)
+                #pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[db][r] *= f;
+        const float mu = m == -INFINITY ? 0.0f : m;
+        H8 pb[2];
+        #pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            u32x4 pk;
+            #pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const float e0 = exp2_fast(fmaf(s[8 * a + 2 * jj], c, -mu));
+                const float e1 = exp2_fast(fmaf(s[8 * a + 2 * jj + 1], c, -mu));
+                l += e0 + e1;
+                pk[jj] = H::pack2(e0, e1);
+            }
+            pb[a] = __builtin_bit_cast(H8, pk);
+        }
+        #pragma unroll
+        for (int a = 0; a < 2; ++a)
+            #pragma unroll
+            for (int db = 0; db < kD / 32; ++db) {
+                const uint32_t d = 32 * db + c32;
+                const _Float16* vr = &vt[d * kTK + (((2 * a + g) ^ vt_swz(d)) * 8)];
+                oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[a], oacc[db]);
+            }
+        asm volatile("" ::: "memory");
+    }
+}
+
+// Q of a wave's 32 columns as the MFMA's B operand: lane (c32, g) holds head dims 16 kk + 8 g .. + 7 of column
+// c32 (zero when has_col is false). The loads stay in flight: wave_keys waits for them after issuing its first
+// tile's loads, so the two round trips overlap.
+template <class T>
+__device__ __forceinline__ void load_q(const DecParams& p, uint32_t b, uint32_t kvh, uint32_t col, bool has_col,
+                                       typename Elem<T>::vec8 (&qreg)[kD / 16])
+{
+    using V8 = typename Elem<T>::vec8;
+    const uint32_t g = (threadIdx.x & 63) >> 5;
+    const uint32_t r = col / p.group, hq = kvh * p.group + col % p.group;
+    const T* src = static_cast<const T*>(p.q) + (size_t)b * p.qs_b + (size_t)hq * p.qs_h + (size_t)r * p.qs_r + 8 * g;
+    #pragma unroll
+    for (int kk = 0; kk < kD / 16; ++kk)
+        qreg[kk] = has_col ? *reinterpret_cast<const V8*>(src + 16 * kk) : V8{};
+}
+
+template <class T>
+__global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p)
+{
+    using V8 = typename Elem<T>::vec8;
     constexpr int KS = kD + 8;
     __shared__ __attribute__((aligned(16))) T ks_all[kWaves][kTK * KS];
     __shared__ __attribute__((aligned(16))) _Float16 vt_all[kWaves][kD * kTK];
@@ -170,12 +316,10 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
     const uint32_t g = lane >> 5, c32 = lane & 31;
     const uint32_t wave = blockIdx.x * kWaves + wl;
     const uint32_t nc = p.nq * p.group, nseg = p.kv_heads * p.ncg;
-    T* ks = ks_all[wl];
-    _Float16* vt = vt_all[wl];
 
     // The rows laid end to end: segment (b, sh) = b * nseg + sh (kv head sh / ncg, column group sh % ncg) holds
     // ctx[b] rows.
-    const uint32_t total = ctx_sum(p, p.batch, lane) * nseg;
+    const uint32_t total = uniform(ctx_sum(p, p.batch, lane) * nseg);
     if (total == 0)
         return;
     const Ranges rg(total, p.n_waves);
@@ -184,12 +328,13 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
         return;
     // The segment holding r0 (seg0: the first row of sequence b's segments).
     uint32_t b, seg0;
-    seq_of(p, r0, lane, b, seg0);
-    uint32_t ctx = ctx_of(p.ctx, b, p.max_ctx);
+    seq_of(p, r0, lane, nseg, b, seg0);
+    b = uniform(b);
+    seg0 = uniform(seg0);
+    uint32_t ctx = uniform(ctx_of(p.ctx, b, p.max_ctx));
     uint32_t sh = (r0 - seg0) / ctx;
     uint32_t row = r0;
 
-    const uint32_t cc = lane % 16, kg = lane / 16;
     while (row < r1) {
         // One piece: segment (b, sh), keys [k_begin, k_end).
         const uint32_t s_start = seg0 + sh * ctx;
@@ -203,117 +348,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
         const bool has_col = c32 < p.ncs && col < nc;
         const uint32_t lim = has_col ? lim_of(p, ctx, col / p.group) : 0u;
         const uint32_t lim_all = lim_of(p, ctx, 0);
-
-        // Q: the B operand (zero past the segment's columns).
         V8 qreg[kD / 16];
-        {
-            const uint32_t r = col / p.group, hq = kvh * p.group + col % p.group;
-            const T* src = static_cast<const T*>(p.q) + (size_t)b * p.qs_b + (size_t)hq * p.qs_h +
-                           (size_t)r * p.qs_r + 8 * g;
-            #pragma unroll
-            for (int kk = 0; kk < kD / 16; ++kk)
-                qreg[kk] = has_col ? *reinterpret_cast<const V8*>(src + 16 * kk) : V8{};
-            #pragma unroll
-            for (int kk = 0; kk < kD / 16; ++kk)
-                settle(qreg[kk]);
-        }
+        load_q<T>(p, b, kvh, col, has_col, qreg);
         const size_t head_off = ((size_t)b * p.kv_heads + kvh) * p.cap * kD;
         const auto krs = buffer_rsrc(static_cast<const T*>(p.k) + head_off, k_end * kD * sizeof(T));
         const auto vrs = buffer_rsrc(static_cast<const T*>(p.v) + head_off, k_end * kD * sizeof(T));
-        // Loads: K chunk i of this lane is row 4 i + lane / 16, head dims 8 (lane % 16) ..; V rows 8 kg + i,
-        // the same head dims. Rows at or past k_end load as zeros.
-        u32x4 kreg[8], vreg[8];
-        auto load_tile = [&](uint32_t j0) {
-            #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                kreg[i] = buffer_load16_nt(krs, ((j0 + 4 * i + kg) * kD + cc * 8) * sizeof(T));
-            #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                vreg[i] = buffer_load16_nt(vrs, ((j0 + 8 * kg + i) * kD + cc * 8) * sizeof(T));
-        };
-        auto store_tile = [&]() {
-            #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                *reinterpret_cast<u32x4*>(&ks[slot_of(4 * i + kg) * KS + cc * 8]) = kreg[i];
-            #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t d = cc * 8 + e;
-                *reinterpret_cast<u32x4*>(&vt[d * kTK + ((kg ^ vt_swz(d)) * 8)]) =
-                    u32x4{f16_pair<T>(vreg[0], vreg[1], e), f16_pair<T>(vreg[2], vreg[3], e),
-                          f16_pair<T>(vreg[4], vreg[5], e), f16_pair<T>(vreg[6], vreg[7], e)};
-            }
-        };
-
         f32x16 oacc[kD / 32];
-        #pragma unroll
-        for (int db = 0; db < kD / 32; ++db)
-            oacc[db] = f32x16{};
-        float m = -INFINITY, l = 0.0f;
-        const float c = p.scale_log2;
-        load_tile(k_begin);
-        for (uint32_t j0 = k_begin; j0 < k_end; j0 += kTK) {
-            store_tile();
-            if (j0 + kTK < k_end)
-                load_tile(j0 + kTK);
-            asm volatile("" ::: "memory");  // LDS writes before other lanes' reads (a wave's LDS ops run in order)
-            f32x16 s = f32x16{};
-            {
-                const T* kr = &ks[c32 * KS + 8 * g];
-                #pragma unroll
-                for (int kk = 0; kk < kD / 16; ++kk)
-                    s = E::mfma32(*reinterpret_cast<const V8*>(kr + 16 * kk), qreg[kk], s);
-            }
-            // Register r holds key j0 + 16 (r / 8) + 8 g + r % 8; keys past the piece or the column's row are
-            // masked.
-            if (j0 + kTK > min(k_end, lim_all)) {
-                const uint32_t end = min(k_end, lim);
-                #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t j = j0 + 16 * (r >> 3) + 8 * g + (r & 7);
-                    s[r] = j < end ? s[r] : -INFINITY;
-                }
-            }
-            float mx = -INFINITY;
-            #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                mx = fmaxf(mx, s[r]);
-            mx = fmaxf(mx, swap_halves(mx)) * c;
-            float f = 1.0f;
-            if (mx > m + kRescale) {
-                f = exp2_fast(m - mx);
-                m = mx;
-            }
-            l *= f;
-            if (__any(f != 1.0f))
-                #pragma unroll
-                for (int db = 0; db < kD / 32; ++db)
-                    #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        oacc[db][r] *= f;
-            const float mu = m == -INFINITY ? 0.0f : m;
-            H8 pb[2];
-            #pragma unroll
-            for (int a = 0; a < 2; ++a) {
-                u32x4 pk;
-                #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const float e0 = exp2_fast(fmaf(s[8 * a + 2 * jj], c, -mu));
-                    const float e1 = exp2_fast(fmaf(s[8 * a + 2 * jj + 1], c, -mu));
-                    l += e0 + e1;
-                    pk[jj] = H::pack2(e0, e1);
-                }
-                pb[a] = __builtin_bit_cast(H8, pk);
-            }
-            #pragma unroll
-            for (int a = 0; a < 2; ++a)
-                #pragma unroll
-                for (int db = 0; db < kD / 32; ++db) {
-                    const uint32_t d = 32 * db + c32;
-                    const _Float16* vr = &vt[d * kTK + (((2 * a + g) ^ vt_swz(d)) * 8)];
-                    oacc[db] = H::mfma32(*reinterpret_cast<const H8*>(vr), pb[a], oacc[db]);
-                }
-            asm volatile("" ::: "memory");
-        }
+        float m, l;
+        wave_keys<T>(p, ks_all[wl], vt_all[wl], qreg, krs, vrs, k_begin, kTK, k_end, lim, lim_all, oacc, m, l);
         // The piece's partial at index wave + segment: unnormalised O^T column c32 of the segment (head dims
         // 32 db + 8 (r / 4) + 4 g + r % 4), maximum and sum.
         const float lt = l + swap_halves(l);
@@ -339,26 +381,147 @@ __global__ __launch_bounds__(kWaves * 64, 2) void decode_split(const DecParams p
             } while (b < p.batch && ctx_of(p.ctx, b, p.max_ctx) == 0);
             if (b >= p.batch)
                 break;
-            ctx = ctx_of(p.ctx, b, p.max_ctx);
+            ctx = uniform(ctx_of(p.ctx, b, p.max_ctx));
         }
     }
 }
 
-// One workgroup of 1024 threads per (head, sequence, row), as kMergeGroups groups of 32 lanes (a lane holds 4 head
+// A whole workgroup on each piece (mako_attn_fwd's few-row route):
+// * One workgroup of kCoopWaves waves a CU; the rows of all (sequence, kv head) segments, laid end to end, are cut
+//   into equal ranges, one a workgroup. Column groups do not make segments here: wave w takes column group
+//   w % ncg and every (kCoopWaves / ncg)-th 32-key tile of the piece (the waves of the two column groups read the
+//   same tiles at about the same time, so the second read is served by the L2).
+// * The waves of a column group combine their partials through LDS (rescaled to their common maximum), and the
+//   workgroup writes one partial a piece and column, at index workgroup + segment as in decode_split: a
+//   workgroup's 8 waves leave one partial where decode_split's would leave 8, so the merge (decode_merge, with one
+//   column group of nc columns) reads 8 times fewer.
+constexpr int kCoopWaves = 8;
+constexpr int kSliceBytes = kTK * (kD + 8) * 2 + kD * kTK * 2;  // a wave's K tile and V^T tile
+
+template <class T>
+__global__ __launch_bounds__(kCoopWaves * 64, 1) void decode_coop(const DecParams p)
+{
+    using V8 = typename Elem<T>::vec8;
+    constexpr uint32_t kThreads = kCoopWaves * 64;
+    __shared__ __attribute__((aligned(16))) unsigned char slices[kCoopWaves][kSliceBytes];
+    __shared__ float2 s_ml[kCoopWaves][32];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wl = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 5, c32 = lane & 31;
+    const uint32_t nc = p.nq * p.group, nseg = p.kv_heads;
+    const uint32_t cg = wl % p.ncg, kw = wl / p.ncg, n_kw = kCoopWaves / p.ncg;
+    T* ks = reinterpret_cast<T*>(slices[wl]);
+    _Float16* vt = reinterpret_cast<_Float16*>(slices[wl] + kTK * (kD + 8) * sizeof(T));
+
+    // The rows laid end to end: segment (b, kvh) = b * kv_heads + kvh holds ctx[b] rows.
+    const uint32_t total = uniform(ctx_sum(p, p.batch, lane) * nseg);
+    if (total == 0)
+        return;
+    const Ranges rg(total, gridDim.x);
+    const uint32_t r0 = rg.start(blockIdx.x), r1 = rg.start(blockIdx.x + 1);
+    if (r0 >= r1)
+        return;
+    uint32_t b, seg0;
+    seq_of(p, r0, lane, nseg, b, seg0);
+    b = uniform(b);
+    seg0 = uniform(seg0);
+    uint32_t ctx = uniform(ctx_of(p.ctx, b, p.max_ctx));
+    uint32_t kvh = (r0 - seg0) / ctx;
+    uint32_t row = r0;
+
+    while (row < r1) {
+        // One piece: segment (b, kvh), keys [k_begin, k_end).
+        const uint32_t s_start = seg0 + kvh * ctx;
+        const uint32_t k_begin = row - s_start;
+        const uint32_t k_end = min(ctx, r1 - s_start);
+        const uint32_t seg = b * nseg + kvh;
+        const uint32_t col = 32 * cg + c32;
+        const bool has_col = c32 < p.ncs && col < nc;
+        const uint32_t lim = has_col ? lim_of(p, ctx, col / p.group) : 0u;
+        const uint32_t lim_all = lim_of(p, ctx, 0);
+        V8 qreg[kD / 16];
+        load_q<T>(p, b, kvh, col, has_col, qreg);
+        const size_t head_off = ((size_t)b * p.kv_heads + kvh) * p.cap * kD;
+        const auto krs = buffer_rsrc(static_cast<const T*>(p.k) + head_off, k_end * kD * sizeof(T));
+        const auto vrs = buffer_rsrc(static_cast<const T*>(p.v) + head_off, k_end * kD * sizeof(T));
+        f32x16 oacc[kD / 32];
+        float m, l;
+        wave_keys<T>(p, ks, vt, qreg, krs, vrs, k_begin + kTK * kw, kTK * n_kw, k_end, lim, lim_all, oacc, m, l);
+
+        // This wave's share into its own slice: quad q (registers 4 (q % 4) .. + 3 of block q / 4: head dims
+        // 32 (q / 4) + 8 (q % 4) + 4 g .. + 3) of lane l at f32x4 q * 64 + l; maximum and row sum a column.
+        {
+            f32x4* red = reinterpret_cast<f32x4*>(slices[wl]);
+            #pragma unroll
+            for (int q = 0; q < 16; ++q)
+                red[q * 64 + lane] = f32x4{oacc[q / 4][4 * (q % 4)], oacc[q / 4][4 * (q % 4) + 1],
+                                           oacc[q / 4][4 * (q % 4) + 2], oacc[q / 4][4 * (q % 4) + 3]};
+            const float lt = l + swap_halves(l);
+            if (g == 0)
+                s_ml[wl][c32] = float2{m, lt};
+        }
+        __syncthreads();
+        // The piece's partial a column: items (column group, column, half, quad) over the workgroup.
+        {
+            const uint32_t per_cg = p.ncs * 32, items = per_cg * p.ncg;
+            for (uint32_t it = tid; it < items; it += kThreads) {
+                const uint32_t icg = it / per_cg, rest = it % per_cg;
+                const uint32_t c = rest / 32, h = (rest / 16) % 2, q = rest % 16, ccol = 32 * icg + c;
+                if (ccol >= nc)
+                    continue;
+                float mx = -INFINITY;
+                for (uint32_t j = 0; j < n_kw; ++j)
+                    mx = fmaxf(mx, s_ml[icg + p.ncg * j][c].x);
+                float sum = 0.0f;
+                f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                for (uint32_t j = 0; j < n_kw; ++j) {
+                    const uint32_t w = icg + p.ncg * j;
+                    const float2 ml = s_ml[w][c];
+                    const float f = ml.x == -INFINITY ? 0.0f : exp2_fast(ml.x - mx);
+                    sum += ml.y * f;
+                    acc += reinterpret_cast<const f32x4*>(slices[w])[q * 64 + 32 * h + c] * f;
+                }
+                const size_t prow = ((size_t)blockIdx.x + seg) * nc + ccol;
+                *reinterpret_cast<f32x4*>(p.part_o + prow * kD + 32 * (q / 4) + 8 * (q % 4) + 4 * h) = acc;
+                if (h == 0 && q == 0)
+                    *reinterpret_cast<float2*>(p.part_ml + prow * 2) = float2{mx, sum};
+            }
+        }
+        __syncthreads();  // the slices are free again
+        // The next segment (sequences with an empty context hold no rows and are skipped).
+        row = s_start + k_end;
+        if (++kvh == nseg) {
+            kvh = 0;
+            seg0 += ctx * nseg;
+            do {
+                ++b;
+            } while (b < p.batch && ctx_of(p.ctx, b, p.max_ctx) == 0);
+            if (b >= p.batch)
+                break;
+            ctx = uniform(ctx_of(p.ctx, b, p.max_ctx));
+        }
+    }
+}
+
+// One workgroup of 256 threads per (head, sequence, row), as kMergeGroups groups of 32 lanes (a lane holds 4 head
 // dims): group gi takes every kMergeGroups-th of the segment's pieces, one pass with a running maximum (all of its
-// pieces' loads in flight at once for up to 8 each), then the groups' (maximum, sum, output) meet in LDS and group 0
-// divides once; lse = (max + log2 sum) ln 2.
-constexpr int kMergeGroups = 32;
+// pieces' loads in flight at once for up to 8 each: one round trip for up to 64 pieces), then the groups' (maximum,
+// sum, output) meet in LDS and group 0 divides once; lse = (max + log2 sum) ln 2. Small workgroups so that every
+// (head, sequence, row) of a call is resident at once.
+constexpr int kMergeGroups = 8;
+constexpr int kMergeThreads = kMergeGroups * 32;
 
 template <class TO>
-__global__ __launch_bounds__(1024) void decode_merge(const DecParams p, TO* __restrict__ o, float* __restrict__ lse)
+__global__ __launch_bounds__(kMergeThreads) void decode_merge(const DecParams p, TO* __restrict__ o,
+                                                              float* __restrict__ lse)
 {
     __shared__ float s_ml[kMergeGroups][2];
     __shared__ f32x4 s_acc[kMergeGroups][kD / 4];
     const uint32_t h = blockIdx.x, b = blockIdx.y, rq = blockIdx.z, gi = threadIdx.x / 32, d4 = threadIdx.x % 32;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t kvh = h / p.group, col = rq * p.group + h % p.group, nseg = p.kv_heads * p.ncg;
-    const uint32_t sh = kvh * p.ncg + col / 32, cs = col % 32;  // the column's segment and place in it
+    const uint32_t sh = kvh * p.ncg + col / p.ncs, cs = col % p.ncs;  // the column's segment and place in it
     const uint32_t total = ctx_sum(p, p.batch, lane) * nseg;
     const uint32_t seq0 = ctx_sum(p, b, lane);
     const uint32_t ctx = ctx_of(p.ctx, b, p.max_ctx);
@@ -452,7 +615,7 @@ void launch_split_merge(const DecParams& p, mako_dtype out, void* o, float* lse,
 {
     const dim3 grid(p.n_waves / kWaves), mgrid(p.heads, p.batch, p.nq);
     hipLaunchKernelGGL((decode_split<T>), grid, dim3(kWaves * 64), 0, s, p);
-    const dim3 mblock(1024);
+    const dim3 mblock(kMergeThreads);
     if (out == MAKO_F32)
         hipLaunchKernelGGL(decode_merge<float>, mgrid, mblock, 0, s, p, static_cast<float*>(o), lse);
     else if (out == MAKO_BF16)
@@ -565,38 +728,58 @@ int launch_decode(const mako_decode_args* a, uint32_t n_waves, mako_dtype in, ma
 namespace mako {
 
 // mako_attn_fwd's route for a few query rows (heads of 128): when the columns (n_q rows x the GQA group) are at most
-// 64, the split kernel over each kv head's keys (those the last row sees; a segment per 32 columns), partials in the
-// stream's cached workspace, and the merge into o [n_q][width] and lse [heads][n_q]. A wave takes at least 256 keys.
-// Returns 1 when launched, 0 when the case does not take this route, -1 when the workspace could not be had.
+// 64, decode_coop over each kv head's keys (those the last row sees), one workgroup a CU taking at least
+// kCoopMinRows keys, partials in the stream's cached workspace, then decode_merge into o [n_q][width] and lse
+// [heads][n_q]. With no key to see, only the merge runs (it writes zeros and lse = -inf). Returns 1 when launched, 0
+// when the case does not take this route, -1 when the workspace could not be had.
 int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
                        const void* v, void* o, float* lse, hipStream_t s)
 {
+    constexpr uint32_t kCoopMinRows = kCoopWaves * 128;
     const uint32_t group = a->heads / a->kv_heads, nc = a->n_q * group;
     if (nc > 64 || a->n_q == 0 || (uint64_t)a->q_pos0 + a->n_q >= 0xffffffffull)
         return 0;
     const uint32_t last = a->q_pos0 + a->n_q - 1;  // the last row's position: it sees the most keys
     const uint32_t n_keys = last >= a->block ? a->n_k : std::min(a->n_k, last + 1);
     const uint32_t ncg = (nc + 31) / 32, ncs = std::min(nc, 32u);
-    const uint32_t resident = resident_waves();
-    if (!resident)
+    const uint32_t cus = device_cus();
+    if (!cus)
         return -1;
-    const uint64_t rows = (uint64_t)a->kv_heads * ncg * n_keys;
-    const uint64_t want = std::min<uint64_t>(std::max<uint64_t>((rows + 255) / 256, 1), resident);
-    const uint32_t n_waves = (uint32_t)((want + kWaves - 1) / kWaves * kWaves);
-    const size_t pieces = (size_t)n_waves + (size_t)a->kv_heads * ncg;
-    void* ws = stream_workspace(kWsSplitK, partials_bytes(pieces, ncs), s);
+    const uint64_t rows = (uint64_t)a->kv_heads * n_keys;
+    const uint32_t n_wg =
+        (uint32_t)std::min<uint64_t>(std::max<uint64_t>((rows + kCoopMinRows - 1) / kCoopMinRows, 1), cus);
+    // one sequence of n_keys keys a kv head: q [heads][q_pad][kD], o [n_q][width], lse [heads][n_q]
+    DecParams p{q, k, v, nullptr, nullptr, nullptr, 1u, a->heads, a->kv_heads, group, a->k_pad, n_keys,
+                n_wg, a->scale * kLog2e, a->n_q, ncg, ncs, a->q_pos0, a->block, a->n_k,
+                0u, a->q_pad * kD, kD, 0u, a->width, 0u, a->n_q, 1u};
+    const auto merge = [&](const DecParams& pm) {
+        const dim3 mgrid(pm.heads, pm.batch, pm.nq), mblock(kMergeThreads);
+        if (out == MAKO_F32)
+            hipLaunchKernelGGL(decode_merge<float>, mgrid, mblock, 0, s, pm, static_cast<float*>(o), lse);
+        else if (out == MAKO_BF16)
+            hipLaunchKernelGGL(decode_merge<__bf16>, mgrid, mblock, 0, s, pm, static_cast<__bf16*>(o), lse);
+        else
+            hipLaunchKernelGGL(decode_merge<_Float16>, mgrid, mblock, 0, s, pm, static_cast<_Float16*>(o), lse);
+    };
+    if (n_keys == 0) {
+        merge(p);  // no partials are read: the context is empty
+        return 1;
+    }
+    const size_t pieces = (size_t)n_wg + a->kv_heads;
+    void* ws = stream_workspace(kWsSplitK, partials_bytes(pieces, nc), s);
     if (!ws)
         return -1;
-    float* part_o = static_cast<float*>(ws);
-    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + part_o_bytes(pieces, ncs));
-    // one sequence of n_keys keys a kv head: q [heads][q_pad][kD], o [n_q][width], lse [heads][n_q]
-    const DecParams p{q, k, v, nullptr, part_o, part_ml, 1u, a->heads, a->kv_heads, group, a->k_pad, n_keys,
-                      n_waves, a->scale * kLog2e, a->n_q, ncg, ncs, a->q_pos0, a->block, a->n_k,
-                      0u, a->q_pad * kD, kD, 0u, a->width, 0u, a->n_q, 1u};
+    p.part_o = static_cast<float*>(ws);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + part_o_bytes(pieces, nc));
+    const dim3 grid(n_wg), block(kCoopWaves * 64);
     if (in == MAKO_BF16)
-        launch_split_merge<__bf16>(p, out, o, lse, s);
+        hipLaunchKernelGGL(decode_coop<__bf16>, grid, block, 0, s, p);
     else
-        launch_split_merge<_Float16>(p, out, o, lse, s);
+        hipLaunchKernelGGL(decode_coop<_Float16>, grid, block, 0, s, p);
+    DecParams pm = p;  // the pieces hold all nc columns: one column group for the merge's lookup
+    pm.ncg = 1;
+    pm.ncs = nc;
+    merge(pm);
     return 1;
 }
 

@@ -1,7 +1,11 @@
 """The decode split's work partition, restated in Python from csrc/attn_decode.hip (Ranges, decode_split's piece
 loop, decode_merge's lookup), checked for the properties the kernels rely on: every K/V row is in exactly one piece,
 piece ids (wave + segment) are unique and inside the partial buffer, and the merge finds exactly the pieces of each
-segment (empty sequences, empty waves when there are fewer rows than waves, the batch-16 shape)."""
+segment (empty sequences, empty waves when there are fewer rows than waves, the batch-16 shape): as many as the
+waves w_lo .. w_hi over it (the segment's rows when there are fewer rows than waves). decode_coop cuts the same way
+over workgroups (one range a workgroup, segments = kv heads), and its waves' tiles (column group w % ncg, every
+(8 / ncg)-th 32-key tile from the piece's start) must cover every key of a piece exactly once for each column
+group."""
 import random
 
 
@@ -41,6 +45,21 @@ def simulate(ctx, KV, n_waves, max_ctx):
                 if b >= B: break
                 c = ctx[b]
     assert all(x == 1 for x in cover), "rows not covered exactly once"
+    # pieces a segment gets: the waves over it (its rows when there are fewer rows than waves)
+    per_seg = {}
+    for (b, kvh, kb, ke) in written.values():
+        per_seg[(b, kvh)] = per_seg.get((b, kvh), 0) + 1
+    q = total // n_waves
+    seq0 = 0
+    for b in range(B):
+        for kvh in range(KV):
+            c = ctx[b]
+            if c == 0: continue
+            s_start = seq0 * KV + kvh * c
+            lo, hi = wave_of(s_start, total, n_waves), wave_of(s_start + c - 1, total, n_waves)
+            target = hi - lo + 1 if q > 0 else c
+            assert per_seg[(b, kvh)] == target, (b, kvh, per_seg[(b, kvh)], target)
+        seq0 += ctx[b]
     # merge lookup
     seq0 = 0
     for b in range(B):
@@ -72,3 +91,35 @@ def test_partition_properties():
         mc = max(ctx); want = max(1, -(-len(ctx) * KV * mc // split)); n = min(want, 2048); n = -(-n // 4) * 4
         simulate(ctx, KV, n, mc)
 
+
+
+def coop_tiles(kb, ke, ncg, waves=8):
+    """Keys each column group's waves visit in a piece [kb, ke): wave w (cg = w % ncg, kw = w // ncg) takes the
+    32-key tiles at kb + 32 (kw + j (waves // ncg)) below ke (decode_coop -> wave_keys)."""
+    n_kw = waves // ncg
+    seen = {cg: [] for cg in range(ncg)}
+    for w in range(waves):
+        cg, kw = w % ncg, w // ncg
+        j0 = kb + 32 * kw
+        while j0 < ke:
+            seen[cg] += [j for j in range(j0, j0 + 32) if j < ke]
+            j0 += 32 * n_kw
+    return seen
+
+
+def test_coop_partition_and_tiles():
+    random.seed(1)
+    # the few-row route: one sequence, kv heads x n_keys rows over ceil(rows / 1024) <= 256 workgroups
+    for kv, n_keys in [(8, 32768), (8, 3000), (2, 4100), (4, 5000), (4, 103), (8, 1), (2, 2047), (1, 1025)]:
+        rows = kv * n_keys
+        n_wg = min(max(-(-rows // 1024), 1), 256)
+        simulate([n_keys], kv, n_wg, n_keys)
+    # and batches of sequences (empty ones included), with fewer rows than workgroups
+    for _ in range(200):
+        ctx = [random.randint(0, 3000) for _ in range(random.randint(1, 6))]
+        simulate(ctx, random.choice([1, 2, 4, 8]), random.choice([1, 3, 64, 256]), max(max(ctx), 1))
+    for kb, ke in [(0, 1024), (0, 1000), (17, 1024), (1000, 1001), (5, 300), (0, 32), (0, 33)]:
+        for ncg in (1, 2):
+            seen = coop_tiles(kb, ke, ncg)
+            for cg in range(ncg):
+                assert sorted(seen[cg]) == list(range(kb, ke)), (kb, ke, ncg, cg)

@@ -1,6 +1,6 @@
 """attention() with a few query rows (mako_attn_fwd, heads of 128): n_q rows x the GQA group <= 64 columns take the
-split-K route (each kv head's keys cut over all CUs, partials merged by LSE) instead of the prefill kernels, which
-would leave the GPU nearly empty. Checked against the oracle on every row: the reference's decode shape
+split-K route (each kv head's keys cut over all CUs, a workgroup's waves combining their partials in LDS, the
+pieces merged by LSE in a second launch) instead of the prefill kernels, which would leave the GPU nearly empty. Checked against the oracle on every row: the reference's decode shape
 (attention(n_q, q_pos0 = ctx - n_q), ops.metal:289) at ctx 32768 with 32 query heads over 8 kv heads for n_q 1, 4
 and 16, and the edges of the route: two column blocks (MHA with 64 rows, GQA 8 with 8 rows), rows whose keys stop
 short of n_k, a prefix-causal block, n_k = 0, and a row count just past the route (prefill kernels)."""
@@ -77,3 +77,39 @@ def test_split_route_matches_prefill_kernel_rows():
     torch.cuda.synchronize()
     np.testing.assert_allclose(G.to_host(tail), G.to_host(full)[n - 4:], rtol=1e-2, atol=1e-3)
     np.testing.assert_allclose(lt.cpu().numpy(), lf.cpu().numpy()[:, n - 4:], rtol=0, atol=1e-4)
+
+
+def test_repeated_calls_same_bits():
+    """Calls in a row on one stream reuse its cached workspace: a repeat gives the same bits (the combine and merge
+    orders are fixed), also after a call over other kv heads, rows and keys in the same workspace, which matches the
+    oracle."""
+    rng = np.random.default_rng(2027)
+
+    def make(heads, kv, n_k, n_q):
+        qb = G.randn_bits(rng, (heads, n_q, 128), O.BF16)
+        kb = G.randn_bits(rng, (kv, n_k, 128), O.BF16)
+        vb = G.randn_bits(rng, (kv, n_k, 128), O.BF16)
+        args = dict(n_q=n_q, q_pad=n_q, n_k=n_k, k_pad=n_k, heads=heads, kv_heads=kv, q_pos0=n_k - n_q, block=U32,
+                    dim=128)
+        return (qb, kb, vb), tuple(G.to_dev(x, O.BF16) for x in (qb, kb, vb)), args
+
+    def call(dev, args):
+        o = torch.full((args["n_q"], args["heads"] * 128), float("nan"), dtype=torch.float32, device="cuda")
+        lse = torch.full((args["heads"], args["n_q"]), float("nan"), dtype=torch.float32, device="cuda")
+        M.attn_fwd(*dev, o, lse=lse, **args)
+        torch.cuda.synchronize()
+        return o.cpu().numpy(), lse.cpu().numpy()
+
+    _, dev_a, args_a = make(32, 8, 9000, 2)
+    host_b, dev_b, args_b = make(12, 4, 5000, 5)
+    first = call(dev_a, args_a)
+    assert np.isfinite(first[0]).all() and np.isfinite(first[1]).all()
+    for _ in range(2):
+        again = call(dev_a, args_a)
+        assert np.array_equal(again[0], first[0]) and np.array_equal(again[1], first[1])
+    got_o, got_l = call(dev_b, args_b)
+    want_o, want_l = O.attn_dense(*host_b, dtype=O.BF16, **args_b)
+    G.assert_attn_close(got_o, want_o, "output")
+    G.assert_lse_close(got_l.astype(np.float64), want_l, "lse")
+    again = call(dev_a, args_a)
+    assert np.array_equal(again[0], first[0]) and np.array_equal(again[1], first[1])
