@@ -81,6 +81,10 @@ def parse(lines):
         if rest.endswith(' lds'):
             mods['lds'] = True
             rest = rest[:-4]
+        for cm in (' nt', ' sc0', ' sc1'):   # cache policy: no effect on the values
+            if rest.endswith(cm):
+                mods[cm.strip()] = True
+                rest = rest[:-len(cm)]
         if 'offen' in rest:
             mods['offen'] = True
         m = re.search(r'offset:(\d+)', rest)
