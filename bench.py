@@ -388,7 +388,8 @@ def bench_other_dims(torch, M, steps, warmup, with_cpu, names=None):
                             kernel="flash_fwd_wide<bf16,bf16,256>",
                             workload="causal GQA, 16 query heads / 2 kv heads, D 256, S 4096, bf16 in/out, LSE "
                                      "(Qwen3.5 gated attention)"),
-        "d64_bidir": dict(H=16, KV=16, D=64, S=4096, block=0, seed=64, kernel="flash_fwd<bf16,bf16,64>",
+        "d64_bidir": dict(H=16, KV=16, D=64, S=4096, block=0, seed=64,
+                          kernel="vt_image<bf16,64> + flash_fwd_r64<bf16,bf16,64> (one call, both kernels)",
                           workload="bidirectional MHA, 16 heads, D 64, S 4096, bf16 in/out, LSE (H3 VAE ViT)"),
     }
     out = {}

@@ -625,7 +625,7 @@ int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, c
 
 // flash_fwd_r64 (attn_fwd64.hip): heads of 128 with 64 rows a wave; 1 launched, 0 when a size does not fit its
 // offsets, -1 when its workspace could not be allocated.
-template <class T, class TO>
+template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                   float* lse, hipStream_t s);
 
@@ -635,8 +635,9 @@ namespace {
 template <class T, class TO>
 bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
 {
-    if (dim == 128) {
-        const int r = launch_fwd64<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s);
+    if (dim == 128 || dim == 64) {
+        const int r = dim == 128 ? launch_fwd64<T, TO, 128>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
+                                 : launch_fwd64<T, TO, 64>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s);
         if (r)
             return r > 0;
     }

@@ -9,11 +9,21 @@
 namespace mako {
 namespace {
 
-constexpr uint32_t kKRow = 272;            // LDS bytes of a K row: 256 + 16 of padding
-constexpr uint32_t kKTile = 64 * kKRow;    // a K tile of 64 keys
-constexpr uint32_t kVTile = 128 * 64 * 2;  // a V^T tile: 128 head dims x 64 keys in f16
 constexpr uint32_t kNBuf = MAKO_FWD64_NBUF; // LDS tile buffers
-constexpr uint32_t kLdsBytes = kNBuf * (kKTile + kVTile);
+
+// The LDS tile geometry of the stream for heads of D (128 or 64; gen_attn_fwd64.set_dim).
+template <int D>
+struct R64 {
+    static constexpr uint32_t kKRow = 2 * D + 16;                    // LDS bytes of a K row: 2 D + 16 of padding
+    static constexpr uint32_t kKTile = 64 * kKRow;                   // a K tile of 64 keys (17 or 9 KiB)
+    static constexpr uint32_t kVTile = D * 64 * 2;                   // a V^T tile: D head dims x 64 keys in f16
+    static constexpr uint32_t kNKP = (kKTile / 1024 - 1) / 4;        // K image KiB pieces a wave DMAs: w + 4 m
+    static constexpr uint32_t kLdsBytes = kNBuf * (kKTile + kVTile);
+};
+constexpr uint32_t kKRow = R64<128>::kKRow;
+constexpr uint32_t kKTile = R64<128>::kKTile;
+constexpr uint32_t kVTile = R64<128>::kVTile;
+constexpr uint32_t kLdsBytes = R64<128>::kLdsBytes;
 
 __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 {
@@ -25,28 +35,29 @@ __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 // fragment read differ by an immediate offset).
 __device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d & 7u) ^ ((d >> 3) & 3u); }
 
-// The V^T tile images: tile t of kv head h is 16 KiB, row d (head dim) of 128 bytes holding keys 64 t .. 64 t + 63 in
-// f16, the 16-byte chunk of keys 64 t + 8 c .. + 7 at slot c ^ vt_swz(d): the LDS layout the kernel reads, so its
-// staging copies tiles unchanged. Keys >= n_k are zero. bf16 becomes f16 rounding toward zero (v_cvt_pkrtz), as the
-// staging of the other attention kernels does. 128 threads make a tile: thread (c, e) loads keys 8 c .. 8 c + 7,
-// head dims 8 e .. 8 e + 7 (eight 16-byte loads; 16 threads cover a 256-byte key row), transposes the 8 x 8 block
-// in registers and stores the eight 16-byte chunks of its head dims.
-// vt_image_tiles: the two tiles 2 bx, 2 bx + 1 of kv head kvh (a workgroup of 256 threads).
-template <class T>
+// The V^T tile images: tile t of kv head h is D x 128 bytes (16 or 8 KiB), row d (head dim) of 128 bytes holding keys
+// 64 t .. 64 t + 63 in f16, the 16-byte chunk of keys 64 t + 8 c .. + 7 at slot c ^ vt_swz(d): the LDS layout the
+// kernel reads, so its staging copies tiles unchanged. Keys >= n_k are zero. bf16 becomes f16 rounding toward zero
+// (v_cvt_pkrtz), as the staging of the other attention kernels does. D threads make a tile: thread (c, e) loads keys
+// 8 c .. 8 c + 7, head dims 8 e .. 8 e + 7 (eight 16-byte loads; D / 8 threads cover a key row), transposes the
+// 8 x 8 block in registers and stores the eight 16-byte chunks of its head dims.
+// vt_image_tiles: the 256 / D tiles (256 / D) bx .. of kv head kvh (a workgroup of 256 threads).
+template <class T, int D = 128>
 __device__ __forceinline__ void vt_image_tiles(const T* v, uint32_t* img, uint32_t n_k, uint32_t k_pad, uint32_t n_vt,
                                                uint32_t bx, uint32_t kvh)
 {
-    const uint32_t tile = bx * 2 + (threadIdx.x >> 7);
+    constexpr uint32_t CPR = D / 8;  // 16-byte chunks of a key row
+    const uint32_t tile = bx * (256 / D) + threadIdx.x / D;
     if (tile >= n_vt)
         return;
-    const uint32_t t = threadIdx.x & 127, e = t & 15, c = t >> 4;
-    const u32x4* src = reinterpret_cast<const u32x4*>(v + ((size_t)kvh * k_pad + (size_t)tile * 64 + 8 * c) * 128) + e;
+    const uint32_t t = threadIdx.x % D, e = t % CPR, c = t / CPR;
+    const u32x4* src = reinterpret_cast<const u32x4*>(v + ((size_t)kvh * k_pad + (size_t)tile * 64 + 8 * c) * D) + e;
     uint32_t x[8][4];  // x[i][m]: head dims 8 e + 2 m, + 1 of key 8 c + i (f16 pairs)
     #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
         u32x4 r = u32x4{0u, 0u, 0u, 0u};
         if (tile * 64 + 8 * c + i < n_k)
-            r = __builtin_nontemporal_load(src + 16 * i);
+            r = __builtin_nontemporal_load(src + CPR * i);
         #pragma unroll
         for (uint32_t m = 0; m < 4; ++m) {
             if constexpr (__is_same(T, __bf16)) {
@@ -58,7 +69,7 @@ __device__ __forceinline__ void vt_image_tiles(const T* v, uint32_t* img, uint32
             }
         }
     }
-    uint32_t* dst = img + ((size_t)kvh * n_vt + tile) * 4096;
+    uint32_t* dst = img + ((size_t)kvh * n_vt + tile) * (D * 32);
     #pragma unroll
     for (uint32_t j = 0; j < 8; ++j) {  // head dim d = 8 e + j: keys 8 c + 2 q, + 1 in dword q
         const uint32_t d = 8 * e + j, m = j >> 1, sh = 16 * (j & 1);
@@ -70,10 +81,10 @@ __device__ __forceinline__ void vt_image_tiles(const T* v, uint32_t* img, uint32
     }
 }
 
-template <class T>
+template <class T, int D = 128>
 __global__ __launch_bounds__(256) void vt_image(const T* v, uint32_t* img, uint32_t n_k, uint32_t k_pad, uint32_t n_vt)
 {
-    vt_image_tiles<T>(v, img, n_k, k_pad, n_vt, blockIdx.x, blockIdx.y);
+    vt_image_tiles<T, D>(v, img, n_k, k_pad, n_vt, blockIdx.x, blockIdx.y);
 }
 
 // A raw buffer descriptor (gfx9 layout) over `bytes` bytes at `base`: offsets at or past the end load zeros and drop

@@ -47,17 +47,37 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-K_ROW = 272             # LDS bytes of a K row (256 + 16 of padding: 16-byte reads down a column are conflict-free)
-K_TILE = 64 * K_ROW     # 17408: 17 pieces of 1 KiB
-V_TILE = 128 * 64 * 2   # 16384: V^T, 128 head dims x 64 keys in f16
 STAGING = os.environ.get("MAKO_FWD64_STAGING", "dma")   # "dma": LDS DMA, "reg": through the staging registers
 NBUF = 4 if STAGING == "dma" else 3   # LDS tile buffers
-DMA_PER_TILE = 9        # LDS DMA loads a wave issues a tile (5 K pieces, 4 V^T pieces)
 RING = 8                # LDS operand ring slots
 AHEAD = 6               # operand reads in flight ahead of their MFMAs (a slot is refilled two fragments after its
                         # last MFMA was issued)
-BAR_AT = 12             # phase PV's fragment after whose MFMAs the tile's barrier sits (its V^T reads landed by then)
 N_K_AHEAD = 6           # K reads of the next phase QK that go out in phase PV's tail, after the barrier
+
+
+def set_dim(d):
+    """The head width's constants (128, or 64: the same stream with half the head dimensions):
+    K_ROW   LDS bytes of a K row: 2 d + 16 of padding (an odd number of 16-byte chunks, so 16-byte reads down a column
+            are conflict-free);
+    K_TILE  the padded K image of a 64-key tile (17 or 9 pieces of 1 KiB: a wave DMAs pieces w + 4 m, m < NKP, and
+            every wave the last, piece 4 NKP);
+    V_TILE  the f16 V^T image of a tile, d rows of 64 keys (a wave DMAs NVP KiB of it);
+    NKK, NDB  16-wide head-dimension steps of Q K^T, 32-wide output blocks;
+    BAR_AT  phase PV's fragment (of 4 NDB) after whose MFMAs the tile's barrier sits."""
+    global D, K_ROW, K_TILE, V_TILE, NKK, NDB, NKP, NVP, DMA_PER_TILE, BAR_AT
+    assert d in (64, 128)
+    D = d
+    K_ROW = 2 * d + 16
+    K_TILE = 64 * K_ROW
+    V_TILE = d * 64 * 2
+    NKK, NDB = d // 16, d // 32
+    NKP = (K_TILE // 1024 - 1) // 4
+    NVP = V_TILE // 4096
+    DMA_PER_TILE = NKP + 1 + NVP   # LDS DMA loads a wave issues a tile (9 at d 128, 5 at 64)
+    BAR_AT = 12 if d == 128 else 6
+
+
+set_dim(128)
 
 # ---- registers ---------------------------------------------------------------------------------------------------
 
@@ -76,12 +96,12 @@ def P(rb, cc, i=None):
 
 def O(rb, db, r=None):
     """Output block: register r holds head dim 32 db + 8 (r / 4) + 4 g + r % 4 of query row c32."""
-    base = 64 * rb + 16 * db
+    base = 16 * NDB * rb + 16 * db
     return f"a{base + r}" if r is not None else f"a[{base}:{base + 15}]"
 
 
 def Q(rb, kk):
-    base = 128 + 32 * rb + 4 * kk
+    base = 128 + 4 * NKK * rb + 4 * kk
     return f"a[{base}:{base + 3}]"
 
 
@@ -224,15 +244,17 @@ def dma_issue():
                 f"s_add_u32 {KRS[0]}, %[kb0], {t}", f"s_addc_u32 {KRS[1]}, %[kb1], 0",
                 f"s_add_u32 {VRS[0]}, %[vb0], {t}", f"s_addc_u32 {VRS[1]}, %[vb1], 0",
                 f"s_cmp_eq_u32 {SD}, -1", f"s_cselect_b32 {KRS[2]}, 0, 0x4000", f"s_mov_b32 {VRS[2]}, {KRS[2]}"]
-    for m in range(4):
+    for m in range(NKP):
         ops += [f"s_add_u32 m0, {SKWW}, {4096 * m}" if m else f"s_mov_b32 m0, {SKWW}", "s_nop 0",
                 f"buffer_load_dwordx4 %[kd{m}], {quad(KRS)}, 0 offen lds"]
-    ops += [f"s_add_u32 m0, {SKW}, {16 * 1024}", "s_nop 0", f"buffer_load_dwordx4 %[kd4], {quad(KRS)}, 0 offen lds"]
+    ops += [f"s_add_u32 m0, {SKW}, {4 * NKP * 1024}", "s_nop 0",
+            f"buffer_load_dwordx4 %[kd4], {quad(KRS)}, 0 offen lds"]
     ops += [f"s_mov_b32 m0, {SVWW}", "s_nop 0"]
-    ops += [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds" for i in range(4)]
+    ops += [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds" for i in range(NVP)]
+    step = 128 * D   # K rows and V^T images: 2 d bytes a key, 64 keys a tile
     for r in (KRS, VRS) if not SPARSE else ():
-        ops += [f"s_add_u32 {r[0]}, {r[0]}, 0x4000", f"s_addc_u32 {r[1]}, {r[1]}, 0",
-                f"s_sub_u32 {r[2]}, {r[2]}, 0x4000", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
+        ops += [f"s_add_u32 {r[0]}, {r[0]}, {step:#x}", f"s_addc_u32 {r[1]}, {r[1]}, 0",
+                f"s_sub_u32 {r[2]}, {r[2]}, {step:#x}", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
     wk, wv = SROT["wk"], SROT["wv"]
     ops += [f"s_cmp_eq_u32 {SBW}, {NBUF - 1}",
             f"s_cselect_b32 {wk}, {(-NBUF * K_TILE) & 0xFFFFFFFF:#x}, 0",
@@ -261,13 +283,13 @@ def barrier():
 
 def k_reads(addr):
     """LDS reads of K fragment f = (kk, t) = (f // 2, f % 2): rows 32 t + c32 (slot order), head dims 16 kk + 8 g."""
-    return [f"ds_read_b128 {{ring}}, {addr} offset:{8704 * (f % 2) + 32 * (f // 2)}" for f in range(16)]
+    return [f"ds_read_b128 {{ring}}, {addr} offset:{32 * K_ROW * (f % 2) + 32 * (f // 2)}" for f in range(2 * NKK)]
 
 
 def qk_mfmas(dtype, sbuf):
     mf = f"v_mfma_f32_32x32x16_{dtype}"
     out = []
-    for f in range(16):
+    for f in range(2 * NKK):
         kk, t = f // 2, f % 2
         for rb in range(2):
             src_c = "0" if kk == 0 else S(sbuf, rb, t)
@@ -277,13 +299,13 @@ def qk_mfmas(dtype, sbuf):
 
 def v_reads():
     """LDS reads of V^T fragment f = (cc, db) = (f // 4, f % 4): head dims 32 db + c32, keys 16 cc + 8 g .. + 7."""
-    return [f"ds_read_b128 {{ring}}, %[vr{f // 4}] offset:{4096 * (f % 4)}" for f in range(16)]
+    return [f"ds_read_b128 {{ring}}, %[vr{f // NDB}] offset:{4096 * (f % NDB)}" for f in range(4 * NDB)]
 
 
 def pv_mfmas():
     out = []
-    for f in range(16):
-        cc, db = f // 4, f % 4
+    for f in range(4 * NDB):
+        cc, db = f // NDB, f % NDB
         for rb in range(2):
             out.append((f, f"v_mfma_f32_32x32x16_f16 {O(rb, db)}, {{ring}}, {P(rb, cc)}, {O(rb, db)}"))
     return out
@@ -485,8 +507,8 @@ def exact_tile(e, dtype, sbuf, kaddr, j0, first=False, w=None):
     # rescale the outputs (the MFMAs that wrote them were issued before the last barrier)
     for rb in range(2 if not first else 0):
         f = TMP[8 + rb]
-        for i in range(64):
-            a, tv = f"a{64 * rb + i}", TMP[10 + (i % 4)]
+        for i in range(16 * NDB):
+            a, tv = f"a{16 * NDB * rb + i}", TMP[10 + (i % 4)]
             e(f"v_accvgpr_read_b32 {tv}, {a}")
             e(f"v_mul_f32 {tv}, {tv}, {f}")
             e(f"v_accvgpr_write_b32 {a}, {tv}")
@@ -512,7 +534,7 @@ def epilogue(e, out_dtype):
     for op in wait_mfma():
         e(op)
     sz = {"f32": 4, "bf16": 2, "f16": 2}[out_dtype]
-    row = 128 * sz
+    row = D * sz
     inv = (TMP[1], TMP[2])
     for rb in range(2):
         lt = TMP[0]
@@ -537,7 +559,7 @@ def epilogue(e, out_dtype):
     # %[ew] ^ (16 x its chunk without the lane's part), %[ew] holding the row, the lane's part and the swizzle
     n = 0
     for rb in range(2):
-        for db in range(4):
+        for db in range(NDB):
             for r4 in range(4):
                 vals = [f"v{4 * n + i}" for i in range(4)]
                 addr = f"v{128 + n}"
@@ -600,14 +622,18 @@ def epilogue(e, out_dtype):
 
 # ---- the kernel body ----------------------------------------------------------------------------------------------
 
-def body(in_dtype, out_dtype, sparse=False):
-    """The stream for one item (a workgroup's rows); sparse: the block-sparse one (tiles from the pass table)."""
+def body(in_dtype, out_dtype, sparse=False, d=128):
+    """The stream for one item (a workgroup's rows) at head width d; sparse: the block-sparse one (tiles from the
+    pass table, heads of 128)."""
     global SPARSE
+    assert d == 128 or (not sparse and STAGING == "dma")
     SPARSE = sparse
+    set_dim(d)
     try:
         return body_of(in_dtype, out_dtype)
     finally:
         SPARSE = False
+        set_dim(128)
 
 
 def body_of(in_dtype, out_dtype):
@@ -637,9 +663,9 @@ def body_of(in_dtype, out_dtype):
         e(f"s_mov_b32 {r[3]}, 0x20000")
     e(f"s_mov_b32 {SBW}, 0")
     # Q into the accumulator registers (rows past n_q load as zeros)
-    e(f"v_add_u32 {TMP[0]}, 0x2000, %[qo]")
+    e(f"v_add_u32 {TMP[0]}, {64 * D:#x}, %[qo]")   # row block 1: 32 rows of 2 d bytes on
     for rb in range(2):
-        for kk in range(8):
+        for kk in range(NKK):
             e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen offset:{32 * kk}")
     if STAGING == "dma":
         # M0 is the compiler's: kept in SM0 while the stream uses it, restored at the end
@@ -657,7 +683,7 @@ def body_of(in_dtype, out_dtype):
                 e(op)
         if SPARSE:
             e(f"s_mov_b32 {SD}, s91")
-        for i in range(128):
+        for i in range(32 * NDB):
             e(f"v_accvgpr_write_b32 a{i}, 0")
     else:
         # tiles 0 and 1 into the (still free) score registers, tile 2 into the staging registers; outputs zeroed
@@ -875,12 +901,14 @@ def check_registers(lines, sparse=False):
 def main():
     out = ["// Generated by gen_attn_fwd64.py (the instruction stream of flash_fwd_r64; the design is described there).",
            "// Do not edit: change the generator and run it.", "#pragma once", ""]
-    for sparse in (False, True) if STAGING == "dma" else (False,):
+    kinds = [(False, 128), (True, 128), (False, 64)] if STAGING == "dma" else [(False, 128)]
+    for sparse, d in kinds:
         for ind in ("bf16", "f16"):
             for outd in ("f32", ind):
-                lines = body(ind, outd, sparse)
+                lines = body(ind, outd, sparse, d)
                 check_registers(lines, sparse)
-                name = f"MAKO_{'SPARSE64' if sparse else 'FWD64'}_ASM_{ind.upper()}_{outd.upper()}"
+                kind = "SPARSE64" if sparse else "FWD64" if d == 128 else "FWD64_D64"
+                name = f"MAKO_{kind}_ASM_{ind.upper()}_{outd.upper()}"
                 out.append(f"#define {name} \\")
                 for ln in lines:
                     out.append(f'    "{ln}\\n" \\')

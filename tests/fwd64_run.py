@@ -20,8 +20,8 @@ SOPS = {'qrs': 's[0:3]', 'ors': 's[12:15]', 'lrs': 's[16:19]', 'c': 's20',
 VREG = {n: f'v{G.CLOBBER_V + i}' for i, n in enumerate(VOPS)}
 
 
-def program(ind, outd):
-    lines = G.body(ind, outd)
+def program(ind, outd, d=128):
+    lines = G.body(ind, outd, d=d)
     out = []
     for ln in lines:
         ln = ln.replace('%=', '0')
@@ -45,18 +45,18 @@ def vt_swz(d):
     return (d & 7) ^ ((d >> 3) & 3)
 
 
-def vt_images(vb, kv, n_k, k_pad, ind):
-    """The f16 V^T tile images: [kv][tile][d 128][slot 8][8 keys], slot s of row d holding keys 8 (s ^ vt_swz(d))."""
+def vt_images(vb, kv, n_k, k_pad, ind, dim=128):
+    """The f16 V^T tile images: [kv][tile][d dim][slot 8][8 keys], slot s of row d holding keys 8 (s ^ vt_swz(d))."""
     nti = (n_k + 63) // 64
     if ind == 'bf16':
         f = vb.astype(np.uint32) << 16
         vals = f.view(np.float32)
-        h = E.f16_rtz(vals).view(np.uint16).reshape(kv, k_pad, 128)
+        h = E.f16_rtz(vals).view(np.uint16).reshape(kv, k_pad, dim)
     else:
-        h = vb.reshape(kv, k_pad, 128).astype(np.uint16)
-    img = np.zeros((kv, nti, 128, 8, 8), np.uint16)
+        h = vb.reshape(kv, k_pad, dim).astype(np.uint16)
+    img = np.zeros((kv, nti, dim, 8, 8), np.uint16)
     for t in range(nti):
-        for d in range(128):
+        for d in range(dim):
             for sl in range(8):
                 c = sl ^ vt_swz(d)
                 keys = t * 64 + 8 * c + np.arange(8)
@@ -65,22 +65,25 @@ def vt_images(vb, kv, n_k, k_pad, ind):
     return img, nti
 
 
-def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verbose=True, kgrow=0.0):
+def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verbose=True, kgrow=0.0, d=128):
     rng = np.random.default_rng(seed)
     dt = O.BF16 if ind == 'bf16' else O.F16
     q_pad = (S_q + 63) // 64 * 64
     k_pad = (S_k + 127) // 128 * 128
     conv = O.to_bf16_bits if ind == 'bf16' else O.to_f16_bits
-    qb = conv(rng.standard_normal((heads, q_pad, 128), dtype=np.float32))
-    kf = rng.standard_normal((kv, k_pad, 128), dtype=np.float32)
+    qb = conv(rng.standard_normal((heads, q_pad, d), dtype=np.float32))
+    kf = rng.standard_normal((kv, k_pad, d), dtype=np.float32)
     if kgrow:
         kf *= (1 + kgrow * (np.arange(k_pad) // 64))[None, :, None].astype(np.float32)
     kb = conv(kf)
-    vb = conv(rng.standard_normal((kv, k_pad, 128), dtype=np.float32))
-    width = heads * 128
+    vb = conv(rng.standard_normal((kv, k_pad, d), dtype=np.float32))
+    width = heads * d
+    # the head width's layout (gen_attn_fwd64.set_dim)
+    K_ROW, V_TILE = 2 * d + 16, 128 * d
+    K_TILE, NKP, row_b = 64 * K_ROW, (64 * K_ROW // 1024 - 1) // 4, 2 * d
     so = 4 if outd == 'f32' else 2
     # global memory
-    img, nti = vt_images(vb, kv, S_k, k_pad, ind)
+    img, nti = vt_images(vb, kv, S_k, k_pad, ind, d)
     sizes = [qb.nbytes, kb.nbytes, vb.nbytes, S_q * width * so + 4096, heads * S_q * 4 + 4096, img.nbytes + 4096]
     offs = np.cumsum([4096] + [((x + 4095) // 4096) * 4096 for x in sizes])
     Q0, K0, V0, O0, L0, I0 = [int(x) for x in offs[:6]]
@@ -92,17 +95,17 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
     fill = np.full(S_q * width, np.nan, np.float32) if so == 4 else None
     if so == 4:
         mem.b[O0:O0 + fill.nbytes] = fill.view(np.uint8)
-    prog, labels = program(ind, outd)
+    prog, labels = program(ind, outd, d)
     group = heads // kv
     hq = 4 if group % 4 == 0 else 2 if group % 2 == 0 else 1
     rows_wg = 256 // hq
     n_qblk = (S_q + rows_wg - 1) // rows_wg
     n_hg = heads // hq
-    c = np.float32(1.0 / np.sqrt(128.0)) * np.float32(1.4426950408889634)
+    c = np.float32(1.0 / np.sqrt(float(d))) * np.float32(1.4426950408889634)
     lane = np.arange(64)
     g, c32 = lane >> 5, lane & 31
     lbase = 0
-    vbase = lbase + G.NBUF * G.K_TILE
+    vbase = lbase + G.NBUF * K_TILE
     t0 = time.time()
     n_instr = 0
     worst = {}
@@ -115,7 +118,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
                 hg, qbk = x + 8 * (kx % per), n_qblk - 1 - kx // per
         else:
             hg, qbk = wid % n_hg, n_qblk - 1 - wid // n_hg
-        emu = E.Emu(prog, labels, mem, G.NBUF * (G.K_TILE + G.V_TILE))
+        emu = E.Emu(prog, labels, mem, G.NBUF * (K_TILE + V_TILE))
         waves = []
         for w in range(4):
             W = E.Wave(w)
@@ -134,18 +137,18 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
             lmin = lim_of(p0, S_k, block)
             lim0 = np.array([lim_of(p0 + cc, S_k, block) for cc in c32]) - 8 * g
             lim1 = np.array([lim_of(p0 + 32 + cc, S_k, block) for cc in c32]) - 8 * g
-            kr = lbase + c32 * G.K_ROW + 16 * g
+            kr = lbase + c32 * K_ROW + 16 * g
             sw = np.array([vt_swz(x) for x in c32])
             vr = [vbase + c32 * 128 + ((((2 * cc + g) ^ sw) & 7) << 4) for cc in range(4)]
 
             def kd_of(i):
                 b = 1024 * i + 16 * lane
-                R, c = b // G.K_ROW, (b % G.K_ROW) // 16
-                return np.array([slot_of(int(r)) for r in R]) * 256 + 16 * np.where(c < 16, c, 0)
-            kds = [kd_of(w + 4 * m) for m in range(4)] + [kd_of(16)]
-            vd = 4096 * w + 16 * lane
-            qo = ((q0 + c32) * 128 + 8 * g) * 2
-            orow = 128 * so
+                R, c = b // K_ROW, (b % K_ROW) // 16
+                return np.array([slot_of(int(r)) for r in R]) * row_b + 16 * np.where(c < d // 8, c, 0)
+            kds = [kd_of(w + 4 * m) for m in range(NKP)] + [0] * (4 - NKP) + [kd_of(4 * NKP)]
+            vd = (V_TILE // 4) * w + 16 * lane
+            qo = ((q0 + c32) * d + 8 * g) * 2
+            orow = d * so
             lpr = orow // 16
             obase = lbase + w * 64 * orow
             if so == 4:
@@ -173,12 +176,12 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
                 W.s[sidx + 1] = (base >> 32) & 0xFFFF
                 W.s[sidx + 2] = nbytes & 0xFFFFFFFF
                 W.s[sidx + 3] = 0x00020000
-            rs(0, Q0 + h * q_pad * 256, S_q * 256)
-            kbase = K0 + kvh * k_pad * 256
-            ibase = I0 + kvh * nti * 16384
-            W.s[26], W.s[27], W.s[28] = kbase & 0xFFFFFFFF, (kbase >> 32) & 0xFFFF, n_keys * 256
-            W.s[29], W.s[30], W.s[31] = ibase & 0xFFFFFFFF, (ibase >> 32) & 0xFFFF, nt * 16384
-            W.s[32], W.s[33], W.s[34] = lbase, lbase + 1024 * w, vbase + 4096 * w
+            rs(0, Q0 + h * q_pad * row_b, S_q * row_b)
+            kbase = K0 + kvh * k_pad * row_b
+            ibase = I0 + kvh * nti * V_TILE
+            W.s[26], W.s[27], W.s[28] = kbase & 0xFFFFFFFF, (kbase >> 32) & 0xFFFF, n_keys * row_b
+            W.s[29], W.s[30], W.s[31] = ibase & 0xFFFFFFFF, (ibase >> 32) & 0xFFFF, nt * V_TILE
+            W.s[32], W.s[33], W.s[34] = lbase, lbase + 1024 * w, vbase + (V_TILE // 4) * w
             rs(12, O0, S_q * width * so)
             rs(16, L0, heads * S_q * 4)
             W.s[20] = int(np.float32(c).view(np.uint32))
@@ -197,7 +200,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
         o = O.bits_to_f32(bitsv, dt).reshape(S_q, width).astype(np.float64)
     lse = mem.b[L0:L0 + heads * S_q * 4].view(np.float32).reshape(heads, S_q).astype(np.float64)
     want_o, want_l = O.attn_dense(qb, kb, vb, n_q=S_q, q_pad=q_pad, n_k=S_k, k_pad=k_pad, heads=heads, kv_heads=kv,
-                                  q_pos0=q_pos0, block=block, dim=128, dtype=dt)
+                                  q_pos0=q_pos0, block=block, dim=d, dtype=dt)
     err = np.abs(o - want_o)
     bad = ~(err <= 2e-3 + 1e-2 * np.abs(want_o))
     lerr = np.abs(lse - want_l)

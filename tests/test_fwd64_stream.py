@@ -1,5 +1,6 @@
-"""CPU checks of flash_fwd_r64's generated instruction stream (mako-common_amd/csrc/gen_attn_fwd64.py): every
-register it names is one its clobber list reserves; no gfx950 software hazard in any of its four type variants; and,
+"""CPU checks of flash_fwd_r64's generated instruction stream (mako-common_amd/csrc/gen_attn_fwd64.py), for heads of
+128 and of 64: every register it names is one its clobber list reserves; no gfx950 software hazard in any of its
+type variants; and,
 on an instruction-level emulator (tests/fwd64_emu.py), outputs and LSE within the attention tolerance of the oracle
 with conflict-free LDS access: causal GQA with a query offset and ragged sizes, bidirectional over eleven tiles,
 prefix-causal, f16 in and out, and inputs whose growing scores send most tiles down the exact path. Two planted
@@ -49,6 +50,33 @@ def test_stream_matches_oracle(case):
     assert r["out_bad"] == 0 and r["lse_bad"] == 0, r
     # the epilogue's 8-byte writes (2-byte outputs) meet 2-way: sixteen lanes of one write cover rows with eight
     # distinct chunk slots; every other LDS access is conflict-free
+    assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
+    if case.get("kgrow"):
+        assert E.EXACT_COUNT[0] > taken  # the exact path ran
+
+
+@pytest.mark.parametrize("ind,outd", VARIANTS)
+def test_d64_registers_and_hazards(ind, outd):
+    lines = G.body(ind, outd, d=64)
+    G.check_registers(lines)
+    assert Hz.check(lines, f"d64 {ind}->{outd}") == 0
+
+
+# heads of 64: the same stream with half the head dimensions (9 KiB K images, 8 KiB V^T images, 32 MFMAs a tile)
+CASES_D64 = [
+    dict(heads=4, kv=1, S_q=64, S_k=300, q_pos0=0, block=0, seed=2),
+    dict(heads=8, kv=2, S_q=100, S_k=330, q_pos0=230, block=U32, seed=1),
+    dict(heads=4, kv=4, S_q=70, S_k=300, q_pos0=200, block=U32, ind="f16", outd="f16", seed=3),
+    dict(heads=2, kv=1, S_q=130, S_k=300, q_pos0=150, block=250, ind="bf16", outd="bf16", seed=5),
+    dict(heads=4, kv=1, S_q=64, S_k=448, q_pos0=0, block=0, seed=7, kgrow=1.5),
+]
+
+
+@pytest.mark.parametrize("case", CASES_D64, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_d64_stream_matches_oracle(case):
+    taken = E.EXACT_COUNT[0]
+    r = R.run(**case, d=64, verbose=False)
+    assert r["out_bad"] == 0 and r["lse_bad"] == 0, r
     assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
     if case.get("kgrow"):
         assert E.EXACT_COUNT[0] > taken  # the exact path ran

@@ -68,6 +68,10 @@ SWEEP = [
     (2, 1, 128, 150, 150, 0, 77, O.F16, "same"),        # prefix-causal, block inside a tile
     (16, 2, 64, 130, 130, 0, U32, O.F16, "f32"),        # D 64, group 8
     (4, 4, 64, 70, 333, 0, 0, O.BF16, "same"),          # D 64, more keys than queries
+    (8, 8, 64, 300, 300, 0, 0, O.BF16, "same"),         # D 64, bidirectional MHA over five tiles (the H3 VAE's kind)
+    (4, 2, 64, 100, 300, 200, U32, O.F16, "f32"),       # D 64, chunked prefill
+    (2, 1, 64, 150, 150, 0, 77, O.BF16, "f32"),         # D 64, prefix-causal, block inside a tile
+    (6, 2, 64, 96, 96, 0, U32, O.F16, "same"),          # D 64, group 3 (hq 1)
     (2, 2, 256, 80, 80, 0, U32, O.BF16, "f32"),         # D 256
     (4, 1, 256, 65, 129, 64, U32, O.F16, "same"),       # D 256, group 4, offset
     (2, 2, 128, 1, 1000, 999, U32, O.BF16, "f32"),      # one query (decode through attention())
@@ -123,6 +127,13 @@ def test_bidirectional_s16384_bf16_sampled():
     """24 heads MHA, D 128, S 16384, bidirectional, bf16 in and out: sampled rows against the oracle."""
     print("bidirectional S16384 bf16", flush=True)
     _sampled(24, 24, 128, 16384, 0, O.BF16, 60, 16384)
+
+
+def test_h3_vae_d64_bidirectional_s4096_bf16_sampled():
+    """16 heads MHA, D 64, S 4096, bidirectional, bf16 in and out (the H3 VAE's attention shape, flash_fwd_r64 at
+    heads of 64): sampled rows against the oracle."""
+    print("bidirectional D64 S4096 bf16", flush=True)
+    _sampled(16, 16, 64, 4096, 0, O.BF16, 200, 64)
 
 
 def test_deterministic_and_row_independent():
