@@ -628,6 +628,9 @@ int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, c
 template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                   float* lse, hipStream_t s);
+template <class T, class TO>
+int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+                    float* lse, hipStream_t s);
 
 namespace {
 
@@ -635,9 +638,10 @@ namespace {
 template <class T, class TO>
 bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
 {
-    if (dim == 128 || dim == 64) {
+    {
         const int r = dim == 128 ? launch_fwd64<T, TO, 128>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
-                                 : launch_fwd64<T, TO, 64>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s);
+                      : dim == 64 ? launch_fwd64<T, TO, 64>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
+                                  : launch_fwd_d256<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s);
         if (r)
             return r > 0;
     }

@@ -74,6 +74,9 @@ SWEEP = [
     (6, 2, 64, 96, 96, 0, U32, O.F16, "same"),          # D 64, group 3 (hq 1)
     (2, 2, 256, 80, 80, 0, U32, O.BF16, "f32"),         # D 256
     (4, 1, 256, 65, 129, 64, U32, O.F16, "same"),       # D 256, group 4, offset
+    (4, 4, 256, 200, 200, 0, 0, O.BF16, "f32"),         # D 256, bidirectional MHA, ragged (hq 1)
+    (16, 2, 256, 130, 300, 170, U32, O.BF16, "same"),   # D 256, group 8, chunked prefill
+    (6, 2, 256, 96, 96, 0, 50, O.F16, "f32"),           # D 256, group 3, prefix-causal inside a tile
     (2, 2, 128, 1, 1000, 999, U32, O.BF16, "f32"),      # one query (decode through attention())
     (2, 1, 128, 40, 5, 0, U32, O.F16, "f32"),           # fewer keys than queries: later rows see n_k keys
 ]
@@ -134,6 +137,13 @@ def test_h3_vae_d64_bidirectional_s4096_bf16_sampled():
     heads of 64): sampled rows against the oracle."""
     print("bidirectional D64 S4096 bf16", flush=True)
     _sampled(16, 16, 64, 4096, 0, O.BF16, 200, 64)
+
+
+def test_qwen35_d256_causal_s4096_bf16_sampled():
+    """16 query heads over 2 kv heads, D 256, S 4096, causal, bf16 in and out (Qwen3.5 gated attention,
+    flash_fwd_d256): sampled rows against the oracle."""
+    print("causal D256 S4096 bf16", flush=True)
+    _sampled(16, 2, 256, 4096, U32, O.BF16, 120, 256)
 
 
 def test_deterministic_and_row_independent():
