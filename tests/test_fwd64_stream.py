@@ -69,6 +69,8 @@ CASES_D64 = [
     dict(heads=4, kv=4, S_q=70, S_k=300, q_pos0=200, block=U32, ind="f16", outd="f16", seed=3),
     dict(heads=2, kv=1, S_q=130, S_k=300, q_pos0=150, block=250, ind="bf16", outd="bf16", seed=5),
     dict(heads=4, kv=1, S_q=64, S_k=448, q_pos0=0, block=0, seed=7, kgrow=1.5),
+    dict(heads=2, kv=1, S_q=3, S_k=0, q_pos0=0, block=U32, seed=8),       # no keys: 0 and lse = -inf
+    dict(heads=8, kv=2, S_q=40, S_k=5, q_pos0=0, block=U32, seed=9),      # fewer keys than queries
 ]
 
 

@@ -77,6 +77,11 @@ SWEEP = [
     (4, 4, 256, 200, 200, 0, 0, O.BF16, "f32"),         # D 256, bidirectional MHA, ragged (hq 1)
     (16, 2, 256, 130, 300, 170, U32, O.BF16, "same"),   # D 256, group 8, chunked prefill
     (6, 2, 256, 96, 96, 0, 50, O.F16, "f32"),           # D 256, group 3, prefix-causal inside a tile
+    (4, 2, 256, 40, 5, 0, U32, O.BF16, "f32"),          # D 256, fewer keys than queries
+    (2, 1, 256, 3, 0, 0, U32, O.F16, "f32"),            # D 256, no keys: 0 and lse = -inf
+    (2, 1, 64, 3, 0, 0, U32, O.BF16, "f32"),            # D 64, no keys
+    (2, 1, 128, 100, 0, 0, U32, O.F16, "same"),         # no keys, rows enough for the prefill kernels
+    (8, 2, 64, 1, 777, 776, U32, O.F16, "f32"),         # D 64, one query row
     (2, 2, 128, 1, 1000, 999, U32, O.BF16, "f32"),      # one query (decode through attention())
     (2, 1, 128, 40, 5, 0, U32, O.F16, "f32"),           # fewer keys than queries: later rows see n_k keys
 ]
@@ -87,7 +92,7 @@ SWEEP = [
 def test_sweep(case):
     heads, kv, dim, n_q, n_k, q_pos0, block, dt, out = case
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))  # the same inputs in every process
-    q_pad, k_pad = (n_q + 63) // 64 * 64, (n_k + 127) // 128 * 128
+    q_pad, k_pad = (n_q + 63) // 64 * 64, max(128, (n_k + 127) // 128 * 128)  # a buffer even for n_k = 0
     qb = G.randn_bits(rng, (heads, q_pad, dim), dt)
     kb = G.randn_bits(rng, (kv, k_pad, dim), dt)
     vb = G.randn_bits(rng, (kv, k_pad, dim), dt)
