@@ -18,7 +18,7 @@ configuration, scaled to the metric's unit by the sample's share of the algorith
 the parity check of the GPU output against the oracle.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
-                  [--only prefill,s512,decode,bidir,sparse,heads,gather,proj,scan,copy]
+                  [--only prefill,s512,decode,bidir,sparse,heads,step,gather,proj,scan,copy]
 """
 import argparse
 import json
@@ -521,6 +521,60 @@ def bench_heads(torch, M, steps, warmup):
     return {"ms": ms, "kernel_ms": kms, "gbps": gbps, "bytes": nbytes, "frac": gbps / PEAK_GBPS}
 
 
+def bench_step(torch, M, steps, warmup):
+    """The attention of a Qwen3-8B prefill step from the projections' fp32 rows (src/models/qwen_text.cpp:308-311,
+    the q / k norms folded into the producers): 4096 tokens, q 32 heads and k 8 heads of 128 RMS-normed and rotated,
+    v 8 heads, causal GQA attention into bf16 rows with the LSE. Timed two ways on the same inputs: one call of
+    mako_attn_fwd_rows (qkv_prep, flash_fwd_r64), and the separate calls (mako_heads three times, then
+    mako_attn_fwd: heads_vec x 3, vt_image, flash_fwd_r64); both give the same bits (checked here, untimed)."""
+    T, D, H, KV = 4096, 128, 32, 8
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    xq = torch.randn((T, H * D), generator=gen, device="cuda")
+    xk = torch.randn((T, KV * D), generator=gen, device="cuda")
+    xv = torch.randn((T, KV * D), generator=gen, device="cuda")
+    ang = torch.rand((T, D // 2), generator=gen, device="cuda") * 6.283
+    cs = torch.stack([ang.cos(), ang.sin()], -1).contiguous()
+    wq, wk = (torch.rand(D, generator=gen, device="cuda") + 0.5 for _ in range(2))
+    yq = torch.empty((H, T, D), dtype=torch.bfloat16, device="cuda")
+    yk, yv = (torch.empty((KV, T, D), dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    o = torch.empty((T, H * D), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((H, T), dtype=torch.float32, device="cuda")
+    hq = dict(rows=T, ld=H * D, col0=0, stride=D, dim=D, heads=H, rope=1, rot=D, eps=1e-6)
+    hk = dict(hq, ld=KV * D, heads=KV)
+    hv = dict(rows=T, ld=KV * D, col0=0, stride=D, dim=D, heads=KV)
+    attn = dict(n_q=T, n_k=T, heads=H, kv_heads=KV, q_pos0=0, block=U32_MAX)
+
+    def fused():
+        M.attn_fwd_rows(xq, xk, xv, o, hq, hk, hv, in_dtype=M.BF16, cs=cs, wq=wq, wk=wk, lse=lse, **attn)
+
+    def separate():
+        M.heads(xq, yq, n_pad=T, cs=cs, w=wq, **hq)
+        M.heads(xk, yk, n_pad=T, cs=cs, w=wk, **hk)
+        M.heads(xv, yv, n_pad=T, **hv)
+        M.attn_fwd(yq, yk, yv, o, lse=lse, q_pad=T, k_pad=T, dim=D, **attn)
+
+    fused()
+    torch.cuda.synchronize()
+    got = (o.view(torch.int16).clone(), lse.clone())
+    separate()
+    torch.cuda.synchronize()
+    same = bool(torch.equal(got[0], o.view(torch.int16)) and torch.equal(got[1].view(torch.int32),
+                                                                         lse.view(torch.int32)))
+    ms_f, kms_f = time_launches(torch, fused, steps, warmup)
+    ms_s, kms_s = time_launches(torch, separate, steps, warmup)
+    flop = 4.0 * D * (T * (T + 1) / 2) * H
+    prep_bytes = 48.0 * T * D * 4 + T * D // 2 * 8 + (H + 2 * KV) * T * D * 2.0
+    return {"value": round(kms_f * 1e3, 1), "unit": "us a step", "higher_is_better": False,
+            "ms_per_step": round(ms_f, 4), "kernel_ms": round(kms_f, 4),
+            "separate_calls": {"ms_per_step": round(ms_s, 4), "kernel_ms": round(kms_s, 4)},
+            "speedup_vs_separate": round(kms_s / kms_f, 3), "same_bits_as_separate": same,
+            "attention_tflops_over_step": round(flop / (kms_f * 1e-3) / 1e12, 1),
+            "qkv_prep_bytes": prep_bytes,
+            "config": {"workload": "Qwen3-8B prefill attention step from fp32 projection rows: 4096 tokens, q 32 and "
+                                   "k 8 heads of 128 RMS-normed and rotated (rope over the whole head), v 8 heads, "
+                                   "causal GQA, bf16 tiles and output, LSE"}}
+
+
 def bench_gather(torch, M, steps, warmup):
     """The split-K and gathered latent-cache helpers (src/kernels/gemm.metal:683-870) at a sparse latent decode
     shape: a 65536-row cache of 512-wide f16 latent rows; 64 consecutive query tokens of 64 heads, each over its own
@@ -637,7 +691,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline and parity legs")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs to run alone (no CPU legs unless --cpu): prefill, s512, decode, "
-                         "few_rows, bidir, dims, sparse, heads, gather, proj, scan, copy; few_rows:N runs the n_q = N "
+                         "few_rows, bidir, dims, sparse, heads, step, gather, proj, scan, copy; few_rows:N runs the n_q = N "
                          "case alone, dims:NAME one head width (d256_causal, d64_bidir)")
     ap.add_argument("--cpu", action="store_true", help="with --only: run the legs' CPU-baseline and parity parts")
     args = ap.parse_args()
@@ -670,6 +724,7 @@ def main():
               "dims": lambda: bench_other_dims(torch, M, args.steps, args.warmup, c, sub.get("dims")),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup, c),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
+              "step": lambda: bench_step(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
               "proj": lambda: bench_proj(torch, M, args.steps, args.warmup),
               "scan": lambda: bench_scan(torch, M, args.steps, args.warmup),
@@ -688,6 +743,7 @@ def main():
     dims = bench_other_dims(torch, M, max(1, args.steps // 2), args.warmup, with_cpu)
     spa = bench_sparse(torch, M, args.steps, args.warmup, with_cpu)
     hds = bench_heads(torch, M, args.steps, args.warmup)
+    stp = bench_step(torch, M, args.steps, args.warmup)
     gat = bench_gather(torch, M, args.steps, args.warmup)
     prj = bench_proj(torch, M, max(1, args.steps // 2), args.warmup)
     scn = bench_scan(torch, M, max(1, args.steps // 4), max(1, args.warmup))
@@ -728,6 +784,7 @@ def main():
                        "config": {"workload": "Qwen3-8B prefill head tiles: 4096 tokens, q 32 and k 8 heads of 128 "
                                               "RMS-normed and rotated, v 8 heads sliced, fp32 rows to bf16 tiles",
                                   "bytes": hds["bytes"]}},
+        "prefill_step_from_rows": stp,
         "latent_decode": {name: {"kernel_ms": v["kernel_ms"], "gbps": v["gbps"], "tflops": v["tflops"],
                                  "bound": v["bound"], "frac": v["frac"]} for name, v in gat.items()},
     }

@@ -193,6 +193,27 @@ int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const f
                const int32_t* map, void* y, void* stream);
 
 /*
+ * Attention straight from fp32 projection rows. No counterpart in the reference, whose prefill steps produce the
+ * head tiles and then attend (TransformerRuntime::heads / heads_norm / heads_partial, then attention:
+ * src/models/qwen_text.cpp:308-311 and 414-418, src/models/h3_vae.cpp:219); it is for callers that keep those
+ * tiles only for the attention call. The result is that of
+ *   mako_heads(hq, in, xq, cs, wq, NULL, qt); mako_heads(hk, in, xk, cs, wk, NULL, kt);
+ *   mako_heads(hv, in, xv, cs, NULL, NULL, vt); mako_attn_fwd(a, hq->dim, in, out, qt, kt, vt, o, lse)
+ * bit for bit, with the tiles [heads][rows][dim] in the stream's workspace: each of hq / hk / hv is read as
+ * mako_heads reads it except n_pad, row0 and clear (the tiles hold exactly `rows` rows); a is read as
+ * mako_attn_fwd reads it except q_pad and k_pad. hq->rows must be a->n_q, hk->rows and hv->rows a->n_k, hq->heads
+ * a->heads, hk->heads and hv->heads a->kv_heads, and the three dims equal (64, 128 or 256).
+ * Heads of 64, 128 or 256 with 16-byte aligned rows (mako_heads' vector path), values neither normed nor rotated,
+ * and more rows than the split-K route takes run as two launches: one that writes the query and key tiles and the
+ * f16 V^T images the prefill kernels stage from (the value tiles are never written), then the prefill kernel.
+ * Other calls run the four launches above. Allocates as mako_attn_fwd does (a workspace per device and stream).
+ */
+int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
+                       const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq, const float* xk,
+                       const float* xv, const float* cs, const float* wq, const float* wk, void* o, float* lse,
+                       void* stream);
+
+/*
  * Split-K and gathered latent-cache primitives of the sparse latent decode (src/kernels/gemm.metal:683-870; no call
  * site in the reference's own engines: they serve a caller that computes the softmax between them). f16 latent rows
  * kv [*][dim], f32 accumulate, f32 outputs.

@@ -731,13 +731,19 @@ namespace mako {
 // 64, decode_coop over each kv head's keys (those the last row sees), one workgroup a CU taking at least
 // kCoopMinRows keys, partials in the stream's cached workspace, then decode_merge into o [n_q][width] and lse
 // [heads][n_q]. With no key to see, only the merge runs (it writes zeros and lse = -inf). Returns 1 when launched, 0
-// when the case does not take this route, -1 when the workspace could not be had.
+// when the case does not take this route (splitk_takes false), -1 when the workspace could not be had.
+bool splitk_takes(const mako_attn_args* a, uint32_t dim)
+{
+    return dim == 128 && a->n_q > 0 && (uint64_t)a->n_q * (a->heads / a->kv_heads) <= 64 &&
+           (uint64_t)a->q_pos0 + a->n_q < 0xffffffffull;
+}
+
 int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
                        const void* v, void* o, float* lse, hipStream_t s)
 {
     constexpr uint32_t kCoopMinRows = kCoopWaves * 128;
     const uint32_t group = a->heads / a->kv_heads, nc = a->n_q * group;
-    if (nc > 64 || a->n_q == 0 || (uint64_t)a->q_pos0 + a->n_q >= 0xffffffffull)
+    if (!splitk_takes(a, 128))
         return 0;
     const uint32_t last = a->q_pos0 + a->n_q - 1;  // the last row's position: it sees the most keys
     const uint32_t n_keys = last >= a->block ? a->n_k : std::min(a->n_k, last + 1);

@@ -627,10 +627,10 @@ int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, c
 // offsets, -1 when its workspace could not be allocated.
 template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                  float* lse, hipStream_t s);
+                 float* lse, hipStream_t s, const void* vt_ready = nullptr);
 template <class T, class TO>
 int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                    float* lse, hipStream_t s);
+                    float* lse, hipStream_t s, const void* vt_ready = nullptr);
 
 namespace {
 
@@ -666,8 +666,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using namespace mako;
 
-extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
-                             const void* k, const void* v, void* o, float* lse, void* stream)
+namespace mako {
+
+int attn_check(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q, const void* k,
+               const void* v, const void* o)
 {
     if (!a || !q || !k || !v || !o)
         return fail(MAKO_EINVAL, "attention: a null argument");
@@ -692,6 +694,20 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
                     dim);
     if (!(a->scale > 0.0f) || a->scale == INFINITY)
         return fail(MAKO_EINVAL, "attention: scale %g (positive and finite)", (double)a->scale);
+    const uint32_t group = a->heads / a->kv_heads;
+    const uint32_t hq = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    if ((a->n_q + rows_per_wg(dim, hq) - 1) / rows_per_wg(dim, hq) > 65535)
+        return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
+    return MAKO_OK;
+}
+
+}  // namespace mako
+
+extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
+                             const void* k, const void* v, void* o, float* lse, void* stream)
+{
+    if (const int e = attn_check(a, dim, in, out, q, k, v, o))
+        return e;
     if (a->n_q == 0)
         return ok();
     const uint32_t group = a->heads / a->kv_heads;
@@ -699,8 +715,6 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
     FwdParams p{q, k, v, o, lse, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads, a->kv_heads, a->q_pos0, a->block,
                 a->width, a->scale * kLog2e, group, hq, rows_per_wg(dim, hq), 0};
     p.n_qblk = (a->n_q + p.rows_wg - 1) / p.rows_wg;
-    if (p.n_qblk > 65535)
-        return fail(MAKO_EINVAL, "attention: %u queries exceed the grid", a->n_q);
     const dim3 grid(a->heads / hq, p.n_qblk);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (dim == 128) {

@@ -190,7 +190,7 @@ uint32_t device_cus();
 // different buffers, so no call waits on the host or inserts a GPU-side wait. A stream's buffers stay with its handle
 // (hipStreamDestroy waits for the stream's work, so a handle reused later may take them over). Returns null, with
 // nothing allocated, when the allocation fails.
-enum WorkspacePurpose { kWsVtImages = 0, kWsSplitK = 1 };
+enum WorkspacePurpose { kWsVtImages = 0, kWsSplitK = 1, kWsRowTiles = 2 };
 void* stream_workspace(WorkspacePurpose purpose, size_t bytes, hipStream_t s);
 
 }  // namespace mako

@@ -35,6 +35,35 @@ __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 // fragment read differ by an immediate offset).
 __device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d & 7u) ^ ((d >> 3) & 3u); }
 
+// The stores of a vt_image thread: x[i][m] holds head dims 8 e + 2 m, + 1 of key 8 c + i (f16 pairs); it writes
+// the eight 16-byte chunks of head dims 8 e .. 8 e + 7 (keys 8 c .. 8 c + 7) of the tile at dst.
+template <int D>
+__device__ __forceinline__ void vt_store_block(uint32_t* dst, const uint32_t (&x)[8][4], uint32_t c, uint32_t e)
+{
+    #pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {  // head dim d = 8 e + j: keys 8 c + 2 q, + 1 in dword q
+        const uint32_t d = 8 * e + j, m = j >> 1, sh = 16 * (j & 1);
+        u32x4 out;
+        #pragma unroll
+        for (uint32_t q = 0; q < 4; ++q)
+            out[q] = ((x[2 * q][m] >> sh) & 0xffffu) | (((x[2 * q + 1][m] >> sh) & 0xffffu) << 16);
+        *reinterpret_cast<u32x4*>(dst + d * 32 + 4 * (c ^ vt_swz(d))) = out;
+    }
+}
+
+// f16 bits of a pair of T values (bf16 rounds toward zero, as the attention kernels' staging does).
+template <class T>
+__device__ __forceinline__ uint32_t f16_pair_of(uint32_t t2)
+{
+    if constexpr (__is_same(T, __bf16)) {
+        const float lo = __builtin_bit_cast(float, t2 << 16);
+        const float hi = __builtin_bit_cast(float, t2 & 0xffff0000u);
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+    } else {
+        return t2;
+    }
+}
+
 // The V^T tile images: tile t of kv head h is D x 128 bytes (16 or 8 KiB), row d (head dim) of 128 bytes holding keys
 // 64 t .. 64 t + 63 in f16, the 16-byte chunk of keys 64 t + 8 c .. + 7 at slot c ^ vt_swz(d): the LDS layout the
 // kernel reads, so its staging copies tiles unchanged. Keys >= n_k are zero. bf16 becomes f16 rounding toward zero
@@ -59,26 +88,40 @@ __device__ __forceinline__ void vt_image_tiles(const T* v, uint32_t* img, uint32
         if (tile * 64 + 8 * c + i < n_k)
             r = __builtin_nontemporal_load(src + CPR * i);
         #pragma unroll
-        for (uint32_t m = 0; m < 4; ++m) {
-            if constexpr (__is_same(T, __bf16)) {
-                const float lo = __builtin_bit_cast(float, r[m] << 16);
-                const float hi = __builtin_bit_cast(float, r[m] & 0xffff0000u);
-                x[i][m] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-            } else {
-                x[i][m] = r[m];
-            }
-        }
+        for (uint32_t m = 0; m < 4; ++m)
+            x[i][m] = f16_pair_of<T>(r[m]);
     }
-    uint32_t* dst = img + ((size_t)kvh * n_vt + tile) * (D * 32);
+    vt_store_block<D>(img + ((size_t)kvh * n_vt + tile) * (D * 32), x, c, e);
+}
+
+// vt_rows_tiles: the same images straight from fp32 rows (attention from projection rows): value d of key j of kv
+// head kvh is x[j * ld + col0 + kvh * stride + d], rounded to T to nearest even (as mako_heads writes a value tile)
+// and then to f16 as vt_image_tiles converts T, so the images equal vt_image's of the tiles mako_heads would write.
+// Thread (c, e) loads two 16-byte pieces of each of its eight keys. x, ld, col0 and stride: 16-byte aligned.
+template <class T, int D>
+__device__ __forceinline__ void vt_rows_tiles(const float* xr, uint32_t ld, uint32_t col0, uint32_t stride,
+                                              uint32_t* img, uint32_t n_k, uint32_t n_vt, uint32_t bx, uint32_t kvh)
+{
+    constexpr uint32_t CPR = D / 8;
+    const uint32_t tile = bx * (256 / D) + threadIdx.x / D;
+    if (tile >= n_vt)
+        return;
+    const uint32_t t = threadIdx.x % D, e = t % CPR, c = t / CPR;
+    const float* src = xr + (size_t)(tile * 64 + 8 * c) * ld + col0 + (size_t)kvh * stride + 8 * e;
+    uint32_t x[8][4];
     #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j) {  // head dim d = 8 e + j: keys 8 c + 2 q, + 1 in dword q
-        const uint32_t d = 8 * e + j, m = j >> 1, sh = 16 * (j & 1);
-        u32x4 out;
-        #pragma unroll
-        for (uint32_t q = 0; q < 4; ++q)
-            out[q] = ((x[2 * q][m] >> sh) & 0xffffu) | (((x[2 * q + 1][m] >> sh) & 0xffffu) << 16);
-        *reinterpret_cast<u32x4*>(dst + d * 32 + 4 * (c ^ vt_swz(d))) = out;
+    for (uint32_t i = 0; i < 8; ++i) {
+        f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+        if (tile * 64 + 8 * c + i < n_k) {
+            a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + (size_t)i * ld));
+            b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + (size_t)i * ld + 4));
+        }
+        x[i][0] = f16_pair_of<T>(Elem<T>::pack2(a[0], a[1]));
+        x[i][1] = f16_pair_of<T>(Elem<T>::pack2(a[2], a[3]));
+        x[i][2] = f16_pair_of<T>(Elem<T>::pack2(b[0], b[1]));
+        x[i][3] = f16_pair_of<T>(Elem<T>::pack2(b[2], b[3]));
     }
+    vt_store_block<D>(img + ((size_t)kvh * n_vt + tile) * (D * 32), x, c, e);
 }
 
 template <class T, int D = 128>

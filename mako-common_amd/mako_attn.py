@@ -16,7 +16,7 @@ U32_MAX = 0xFFFFFFFF
 # Every symbol include/mako_attn.h declares.
 EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cube_select_workspace",
            "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode",
-           "mako_attn_decode_noalloc", "mako_heads",
+           "mako_attn_decode_noalloc", "mako_heads", "mako_attn_fwd_rows",
            "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots", "mako_proj_bf16",
            "mako_kda_scan")
 
@@ -91,6 +91,8 @@ def lib():
         L.mako_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P, SZ, P]
         L.mako_attn_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), I, I, P, P, P, P, P, P, P]
         L.mako_heads.argtypes = [ctypes.POINTER(HeadsArgs), I, P, P, P, P, P, P]
+        L.mako_attn_fwd_rows.argtypes = [ctypes.POINTER(AttnArgs)] + [ctypes.POINTER(HeadsArgs)] * 3 + [I, I] + \
+            [P] * 9
         L.mako_attn_pv.argtypes = [ctypes.POINTER(PvArgs), P, P, P, P]
         L.mako_attn_gather_scores.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
         L.mako_attn_gather_pv.argtypes = [ctypes.POINTER(GatherArgs), P, P, P, P, P, P]
@@ -98,7 +100,7 @@ def lib():
         L.mako_proj_bf16.argtypes = [ctypes.POINTER(GemmArgs), I, I, P, P, P, P]
         L.mako_kda_scan.argtypes = [ctypes.POINTER(ScanArgs)] + [P] * 9
         for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode",
-                     "mako_attn_decode_noalloc", "mako_heads",
+                     "mako_attn_decode_noalloc", "mako_heads", "mako_attn_fwd_rows",
                      "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots",
                      "mako_proj_bf16", "mako_kda_scan"):
             getattr(L, name).restype = I
@@ -215,6 +217,21 @@ def heads(x, y, *, rows, ld, col0, stride, dim, heads, n_pad, row0=0, rope=0, ro
     a = HeadsArgs(rows, ld, col0, stride, dim, heads, n_pad, row0, rope, rot, eps, clear)
     _check(lib().mako_heads(ctypes.byref(a), dtype_code(y), _ptr(x), _ptr(cs), _ptr(w), _ptr(map_), _ptr(y),
                             _stream(stream)))
+
+
+def attn_fwd_rows(xq, xk, xv, o, hq, hk, hv, *, n_q, n_k, heads, kv_heads, q_pos0, block, in_dtype, cs=None,
+                  wq=None, wk=None, lse=None, scale=None, width=None, stream=None):
+    """mako_attn_fwd_rows on torch tensors: xq, xk, xv float32 rows; hq, hk, hv dicts of mako_heads_args fields
+    (rows, ld, col0, stride, dim, heads, rope, rot, eps); o [n_q][width] of float32 or in_dtype (F16 / BF16)."""
+    dim = hq["dim"]
+    width = heads * dim if width is None else width
+    scale = 1.0 / dim ** 0.5 if scale is None else scale
+    a = AttnArgs(n_q, 0, n_k, 0, heads, kv_heads, q_pos0, block & U32_MAX, width, scale)
+    fields = ("rows", "ld", "col0", "stride", "dim", "heads", "n_pad", "row0", "rope", "rot", "eps", "clear")
+    hs = [HeadsArgs(*[h.get(f, 0) for f in fields]) for h in (hq, hk, hv)]
+    _check(lib().mako_attn_fwd_rows(ctypes.byref(a), *[ctypes.byref(h) for h in hs], in_dtype, dtype_code(o),
+                                    _ptr(xq), _ptr(xk), _ptr(xv), _ptr(cs), _ptr(wq), _ptr(wk), _ptr(o), _ptr(lse),
+                                    _stream(stream)))
 
 
 def attn_pv(p, kv, partial, *, heads, dim, n_kv, keys_per_split, stream=None):

@@ -141,6 +141,46 @@ def test_heads_refuses(kw, code, msg):
     assert rc == code and msg in err, (rc, err)
 
 
+def rows_rc(**kw):
+    """mako_attn_fwd_rows with the Qwen3-8B step's arguments (64 tokens) and fake device pointers, changed by kw."""
+    a = dict(n_q=64, q_pad=0, n_k=64, k_pad=0, heads=32, kv_heads=8, q_pos0=0, block=0xFFFFFFFF, width=4096,
+             scale=0.088)
+    a.update(kw.pop("attn", {}))
+    base = dict(rows=64, ld=4096, col0=0, stride=128, dim=128, heads=32, n_pad=0, row0=0, rope=1, rot=128, eps=1e-6,
+                clear=0)
+    hs = []
+    for name, extra in (("hq", {}), ("hk", dict(ld=1024, heads=8)),
+                        ("hv", dict(ld=1024, heads=8, rope=0, rot=0, eps=0.0))):
+        h = dict(base, **extra)
+        h.update(kw.pop(name, {}))
+        hs.append(M.HeadsArgs(*[h[f] for f, _ in M.HeadsArgs._fields_]))
+    args = M.AttnArgs(*[a[f] for f, _ in M.AttnArgs._fields_])
+    ins, out = kw.pop("in_", M.BF16), kw.pop("out", M.F32)
+    ptrs = [kw.pop(n, FAKE) for n in ("xq", "xk", "xv", "cs", "wq", "wk", "o")]
+    rc = M.lib().mako_attn_fwd_rows(ctypes.byref(args), *[ctypes.byref(h) for h in hs], ins, out, *ptrs, None, None)
+    return rc, M.lib().mako_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(o=None), M.EINVAL, "null"),
+    (dict(hk=dict(dim=64)), M.EINVAL, "heads of 128, 64"),
+    (dict(hq=dict(heads=16)), M.EINVAL, "16 / 8 / 8 heads produced for 32 over 8"),
+    (dict(hv=dict(rows=60)), M.EINVAL, "64 / 64 / 60 rows produced"),
+    (dict(in_=M.F32), M.EUNSUPPORTED, "input type"),
+    (dict(attn=dict(scale=0.0)), M.EINVAL, "scale"),
+    (dict(hq=dict(rot=130)), M.EINVAL, "over 130"),
+    (dict(wk=None), M.EINVAL, "without a weight"),
+    (dict(hv=dict(eps=1e-6)), M.EINVAL, "without a weight"),      # the value producer takes no weight
+    (dict(hk=dict(col0=4)), M.EINVAL, "exceed rows of 1024"),
+    (dict(xv=None), M.EINVAL, "null"),
+])
+def test_rows_refuses(kw, code, msg):
+    """mako_attn_fwd_rows refuses what mako_heads and mako_attn_fwd refuse, and arguments that do not describe one
+    step (heads, rows or widths that disagree), before touching the device."""
+    rc, err = rows_rc(**kw)
+    assert rc == code and msg in err, (rc, err)
+
+
 def gather_rc(fn, **kw):
     """Calls one of the four gathered decode helpers with valid arguments but for the overrides in kw."""
     if fn == "mako_attn_pv":
