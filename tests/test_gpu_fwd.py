@@ -109,6 +109,12 @@ def test_sweep(case):
     assert np.all(o[n_q:] == 12288.0), "rows past n_q were written"
 
 
+def every_tile(rng, heads, S):
+    """One random row of every (head, 64-row query tile): each workgroup item of the launch is compared."""
+    h, t = np.meshgrid(np.arange(heads), np.arange(S // 64), indexing="ij")
+    return np.stack([h.ravel(), t.ravel() * 64 + rng.integers(0, 64, h.size)], 1).astype(np.uint32)
+
+
 def _sampled(heads, kv, dim, S, block, dt, n_rows, seed):
     rng = np.random.default_rng(seed)
     qb, kb, vb = (G.randn_bits(rng, (h, S, dim), dt) for h in (heads, kv, kv))
@@ -116,6 +122,7 @@ def _sampled(heads, kv, dim, S, block, dt, n_rows, seed):
     o, lse = run_fwd(qb, kb, vb, dt, dt, **args)
     rows = np.concatenate([[0, 1, 31, 32, 63, 64, S - 1], rng.integers(0, S, n_rows)])
     hr = np.stack([rng.integers(0, heads, len(rows)), rows], 1).astype(np.uint32)
+    hr = np.concatenate([hr, every_tile(rng, heads, S)])
     want_o, want_l = O.attn_dense_rows(qb, kb, vb, hr, dtype=dt, **args)
     got_o = np.stack([o[r, h * dim:(h + 1) * dim] for h, r in hr])
     got_l = np.array([lse[h, r] for h, r in hr])
@@ -126,27 +133,29 @@ def _sampled(heads, kv, dim, S, block, dt, n_rows, seed):
 
 
 def test_qwen3_8b_causal_s4096_bf16_sampled():
-    """32 query heads over 8 kv heads, D 128, S 4096, causal, bf16 in and out: sampled rows against the oracle."""
+    """32 query heads over 8 kv heads, D 128, S 4096, causal, bf16 in and out: one row of every (head, query tile)
+    and sampled rows against the oracle."""
     print("causal S4096 bf16", flush=True)
     _sampled(32, 8, 128, 4096, U32, O.BF16, 300, 4096)
 
 
 def test_bidirectional_s16384_bf16_sampled():
-    """24 heads MHA, D 128, S 16384, bidirectional, bf16 in and out: sampled rows against the oracle."""
+    """24 heads MHA, D 128, S 16384, bidirectional, bf16 in and out: one row of every (head, query tile) and
+    sampled rows against the oracle."""
     print("bidirectional S16384 bf16", flush=True)
     _sampled(24, 24, 128, 16384, 0, O.BF16, 60, 16384)
 
 
 def test_h3_vae_d64_bidirectional_s4096_bf16_sampled():
     """16 heads MHA, D 64, S 4096, bidirectional, bf16 in and out (the H3 VAE's attention shape, flash_fwd_r64 at
-    heads of 64): sampled rows against the oracle."""
+    heads of 64): one row of every (head, query tile) and sampled rows against the oracle."""
     print("bidirectional D64 S4096 bf16", flush=True)
     _sampled(16, 16, 64, 4096, 0, O.BF16, 200, 64)
 
 
 def test_qwen35_d256_causal_s4096_bf16_sampled():
     """16 query heads over 2 kv heads, D 256, S 4096, causal, bf16 in and out (Qwen3.5 gated attention,
-    flash_fwd_d256): sampled rows against the oracle."""
+    flash_fwd_d256): one row of every (head, query tile) and sampled rows against the oracle."""
     print("causal D256 S4096 bf16", flush=True)
     _sampled(16, 2, 256, 4096, U32, O.BF16, 120, 256)
 

@@ -197,7 +197,8 @@ def test_causal_full_lists_equal_causal_dense():
 
 def test_window_random_s16384_sampled():
     """B1, 32 query heads over 8 kv heads, D 128, S 16384, 64x64 blocks, each block: the diagonal (causal), the 8
-    before it and 8 random earlier ones (seed 16384, one list per kv head), bf16: sampled rows vs the oracle."""
+    before it and 8 random earlier ones (seed 16384, one list per kv head), bf16: one row of every (head, query tile)
+    and sampled rows vs the oracle."""
     heads, kv, S = 32, 8, 16384
     nb = S // 64
     sel, nsel = M.window_random_blocks(nb, kv, seed=16384)
@@ -215,6 +216,10 @@ def test_window_random_s16384_sampled():
     rng = np.random.default_rng(2)
     rows = np.concatenate([[0, 1, 63, 64, 511, 512, S - 1], rng.integers(0, S, 150)])
     hr = np.stack([rng.integers(0, heads, len(rows)), rows], 1).astype(np.uint32)
+    # and one random row of every (head, 64-row query tile): each workgroup item of the launch is compared
+    h_, t_ = np.meshgrid(np.arange(heads), np.arange(nb), indexing="ij")
+    hr = np.concatenate([hr, np.stack([h_.ravel(), t_.ravel() * 64 + rng.integers(0, 64, h_.size)], 1)]).astype(
+        np.uint32)
     bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
     want_o, want_l = O.attn_sparse_rows(bits(q), bits(k), bits(v), sel, nsel, valid, hr, dtype=O.BF16, **args)
     got = np.stack([o[r, h * 128:(h + 1) * 128] for h, r in hr])
