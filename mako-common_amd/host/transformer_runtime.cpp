@@ -93,6 +93,30 @@ void TransformerRuntime::attention(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buff
     after(enc, label);
 }
 
+void TransformerRuntime::attention_rows(gpu::Encoder*& enc, gpu::Buffer* xq, uint32_t ld_q, gpu::Buffer* xk,
+                                        gpu::Buffer* xv, uint32_t ld_kv, gpu::Buffer* cs, uint32_t rot,
+                                        gpu::Buffer* wq, gpu::Buffer* wk, float eps, gpu::Buffer* o, uint32_t n_q,
+                                        uint32_t n_k, uint32_t n_heads, uint32_t kv_heads, uint32_t q_pos0,
+                                        uint32_t block, uint32_t dim, const AttnOptions& opt)
+{
+    if (dim != 64 && dim != 128 && dim != 256)
+        throw std::runtime_error(fmt("attention: heads of %u", dim));
+    if (rot % 2 || rot > dim)
+        throw std::runtime_error(fmt("heads_partial: heads of %u with %u rotated", dim, rot));
+    const uint32_t rope = rot ? 1u : 0u;
+    const mako_heads_args hq{n_q, ld_q, 0, dim, dim, n_heads, n_q, 0, rope, rot, wq ? eps : 0.0f, 0};
+    const mako_heads_args hk{n_k, ld_kv, 0, dim, dim, kv_heads, n_k, 0, rope, rot, wk ? eps : 0.0f, 0};
+    const mako_heads_args hv{n_k, ld_kv, 0, dim, dim, kv_heads, n_k, 0, 0, 0, 0.0f, 0};
+    const mako_attn_args a{n_q, 0, n_k, 0, n_heads, kv_heads, q_pos0, block, n_heads * dim,
+                           1.0f / std::sqrt(float(dim))};
+    const auto f = [](gpu::Buffer* b) { return b ? static_cast<const float*>(b->ptr) : nullptr; };
+    before(enc);
+    for (int r = repeats("attention_rows"); r > 0; --r)
+        check(mako_attn_fwd_rows(&a, &hq, &hk, &hv, opt.in, opt.out, f(xq), f(xk), f(xv), f(cs), f(wq), f(wk),
+                                 o->ptr, opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
+    after(enc, "attention_rows");
+}
+
 void TransformerRuntime::cube_select(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, uint32_t heads, uint32_t q_pad,
                                      uint32_t k_pad, uint32_t n_cubes, gpu::Buffer* cnt, uint32_t topk,
                                      gpu::Buffer*& sel, gpu::Buffer*& nsel, uint32_t local, uint32_t stride,

@@ -56,6 +56,15 @@ protected:
     void attention(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buffer* k, gpu::Buffer* v, gpu::Buffer* o, uint32_t n_q,
                    uint32_t q_pad, uint32_t n_k, uint32_t k_pad, uint32_t heads, uint32_t kv_heads, uint32_t q_pos0,
                    uint32_t block, uint32_t dim = kHeadDim, const AttnOptions& opt = {});
+    // Attention straight from fp32 projection rows (no counterpart in the reference, whose prefill steps call the
+    // producers and then attention): query heads of dim `dim` side by side in xq rows of ld_q, key and value heads
+    // in xk / xv rows of ld_kv; q and k RMS-normed when wq / wk are given (eps) and their first rot values rotated
+    // by cs [T][rot / 2] (i with i + rot / 2) as heads_partial does, v sliced; then attention() over them. The
+    // same results as those calls, in two launches where the fused kernels apply (mako_attn_fwd_rows).
+    void attention_rows(gpu::Encoder*& enc, gpu::Buffer* xq, uint32_t ld_q, gpu::Buffer* xk, gpu::Buffer* xv,
+                        uint32_t ld_kv, gpu::Buffer* cs, uint32_t rot, gpu::Buffer* wq, gpu::Buffer* wk, float eps,
+                        gpu::Buffer* o, uint32_t n_q, uint32_t n_k, uint32_t heads, uint32_t kv_heads,
+                        uint32_t q_pos0, uint32_t block, uint32_t dim = kHeadDim, const AttnOptions& opt = {});
     // Per head and query cube, the `topk` key cubes by the dot product of the cubes' mean q and k, into the
     // Runtime-owned scratch sel [heads][n_cubes][min(topk, n_cubes)] and nsel [heads][n_cubes] (returned by
     // reference, valid until the next call). local: 0 by score alone, 1 the query cube first, 3 also the cubes

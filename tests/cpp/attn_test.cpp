@@ -41,6 +41,7 @@ class Harness final : public mako::models::TransformerRuntime {
 public:
     explicit Harness(mako::gpu::Telemetry t = mako::gpu::Telemetry::kernels) : TransformerRuntime(t) {}
     using TransformerRuntime::attention;
+    using TransformerRuntime::attention_rows;
     using TransformerRuntime::attention_decode;
     using TransformerRuntime::heads;
     using TransformerRuntime::heads_partial;
@@ -358,6 +359,43 @@ int main()
             threw = std::string(e.what()) == "heads_partial: heads of 128 with 95 rotated";
         }
         check(threw, "heads_partial refuses an odd rotation");
+    }
+    // attention_rows(): the producers and attention in one call, against heads_partial x 3 + attention() through
+    // the same runtime, bit for bit (32 / 8 heads of 128 over 300 tokens, q and k normed and rotated, bf16 tiles).
+    {
+        const uint32_t T = 300, H = 32, KV = 8, D = 128;
+        std::vector<float> xq(size_t(T) * H * D), xk(size_t(T) * KV * D), xv(xk.size()), cs(size_t(T) * D);
+        std::vector<float> wq(D), wk(D);
+        for (auto* v : {&xq, &xk, &xv})
+            for (auto& x : *v)
+                x = float(2 * normal());
+        for (uint32_t t = 0; t < T; ++t)
+            for (uint32_t i = 0; i < D / 2; ++i) {
+                const double ang = 0.001 * (t + 1) * (i + 1);
+                cs[(size_t(t) * D / 2 + i) * 2] = float(std::cos(ang));
+                cs[(size_t(t) * D / 2 + i) * 2 + 1] = float(std::sin(ang));
+            }
+        for (uint32_t i = 0; i < D; ++i) {
+            wq[i] = float(0.5 + 0.004 * i);
+            wk[i] = float(1.5 - 0.004 * i);
+        }
+        auto qx = put(h, "rq", xq), kx = put(h, "rk", xk), vx = put(h, "rv", xv), cb = put(h, "rcs", cs);
+        auto wqb = put(h, "rwq", wq), wkb = put(h, "rwk", wk);
+        auto o1 = h.scratch("ro1", size_t(T) * H * D * 4), o2 = h.scratch("ro2", size_t(T) * H * D * 4);
+        auto qt = h.scratch("rqt", size_t(H) * T * D * 2), kt = h.scratch("rkt", size_t(KV) * T * D * 2);
+        auto vt = h.scratch("rvt", size_t(KV) * T * D * 2);
+        mako::models::AttnOptions opt;
+        opt.in = MAKO_BF16;
+        auto* enc = h.encoder();
+        h.attention_rows(enc, qx, H * D, kx, vx, KV * D, cb, D, wqb, wkb, 1e-6f, o1, T, T, H, KV, 0, UINT32_MAX, D,
+                         opt);
+        h.heads_partial(enc, qx, H * D, 0, D, D, D, H, T, T, cb, wqb, 1e-6f, qt, nullptr, MAKO_BF16);
+        h.heads_partial(enc, kx, KV * D, 0, D, D, D, KV, T, T, cb, wkb, 1e-6f, kt, nullptr, MAKO_BF16);
+        h.heads_partial(enc, vx, KV * D, 0, D, D, 0, KV, T, T, nullptr, nullptr, 0.0f, vt, nullptr, MAKO_BF16);
+        h.attention(enc, qt, kt, vt, o2, T, T, T, T, H, KV, 0, UINT32_MAX, D, opt);
+        h.finish(enc);
+        const auto a = get<uint32_t>(o1, size_t(T) * H * D), b = get<uint32_t>(o2, a.size());
+        check(a == b, "attention_rows equals heads_partial x 3 + attention() bit for bit");
     }
     // The output projection after attention: proj() with BF16 weights (f32 rows, the split, bf16 rows).
     {

@@ -1,7 +1,7 @@
 """The C++ host side on the GPU: tests/cpp/sparse_attn_test (the reference's tests/sparse_attn_test.cpp
 restated through TransformerRuntime::cube_select / attention_sparse) and tests/cpp/attn_test (attention() with the
 reference's arguments and defaults, AttnOptions, attention_decode, the probe hook after attention(), layer / part
-timing, MAKO_REPEAT, a refused head width). Each prints ok / FAIL
+timing, MAKO_REPEAT, a refused head width, attention_rows against the producers and attention() bit for bit). Each prints ok / FAIL
 lines and exits nonzero on a failure."""
 import os
 import subprocess
