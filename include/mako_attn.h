@@ -196,8 +196,11 @@ int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const f
  * Attention straight from fp32 projection rows. No counterpart in the reference, whose prefill steps produce the
  * head tiles and then attend (TransformerRuntime::heads / heads_norm / heads_partial, then attention:
  * src/models/qwen_text.cpp:308-311 and 414-418, src/models/h3_vae.cpp:219); it is for callers that keep those
- * tiles only for the attention call. The result is that of
- *   mako_heads(hq, in, xq, cs, wq, NULL, qt); mako_heads(hk, in, xk, cs, wk, NULL, kt);
+ * tiles only for the attention call. cs holds the angles of key positions 0 .. n_k - 1 (one row a key, as the key
+ * producer reads it); query row t sits at position q_pos0 + t and is rotated by row q_pos0 + t, so a rotated query
+ * head needs q_pos0 + n_q <= n_k (MAKO_EINVAL otherwise; with n_k = 0 the queries are unused and no angle is read).
+ * The result is that of
+ *   mako_heads(hq, in, xq, cs + q_pos0 * hq->rot, wq, NULL, qt); mako_heads(hk, in, xk, cs, wk, NULL, kt);
  *   mako_heads(hv, in, xv, cs, NULL, NULL, vt); mako_attn_fwd(a, hq->dim, in, out, qt, kt, vt, o, lse)
  * bit for bit, with the tiles [heads][rows][dim] in the stream's workspace: each of hq / hk / hv is read as
  * mako_heads reads it except n_pad, row0 and clear (the tiles hold exactly `rows` rows); a is read as

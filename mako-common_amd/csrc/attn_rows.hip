@@ -134,7 +134,17 @@ extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args
     t.k_pad = a->n_k;
     if (const int e = attn_check(&t, dim, in, out, o, o, o, o))
         return e;
-    if (const int e = heads_check(&tq, in, xq, cs, wq, o))
+    // The angle table holds one row a key position (0 .. n_k - 1, the key producer's rows); query row t sits at
+    // position q_pos0 + t and takes that row. With no keys every row is fully masked and the queries are never
+    // used, so they are not rotated (no angle is read).
+    if (a->n_k == 0)
+        tq.rope = 0;
+    if (tq.rope && (uint64_t)a->q_pos0 + a->n_q > a->n_k)
+        return fail(MAKO_EINVAL,
+                    "attention from rows: rotated queries at positions %u .. %llu past the %u angle rows", a->q_pos0,
+                    (unsigned long long)a->q_pos0 + a->n_q - 1, a->n_k);
+    const float* csq = cs && tq.rope ? cs + (size_t)a->q_pos0 * hq->rot : cs;
+    if (const int e = heads_check(&tq, in, xq, csq, wq, o))
         return e;
     if (const int e = heads_check(&tk, in, xk, cs, wk, o))
         return e;
@@ -147,7 +157,7 @@ extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args
                  k_bytes = round256((size_t)a->kv_heads * a->n_k * dim * 2);
     const uint32_t osz = out == MAKO_F32 ? 4u : 2u;
     const bool fits = dim == 256 ? d256_fits(&t) : dim == 128 ? fwd64_fits<128>(&t, osz) : fwd64_fits<64>(&t, osz);
-    const bool fused = fits && !splitk_takes(&t, dim) && heads_vec_takes(&tq, xq, cs, wq, o) &&
+    const bool fused = fits && !splitk_takes(&t, dim) && heads_vec_takes(&tq, xq, csq, wq, o) &&
                        heads_vec_takes(&tk, xk, cs, wk, o) && tv.rope == 0 && tv.eps == 0.0f &&
                        heads_vec_takes(&tv, xv, nullptr, nullptr, o);
     char* ws = static_cast<char*>(stream_workspace(kWsRowTiles, q_bytes + 2 * k_bytes + 256, s));
@@ -157,14 +167,14 @@ extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args
     void *qt = ws, *kt = ws + q_bytes, *vt = ws + q_bytes + k_bytes;
     if (!fused) {
         // The producers and attention as separate launches (the same results).
-        int e = mako_heads(&tq, in, xq, cs, wq, nullptr, qt, stream);
+        int e = mako_heads(&tq, in, xq, csq, wq, nullptr, qt, stream);
         if (!e)
             e = mako_heads(&tk, in, xk, cs, wk, nullptr, kt, stream);
         if (!e)
             e = mako_heads(&tv, in, xv, cs, nullptr, nullptr, vt, stream);
         return e ? e : mako_attn_fwd(&t, dim, in, out, qt, kt, vt, o, lse, stream);
     }
-    const HeadsParams pq = heads_params(&tq, xq, cs, wq, nullptr, qt, true);
+    const HeadsParams pq = heads_params(&tq, xq, csq, wq, nullptr, qt, true);
     const HeadsParams pk = heads_params(&tk, xk, cs, wk, nullptr, kt, true);
     if (in == MAKO_BF16)
         return out == MAKO_F32 ? launch_rows_dim<__bf16, float>(dim, &t, pq, pk, &tv, xv, o, lse, s)

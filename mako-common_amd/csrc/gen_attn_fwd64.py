@@ -230,27 +230,41 @@ def stage_writes(kregs=KSTG, vregs=VSTG):
 
 
 def dma_issue():
+    """The LDS DMA loads of the next tile, flat (dma_groups() in order)."""
+    groups, tail = dma_groups()
+    return sum(groups, []) + tail
+
+
+def dma_groups():
     """LDS DMA loads of the next tile into buffer SBW (lane l of a load writes 16 bytes at M0 + offset + 16 l), then
     the sources move on by a tile and the destinations to the next buffer. K: pieces w, w + 4, w + 8, w + 12 of the
     17 KiB image at M0 = their LDS address, and piece 16 (every wave; the same bytes to the same place). V^T: the
     wave's 4 KiB of the tile image, as four 1 KiB loads whose offset moves source and destination alike. A write of
     M0 is read by an LDS load after one wait state. Record counts shrink by a tile and stop at zero. Sparse: the
     sources are set from SD, the tile's first key (K rows and V^T images are both 256 bytes a key), one tile long, or
-    empty when SD is -1."""
-    ops = []
+    empty when SD is -1.
+    Returns (groups, tail): a group per load (with the M0 write it needs), and the scalar work after the last load.
+    A phase spreads the groups evenly between its MFMAs: a burst of these loads holds up the wave's vector and matrix
+    instructions behind it (a timing probe of the plain iteration on one CU: 2654 cycles a tile with the loads at
+    the phase's start, 2536 spread one every few MFMAs)."""
+    groups = []
+    pre = []
     if SPARSE:
         t = SROT["k"]
-        ops += [f"s_lshl_b32 {t}, {SD}, 8",
-                f"s_add_u32 {KRS[0]}, %[kb0], {t}", f"s_addc_u32 {KRS[1]}, %[kb1], 0",
-                f"s_add_u32 {VRS[0]}, %[vb0], {t}", f"s_addc_u32 {VRS[1]}, %[vb1], 0",
-                f"s_cmp_eq_u32 {SD}, -1", f"s_cselect_b32 {KRS[2]}, 0, 0x4000", f"s_mov_b32 {VRS[2]}, {KRS[2]}"]
+        pre = [f"s_lshl_b32 {t}, {SD}, 8",
+               f"s_add_u32 {KRS[0]}, %[kb0], {t}", f"s_addc_u32 {KRS[1]}, %[kb1], 0",
+               f"s_add_u32 {VRS[0]}, %[vb0], {t}", f"s_addc_u32 {VRS[1]}, %[vb1], 0",
+               f"s_cmp_eq_u32 {SD}, -1", f"s_cselect_b32 {KRS[2]}, 0, 0x4000", f"s_mov_b32 {VRS[2]}, {KRS[2]}"]
     for m in range(NKP):
-        ops += [f"s_add_u32 m0, {SKWW}, {4096 * m}" if m else f"s_mov_b32 m0, {SKWW}", "s_nop 0",
-                f"buffer_load_dwordx4 %[kd{m}], {quad(KRS)}, 0 offen lds"]
-    ops += [f"s_add_u32 m0, {SKW}, {4 * NKP * 1024}", "s_nop 0",
-            f"buffer_load_dwordx4 %[kd4], {quad(KRS)}, 0 offen lds"]
-    ops += [f"s_mov_b32 m0, {SVWW}", "s_nop 0"]
-    ops += [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds" for i in range(NVP)]
+        groups.append([f"s_add_u32 m0, {SKWW}, {4096 * m}" if m else f"s_mov_b32 m0, {SKWW}", "s_nop 0",
+                       f"buffer_load_dwordx4 %[kd{m}], {quad(KRS)}, 0 offen lds"])
+    groups.append([f"s_add_u32 m0, {SKW}, {4 * NKP * 1024}", "s_nop 0",
+                   f"buffer_load_dwordx4 %[kd4], {quad(KRS)}, 0 offen lds"])
+    for i in range(NVP):
+        groups.append(([f"s_mov_b32 m0, {SVWW}", "s_nop 0"] if i == 0 else []) +
+                      [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds"])
+    groups[0] = pre + groups[0]
+    ops = []
     step = 128 * D   # K rows and V^T images: 2 d bytes a key, 64 keys a tile
     for r in (KRS, VRS) if not SPARSE else ():
         ops += [f"s_add_u32 {r[0]}, {r[0]}, {step:#x}", f"s_addc_u32 {r[1]}, {r[1]}, 0",
@@ -262,7 +276,7 @@ def dma_issue():
             f"s_add_u32 {wk}, {wk}, {K_TILE:#x}", f"s_add_u32 {wv}, {wv}, {V_TILE:#x}",
             f"s_add_u32 {SKW}, {SKW}, {wk}", f"s_add_u32 {SKWW}, {SKWW}, {wk}", f"s_add_u32 {SVWW}, {SVWW}, {wv}",
             f"s_add_u32 {SBW}, {SBW}, 1", f"s_cmp_eq_u32 {SBW}, {NBUF}", f"s_cselect_b32 {SBW}, 0, {SBW}"]
-    return ops
+    return groups, ops
 
 
 def staging():
@@ -311,13 +325,15 @@ def pv_mfmas():
     return out
 
 
-def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=()):
+def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=(), dma=None):
     """Emits the MFMAs of a phase, each tagged with the fragment it reads, fed by a ring of RING LDS reads, with the
     instructions of `valu` spread evenly between them. Fragment f lives in ring slot f % RING; its read goes out AHEAD
     fragments before its MFMAs (a slot is refilled two fragments after its previous occupant's last MFMA). The first
     `pre` reads were issued before the phase began, as the last LDS instructions before it. nxt = (kind, reads) of
     the next phase: its read m goes out after fragment len(reads) + m - AHEAD of this phase, and not before `gate`,
-    the instructions emitted after fragment gate_at's MFMAs. Returns how many of the next phase's reads went out.
+    the instructions emitted after fragment gate_at's MFMAs. dma = (groups, tail) of dma_groups(): group i after
+    MFMA i * n / len(groups) (after that MFMA's share of `valu`), the tail after the last MFMA's.
+    Returns how many of the next phase's reads went out.
     LDS returns in order, so the wait for a read is lgkmcnt(LDS instructions issued after it); LDS instructions inside
     `valu` are counted too."""
     issued = [(kind, f) for f in range(pre)]
@@ -347,6 +363,12 @@ def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=()):
     per = [0] * n
     for i in range(len(valu)):
         per[min(n - 1, i * n // len(valu))] += 1
+    dslot = [[] for _ in range(n)]
+    if dma:
+        groups, tail = dma
+        for i, grp in enumerate(groups):
+            dslot[i * n // len(groups)] += grp
+        dslot[n - 1] += tail
     vi = 0
     for i, (f, text) in enumerate(mfmas):
         if i == 0 or mfmas[i - 1][0] != f:
@@ -365,6 +387,8 @@ def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=()):
             e(op)
             if op.startswith("ds_"):
                 issued.append(None)
+        for op in dslot[i]:
+            e(op)
     assert vi == len(valu)
     assert gate_at is None or gate_at in {f for f, _ in mfmas}
     return n_next
@@ -737,13 +761,15 @@ def body_rest(e, in_dtype, out_dtype):
         K(j + 2) for the next iteration's phase QK."""
         cur, nxt = par, 1 - par
         tag = f"{variant}{par}"
-        valu = staging()
+        # the staging of tile j + 3: DMA loads spread between phase QK's MFMAs (register staging: in the list)
+        dma = dma_groups() if STAGING == "dma" and variant != "last" else None
+        valu = [] if dma else staging()
         if variant != "first":
             valu += pack_and_sum(cur)
         n_v = 0
         if variant != "last":
             n_v = phase(e, "K", k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu, pre=0 if variant == "first" else N_K_AHEAD,
-                        nxt=("V", v_reads()))
+                        nxt=("V", v_reads()), dma=dma)
         else:
             for op in valu:
                 e(op)

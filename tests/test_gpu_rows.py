@@ -71,9 +71,10 @@ def run_separate(host, hs, *, n_q, n_k, heads, kv, q_pos0, block, dt, out):
     qt = torch.zeros((heads, max(n_q, 1), dim), dtype=tdt, device="cuda")
     kt = torch.zeros((kv, max(n_k, 1), dim), dtype=tdt, device="cuda")
     vt = torch.zeros((kv, max(n_k, 1), dim), dtype=tdt, device="cuda")
-    for x, h, y, w in ((xq, hq, qt, wq), (xk, hk, kt, wk), (xv, hv, vt, None)):
+    csq = cs[q_pos0:] if cs is not None else None  # query row t sits at position q_pos0 + t
+    for x, h, y, w, c in ((xq, hq, qt, wq, csq), (xk, hk, kt, wk, cs), (xv, hv, vt, None, cs)):
         if h["rows"]:
-            M.heads(x, y, n_pad=y.shape[1], cs=cs if h.get("rope") else None, w=w if h.get("eps") else None, **h)
+            M.heads(x, y, n_pad=y.shape[1], cs=c if h.get("rope") else None, w=w if h.get("eps") else None, **h)
     odt = torch.float32 if out == "f32" else tdt
     o = torch.full((n_q, heads * dim), float("nan"), dtype=odt, device="cuda")
     lse = torch.full((heads, max(n_q, 1)), float("nan"), dtype=torch.float32, device="cuda")
@@ -88,9 +89,10 @@ def oracle(host, hs, *, n_q, n_k, heads, kv, q_pos0, block, dt):
     hq, hk, hv = hs
     dim = hq["dim"]
     tiles = []
-    for x, h, w, rows in ((xq, hq, wq, n_q), (xk, hk, wk, n_k), (xv, hv, None, n_k)):
+    csq = cs[q_pos0:q_pos0 + n_q]  # the angles of positions q_pos0 .. q_pos0 + n_q - 1
+    for x, h, w, rows, c in ((xq, hq, wq, n_q, csq), (xk, hk, wk, n_k, cs), (xv, hv, None, n_k, cs)):
         a = dict(h, n_pad=max(rows, 1))
-        tiles.append(O.heads(x, cs if a.get("rope") else None, w if a.get("eps") else None, None, out=dt, **a))
+        tiles.append(O.heads(x, c if a.get("rope") else None, w if a.get("eps") else None, None, out=dt, **a))
     return O.attn_dense(*tiles, n_q=n_q, q_pad=max(n_q, 1), n_k=n_k, k_pad=max(n_k, 1), heads=heads,
                         kv_heads=kv, q_pos0=q_pos0, block=block, dim=dim, dtype=dt)
 
@@ -131,6 +133,31 @@ def test_rows_against_separate_launches_and_oracle(case):
     got_o = G.to_host(o)
     G.assert_attn_close(got_o, want_o, "output")
     G.assert_lse_close(lse.cpu().numpy().astype(np.float64)[:, :T_q], want_l, "lse")
+
+
+def test_offset_queries_equal_the_last_rows_of_the_whole_prefill():
+    """Rotated queries at q_pos0 > 0 take the angles of their positions: 100 queries at positions 200 .. 299 over
+    300 keys give the same rows (within the attention tolerance) as rows 200 .. 299 of the whole 300-row prefill
+    whose query rows 200 .. 299 are the same projection rows. A query rotated by the angle of its row index instead
+    of its position would score every key at the wrong relative position."""
+    rng = np.random.default_rng(17)
+    T, off, heads, kv, dim = 300, 200, 8, 2, 128
+    host, (hq, hk, hv) = make(rng, T_q=T, T_k=T, heads=heads, kv=kv, dim=dim, rope=1, rot=128, eps_q=1e-6,
+                              eps_k=1e-6)
+    xq, xk, xv, cs, wq, wk = host
+    kw = dict(n_k=T, heads=heads, kv=kv, block=U32, dt=O.BF16, out="f32")
+    whole, wl = run_rows(host, (hq, hk, hv), n_q=T, q_pos0=0, **kw)
+    part_host = (np.ascontiguousarray(xq[off:]), xk, xv, cs, wq, wk)
+    part, pl = run_rows(part_host, (dict(hq, rows=T - off), hk, hv), n_q=T - off, q_pos0=off, **kw)
+    G.assert_attn_close(G.to_host(part), G.to_host(whole)[off:], "offset rows")
+    G.assert_lse_close(pl.cpu().numpy().astype(np.float64)[:, :T - off], wl.cpu().numpy()[:, off:], "offset lse")
+
+
+def test_rows_refuses_query_angles_past_the_table():
+    rng = np.random.default_rng(5)
+    host, (hq, hk, hv) = make(rng, T_q=64, T_k=100, heads=4, kv=2, dim=128, rope=1, rot=128, eps_q=0.0, eps_k=0.0)
+    with pytest.raises(M.MakoError, match="angle rows"):
+        run_rows(host, (hq, hk, hv), n_q=64, n_k=100, heads=4, kv=2, q_pos0=50, block=U32, dt=O.BF16, out="f32")
 
 
 def test_rows_refuses_a_normed_value_head():
