@@ -206,7 +206,7 @@ def bench_prefill(torch, M, steps, warmup, with_cpu):
     out = {"ms": ms, "kernel_ms": kms, "tflops": tflops, "flop": flop,
            "roofline": {"bound": "mfma", "achieved": ktflops, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": ktflops / PEAK_TFLOPS, "traffic": traffic("flash_fwd_causal_s4096"),
-                        "kernel": "vt_image<bf16> + flash_fwd_r64<bf16,bf16> (one call, both kernels)", "kernel_ms": kms}}
+                        "kernel": "flash_fwd_r64<bf16,bf16> (one launch a call)", "kernel_ms": kms}}
     if with_cpu:
         import oracle as O
 
@@ -241,7 +241,7 @@ def bench_s512(torch, M, steps, warmup, with_cpu):
            "dtype": "f16",
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_causal_s512"),
-                        "kernel": "vt_image<f16> + flash_fwd_r64<f16,f32> (one call, both kernels)", "kernel_ms": kms,
+                        "kernel": "flash_fwd_r64<f16,f32> (one launch a call)", "kernel_ms": kms,
                         "note": "1.08 GFLOP: 16 workgroups on 256 CUs, launch- and latency-bound"},
            "config": {"workload": "causal GQA prefill, batch 1, 16 query heads / 8 kv heads, D 128, S 512, f16 in, "
                                   "f32 out, LSE (the reference-CPU-runnable case)"}}
@@ -368,7 +368,7 @@ def bench_bidir(torch, M, steps, warmup, with_cpu):
            "kernel_ms": round(kms, 4), "frac": round(kt / PEAK_TFLOPS, 4), "dtype": "bf16",
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_bidir_s16384"),
-                        "kernel": "vt_image<bf16> + flash_fwd_r64<bf16,bf16> (one call, both kernels)", "kernel_ms": kms},
+                        "kernel": "flash_fwd_r64<bf16,bf16> (one launch a call)", "kernel_ms": kms},
            "config": {"workload": "bidirectional MHA, 24 heads, D 128, S 16384, bf16 in/out, LSE"}}
     if with_cpu:
         import oracle as O
@@ -389,7 +389,7 @@ def bench_other_dims(torch, M, steps, warmup, with_cpu, names=None):
                             workload="causal GQA, 16 query heads / 2 kv heads, D 256, S 4096, bf16 in/out, LSE "
                                      "(Qwen3.5 gated attention)"),
         "d64_bidir": dict(H=16, KV=16, D=64, S=4096, block=0, seed=64,
-                          kernel="vt_image<bf16,64> + flash_fwd_r64<bf16,bf16,64> (one call, both kernels)",
+                          kernel="flash_fwd_r64<bf16,bf16,64> (one launch a call)",
                           workload="bidirectional MHA, 16 heads, D 64, S 4096, bf16 in/out, LSE (H3 VAE ViT)"),
     }
     out = {}
@@ -458,7 +458,7 @@ def bench_sparse(torch, M, steps, warmup, with_cpu):
            "gathered_gbps": round(gathered / (kms * 1e-3) / 1e9, 1),
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": kt / PEAK_TFLOPS, "traffic": hbm,
-                        "kernel": "sparse_prep<bf16> + flash_sparse_r64<bf16,bf16> (one call, both kernels)",
+                        "kernel": "sparse_prep (pass table) + flash_sparse_r64<bf16,bf16> (one call, both kernels)",
                         "kernel_ms": kms,
                         "hbm_frac": None if hbm is None else hbm / (kms * 1e-3) / 1e9 / PEAK_GBPS,
                         "note": "gathered K + V (1.105 GB) is L2 traffic; HBM moves the counted bytes"},
@@ -526,7 +526,7 @@ def bench_step(torch, M, steps, warmup):
     the q / k norms folded into the producers): 4096 tokens, q 32 heads and k 8 heads of 128 RMS-normed and rotated,
     v 8 heads, causal GQA attention into bf16 rows with the LSE. Timed two ways on the same inputs: one call of
     mako_attn_fwd_rows (qkv_prep, flash_fwd_r64), and the separate calls (mako_heads three times, then
-    mako_attn_fwd: heads_vec x 3, vt_image, flash_fwd_r64); both give the same bits (checked here, untimed)."""
+    mako_attn_fwd: heads_vec x 3, flash_fwd_r64); both give the same bits (checked here, untimed)."""
     T, D, H, KV = 4096, 128, 32, 8
     gen = torch.Generator(device="cuda").manual_seed(4096)
     xq = torch.randn((T, H * D), generator=gen, device="cuda")

@@ -88,11 +88,16 @@ const char* mako_last_error(void);
  * launch. Replaces TransformerRuntime::attention (src/models/runtime.hpp:90-95; src/models/runtime.cpp:262-273)
  * and the kernels it dispatches, flash_attn_coop_{64,128}_32 and flash_attn_sg_256_16x32_4
  * (src/kernels/ops.metal:106-214, 230-369). dim 64, 128 or 256; heads a multiple of kv_heads. Keys past n_k
- * are masked (their rows need not be zero); fully masked rows give 0 and lse = -inf. Heads of 128 take one of two
- * routes: a few query rows (n_q x heads / kv_heads <= 64, as the reference's decode, attention with n_q = 1)
- * split-K over the keys; more rows, the prefill kernel, after a pass that writes V as f16 V^T tiles. Both keep a
- * workspace per (device, stream), allocated stream-ordered the first time a call needs it (or more of it), so
- * such a call allocates; later calls on the stream reuse it.
+ * are masked (their rows need not be zero); fully masked rows give 0 and lse = -inf. Precision: P (the softmax
+ * numerators) is rounded to the input type for P V, as the reference rounds it to half (src/kernels/ops.metal:329):
+ * f16 inputs f16 P (relative error <= 2^-11 a probability), bf16 inputs bf16 P (<= 2^-8; rows that see fewer than 64
+ * keys get probabilities to ~16 bits). V is used in its own type, bf16 V over its whole range, except at dim 256,
+ * whose kernel converts bf16 V to f16 rounding toward zero (|v| above 65504 saturates, below 6.1e-5 loses bits).
+ * The sums and the LSE add the unrounded f32 exponentials. Heads of 64 and 128 take one of two routes: a few query
+ * rows (n_q x heads / kv_heads <= 64, as the reference's decode, attention with n_q = 1) split-K over the keys,
+ * which keeps a workspace per (device, stream), allocated stream-ordered the first time a call needs it (or more of
+ * it); more rows, the prefill kernel, one launch that allocates nothing. Heads of 256 first write V as f16 V^T tiles
+ * into such a workspace.
  */
 int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
                   const void* k, const void* v, void* o, float* lse, void* stream);
@@ -121,9 +126,10 @@ int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_
  * output goes to o row map[r] (dropped when map[r] < 0). Requires q_pad % 64 == 0, k_pad % 128 == 0,
  * dense0 % 32 == 0 (the reference's checks) and n_cubes * 64 <= k_pad. lse [heads][q_pad] by tile row (may be
  * NULL). Lists shared by a kv head's query heads (sel_heads == kv_heads) in groups of 4, with dense0 % 64 == 0
- * and valid 16-byte aligned, take a route that first writes f16 V^T tile images and a pass table into a workspace
- * per (device, stream), allocated stream-ordered the first time a call needs it (or more of it); other calls
- * allocate nothing.
+ * and valid 16-byte aligned, take a route that first writes a pass table into a workspace per (device, stream),
+ * allocated stream-ordered the first time a call needs it (or more of it); P rounds as in mako_attn_fwd (bf16 P for
+ * bf16 inputs; rows whose first pass is not a full one get tile-0 probabilities to ~16 bits). Other calls allocate
+ * nothing and convert bf16 V and P to f16 (V rounding toward zero: |v| above 65504 saturates).
  */
 int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
                      const void* v, void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
@@ -207,9 +213,10 @@ int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const f
  * mako_attn_fwd reads it except q_pad and k_pad. hq->rows must be a->n_q, hk->rows and hv->rows a->n_k, hq->heads
  * a->heads, hk->heads and hv->heads a->kv_heads, and the three dims equal (64, 128 or 256).
  * Heads of 64, 128 or 256 with 16-byte aligned rows (mako_heads' vector path), values neither normed nor rotated,
- * and more rows than the split-K route takes run as two launches: one that writes the query and key tiles and the
- * f16 V^T images the prefill kernels stage from (the value tiles are never written), then the prefill kernel.
- * Other calls run the four launches above. Allocates as mako_attn_fwd does (a workspace per device and stream).
+ * and more rows than the split-K route takes run as two launches: one that writes the query, key and value tiles
+ * (heads of 256: the f16 V^T images their kernel stages from instead of the value tiles), then the prefill kernel.
+ * Other calls run the four launches above. The tiles live in a workspace per device and stream, allocated
+ * stream-ordered the first time a call needs it (or more of it).
  */
 int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
                        const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq, const float* xk,

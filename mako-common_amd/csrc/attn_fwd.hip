@@ -623,18 +623,18 @@ uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uin
 int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
                        const void* v, void* o, float* lse, hipStream_t s);
 
-// flash_fwd_r64 (attn_fwd64.hip): heads of 128 with 64 rows a wave; 1 launched, 0 when a size does not fit its
-// offsets, -1 when its workspace could not be allocated.
+// flash_fwd_r64 (attn_fwd64.hip): heads of 128 and 64 with 64 rows a wave; 1 launched, 0 when a size does not fit
+// its offsets. flash_fwd_d256: heads of 256; the same, or -1 when its workspace could not be allocated.
 template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                 float* lse, hipStream_t s, const void* vt_ready = nullptr);
+                 float* lse, hipStream_t s);
 template <class T, class TO>
 int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                     float* lse, hipStream_t s, const void* vt_ready = nullptr);
 
 namespace {
 
-// false when flash_fwd_r64's workspace could not be allocated (nothing was launched).
+// false when flash_fwd_d256's workspace could not be allocated (nothing was launched).
 template <class T, class TO>
 bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
 {

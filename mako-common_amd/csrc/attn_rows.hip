@@ -3,12 +3,13 @@
 // :414-418, src/models/h3_vae.cpp:219) as two launches instead of four.
 //
 // qkv_prep, one launch, three kinds of workgroup:
-//   * the V^T tile images that flash_fwd_r64 / flash_fwd_d256 stage from, written straight from the value rows
-//     (vt_rows_tiles): the value tiles are never written, nor read back by vt_image;
+//   * the value tiles as mako_heads writes them (heads_vec_item; flash_fwd_r64 stages V from its rows), or, for heads
+//     of 256, the V^T tile images flash_fwd_d256 stages from, written straight from the value rows (vt_rows_tiles):
+//     the value tiles are then never written, nor read back by vt_image;
 //   * the key tiles, normed and rotated as mako_heads writes them (heads_vec_item);
 //   * the query tiles, the same.
-// Then the attention kernel over those tiles and images (launch_fwd64 / launch_fwd_d256 with the images ready).
-// Every value is rounded as the separate launches round it, so both give the same bits.
+// Then the attention kernel over those tiles (launch_fwd64; launch_fwd_d256 with the images ready). Every value is
+// rounded as the separate launches round it, so both give the same bits.
 //
 // Bound: HBM for qkv_prep (4 bytes read a value, 2 written), then the attention kernel's MFMA bound.
 #include "fwd64_common.hpp"
@@ -24,7 +25,7 @@ bool fwd64_fits(const mako_attn_args* a, uint32_t out_bytes);
 bool d256_fits(const mako_attn_args* a);
 template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                 float* lse, hipStream_t s, const void* vt_ready);
+                 float* lse, hipStream_t s);
 template <class T, class TO>
 int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                     float* lse, hipStream_t s, const void* vt_ready);
@@ -38,15 +39,19 @@ struct VtRowsParams {
     uint32_t nbx;  // workgroups a kv head (256 / D tiles each)
 };
 
-// Workgroups [0, nbv): V^T images (kv head b / nbx); then nbk of key items; then the query items.
+// Workgroups [0, nbv): value tiles (value items; heads of 256: V^T images of kv head b / nbx); then nbk of key
+// items; then the query items.
 template <class T, int D>
-__global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const HeadsParams pk, const VtRowsParams pv,
-                                                uint32_t nbv, uint32_t nbk)
+__global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const HeadsParams pk, const HeadsParams pvt,
+                                                const VtRowsParams pv, uint32_t nbv, uint32_t nbk)
 {
     uint32_t b = blockIdx.x;
     const uint32_t w = threadIdx.x >> 6;
     if (b < nbv) {
-        vt_rows_tiles<T, D>(pv.x, pv.ld, pv.col0, pv.stride, pv.img, pv.n_k, pv.n_vt, b % pv.nbx, b / pv.nbx);
+        if constexpr (D == 256)
+            vt_rows_tiles<T, D>(pv.x, pv.ld, pv.col0, pv.stride, pv.img, pv.n_k, pv.n_vt, b % pv.nbx, b / pv.nbx);
+        else
+            heads_vec_item<T, D / 4>(pvt, (uint64_t)b * kItems + w);
         return;
     }
     b -= nbv;
@@ -60,32 +65,35 @@ __global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const Head
 
 size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// The fused route for heads of D: qkv_prep, then the attention kernel.
+// The fused route for heads of D: qkv_prep, then the attention kernel. pvt: the value producer (its tiles at pvt.y,
+// the V the attention kernel reads); heads of 256 write V^T images instead, in the stream's workspace.
 template <class T, class TO, int D>
-int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParams& pk, const mako_heads_args* hv,
-                const float* xv, void* o, float* lse, hipStream_t s)
+int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParams& pk, const HeadsParams& pvt,
+                const mako_heads_args* hv, const float* xv, void* o, float* lse, hipStream_t s)
 {
     using L = R64<D>;
     const uint32_t n_vt = (t->n_k + 63) / 64, nbx = (n_vt + 256 / D - 1) / (256 / D);
-    const size_t vt_bytes = (size_t)t->kv_heads * n_vt * L::kVTile;
     void* vt = nullptr;
-    if (vt_bytes && !(vt = stream_workspace(kWsVtImages, vt_bytes, s)))
-        return fail(MAKO_EHIP, "attention from rows: no device memory for the V^T images (%zu bytes)", vt_bytes);
+    if constexpr (D == 256) {
+        const size_t vt_bytes = (size_t)t->kv_heads * n_vt * L::kVTile;
+        if (vt_bytes && !(vt = stream_workspace(kWsVtImages, vt_bytes, s)))
+            return fail(MAKO_EHIP, "attention from rows: no device memory for the V^T images (%zu bytes)", vt_bytes);
+    }
     const VtRowsParams pv{xv, static_cast<uint32_t*>(vt), hv->ld, hv->col0, hv->stride, t->n_k, n_vt, nbx};
-    const uint64_t nbv = (uint64_t)nbx * t->kv_heads, nbk = (pk.n_items + kItems - 1) / kItems,
-                   nbq = (pq.n_items + kItems - 1) / kItems;
+    const uint64_t nbv = D == 256 ? (uint64_t)nbx * t->kv_heads : (pvt.n_items + kItems - 1) / kItems,
+                   nbk = (pk.n_items + kItems - 1) / kItems, nbq = (pq.n_items + kItems - 1) / kItems;
     if (nbv + nbk + nbq > 0x7fffffffu)
         return fail(MAKO_EINVAL, "attention from rows: %llu workgroups exceed the grid",
                     (unsigned long long)(nbv + nbk + nbq));
     if (nbv + nbk + nbq)
-        hipLaunchKernelGGL((qkv_prep<T, D>), dim3((uint32_t)(nbv + nbk + nbq)), dim3(256), 0, s, pq, pk, pv,
+        hipLaunchKernelGGL((qkv_prep<T, D>), dim3((uint32_t)(nbv + nbk + nbq)), dim3(256), 0, s, pq, pk, pvt, pv,
                            (uint32_t)nbv, (uint32_t)nbk);
     const float sl2 = t->scale * 1.4426950408889634f;
     int r;
     if constexpr (D == 256)
         r = launch_fwd_d256<T, TO>(t, sl2, pq.y, pk.y, pk.y, o, lse, s, vt);
     else
-        r = launch_fwd64<T, TO, D>(t, sl2, pq.y, pk.y, pk.y, o, lse, s, vt);
+        r = launch_fwd64<T, TO, D>(t, sl2, pq.y, pk.y, pvt.y, o, lse, s);
     if (r <= 0)  // (the route was chosen where the kernel fits and its images are given)
         return fail(MAKO_EHIP, "attention from rows: the attention kernel refused a checked call");
     return check_launch("attention from rows");
@@ -93,11 +101,12 @@ int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParam
 
 template <class T, class TO>
 int launch_rows_dim(uint32_t dim, const mako_attn_args* t, const HeadsParams& pq, const HeadsParams& pk,
-                    const mako_heads_args* hv, const float* xv, void* o, float* lse, hipStream_t s)
+                    const HeadsParams& pvt, const mako_heads_args* hv, const float* xv, void* o, float* lse,
+                    hipStream_t s)
 {
-    return dim == 128  ? launch_rows<T, TO, 128>(t, pq, pk, hv, xv, o, lse, s)
-           : dim == 64 ? launch_rows<T, TO, 64>(t, pq, pk, hv, xv, o, lse, s)
-                       : launch_rows<T, TO, 256>(t, pq, pk, hv, xv, o, lse, s);
+    return dim == 128  ? launch_rows<T, TO, 128>(t, pq, pk, pvt, hv, xv, o, lse, s)
+           : dim == 64 ? launch_rows<T, TO, 64>(t, pq, pk, pvt, hv, xv, o, lse, s)
+                       : launch_rows<T, TO, 256>(t, pq, pk, pvt, hv, xv, o, lse, s);
 }
 
 }  // namespace
@@ -176,9 +185,10 @@ extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args
     }
     const HeadsParams pq = heads_params(&tq, xq, csq, wq, nullptr, qt, true);
     const HeadsParams pk = heads_params(&tk, xk, cs, wk, nullptr, kt, true);
+    const HeadsParams pvt = heads_params(&tv, xv, nullptr, nullptr, nullptr, vt, true);
     if (in == MAKO_BF16)
-        return out == MAKO_F32 ? launch_rows_dim<__bf16, float>(dim, &t, pq, pk, &tv, xv, o, lse, s)
-                               : launch_rows_dim<__bf16, __bf16>(dim, &t, pq, pk, &tv, xv, o, lse, s);
-    return out == MAKO_F32 ? launch_rows_dim<_Float16, float>(dim, &t, pq, pk, &tv, xv, o, lse, s)
-                           : launch_rows_dim<_Float16, _Float16>(dim, &t, pq, pk, &tv, xv, o, lse, s);
+        return out == MAKO_F32 ? launch_rows_dim<__bf16, float>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s)
+                               : launch_rows_dim<__bf16, __bf16>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s);
+    return out == MAKO_F32 ? launch_rows_dim<_Float16, float>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s)
+                           : launch_rows_dim<_Float16, _Float16>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s);
 }

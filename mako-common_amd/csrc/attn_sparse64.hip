@@ -8,16 +8,16 @@
 //
 // The route (mako_attn_sparse takes it when its conditions hold, else flash_sparse8 / flash_sparse): lists shared by
 // a kv head's query heads (sel_heads == kv_heads) in groups of 4, so a workgroup is one 64-row query tile of 4 query
-// heads (one wave a head) over one list, and every K / V^T tile staged in LDS serves all four; dense0 a multiple of
-// 64 and valid 16-byte aligned, so every pass is one 64-key tile of the V^T images.
+// heads (one wave a head) over one list, and every K / V tile staged in LDS serves all four; dense0 a multiple of
+// 64 and valid 16-byte aligned, so every pass is one 64-key tile. K and V are staged from their rows (rows past n_k
+// too, since only valid masks keys; as the reference, masked keys need finite values).
 //
-// Before it, sparse_prep (one launch) writes the V^T tile images of every key row (as vt_image; rows past n_k are
-// copied too, since only valid masks keys) and the pass table: for each (kv head, query tile) list, entry ps =
+// Before it, sparse_prep (one launch) writes the pass table: for each (kv head, query tile) list, entry ps =
 // {first key of pass ps, 0, W0, W1}, -1 (none) past the list. W_g holds the validity of the 32 keys the lanes of half
 // g of a wave hold (bit 16 t + r: key 32 t + 16 (r / 8) + 8 g + r % 8 of the tile): valid and before the pass's end.
 // A causal pass wholly after the tile's rows is none (its keys are all masked anyway; none stages zeros), and the
 // first pass that no bound cuts comes first (it sets the rows' running maximum from all of its keys). The stream
-// reads each tile's entry with scalar loads an iteration ahead: the first key sets the tile's K and V^T sources, and
+// reads each tile's entry with scalar loads an iteration ahead: the first key sets the tile's K and V sources, and
 // a tile whose words are not all ones is masked by them as well as by the causal row limit.
 #include "fwd64_common.hpp"
 
@@ -51,18 +51,10 @@ __device__ __forceinline__ Passes passes_of(const uint16_t* nsel, uint32_t kvh, 
     return r;
 }
 
-// Workgroups [0, img_blocks) write V^T images (vt_image's work, two tiles a workgroup: x = block % per_head tile
-// pairs, kv head block / per_head); the rest write pass-table entries, one a thread.
-template <class T>
-__global__ __launch_bounds__(256) void sparse_prep(const T* v, uint32_t* img, uint32_t k_pad, uint32_t n_vt,
-                                                   uint32_t img_blocks, const SparsePlan p)
+// The pass-table entries, one a thread.
+__global__ __launch_bounds__(256) void sparse_prep(const SparsePlan p)
 {
-    if (blockIdx.x < img_blocks) {
-        const uint32_t per = (n_vt + 1) / 2;
-        vt_image_tiles<T>(v, img, k_pad, k_pad, n_vt, blockIdx.x % per, blockIdx.x / per);
-        return;
-    }
-    const uint32_t idx = (blockIdx.x - img_blocks) * 256 + threadIdx.x;
+    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
     const uint32_t list = idx / p.n_ent, ps = idx % p.n_ent;
     if (list >= p.kv_heads * p.n_qt)
         return;
@@ -125,7 +117,7 @@ __global__ __launch_bounds__(256) void sparse_prep(const T* v, uint32_t* img, ui
 struct Sparse64Params {
     const void* q;
     const void* k;
-    const void* vt;          // V^T tile images: [kv_heads][n_vt][128][64] f16, n_vt = k_pad / 64
+    const void* v;
     void* o;
     float* lse;
     const uint16_t* nsel;
@@ -134,7 +126,7 @@ struct Sparse64Params {
     uint32_t n_q, q_pad, n_k, k_pad, heads, kv_heads, width;
     float scale_log2;
     uint32_t n_cubes, max_sel, dense0, dense1, causal;
-    uint32_t group, n_hg, n_qt, n_vt, n_ent, n_items;
+    uint32_t group, n_hg, n_qt, n_ent, n_items;
 };
 
 template <class T, class TO>
@@ -172,17 +164,16 @@ __global__ __launch_bounds__(256, 1) void flash_sparse_r64(const Sparse64Params 
     const uint32_t vbase = lbase + kNBuf * kKTile;
     uint32_t kr = lbase + c32 * kKRow + 16 * g;
     const uint32_t kr0 = kr;
-    const uint32_t sw = vt_swz(c32);
-    uint32_t vr0 = vbase + c32 * 128 + ((((0 + g) ^ sw) & 7u) << 4);
-    uint32_t vr1 = vbase + c32 * 128 + ((((2 + g) ^ sw) & 7u) << 4);
-    uint32_t vr2 = vbase + c32 * 128 + ((((4 + g) ^ sw) & 7u) << 4);
-    uint32_t vr3 = vbase + c32 * 128 + ((((6 + g) ^ sw) & 7u) << 4);
+    const uint32_t th = (lane >> 4) & 1u, ti = lane & 15u;
+    const uint32_t vrow = vbase + (8 * g + ti / 4) * 256 + 8 * (ti % 4);
+    uint32_t vr0 = vrow + 32 * v_unit(th, ti / 4);
+    uint32_t vr1 = vrow + 32 * v_unit(2 + th, ti / 4);
     auto kd_of = [&](uint32_t i) {
         const uint32_t by = 1024 * i + 16 * lane, row = by / kKRow, ch = by % kKRow / 16;
         return slot_of(row) * 256 + 16 * (ch < 16 ? ch : 0);
     };
     const uint32_t kd0 = kd_of(w), kd1 = kd_of(w + 4), kd2 = kd_of(w + 8), kd3 = kd_of(w + 12), kd4 = kd_of(16);
-    const uint32_t vd = 4096 * w + 16 * lane;
+    const uint32_t vd = 4096 * w + vd_of<128>(lane);
     const uint32_t skw = __builtin_amdgcn_readfirstlane(lbase), skww = __builtin_amdgcn_readfirstlane(lbase + 1024 * w);
     const uint32_t svww = __builtin_amdgcn_readfirstlane(vbase + 4096 * w);
     const uint32_t qo = ((q0 + c32) * 128 + 8 * g) * 2;
@@ -209,8 +200,7 @@ __global__ __launch_bounds__(256, 1) void flash_sparse_r64(const Sparse64Params 
     const u32x4 mrs = rsrc_of(p.map, p.n_q * 4);
     const uint64_t ent = reinterpret_cast<uint64_t>(p.table + ((size_t)kvh * p.n_qt + qt) * p.n_ent);
     const uint64_t kbase = reinterpret_cast<uint64_t>(static_cast<const T*>(p.k) + (size_t)kvh * p.k_pad * 128);
-    const uint64_t vtbase = reinterpret_cast<uint64_t>(static_cast<const unsigned char*>(p.vt) +
-                                                       (size_t)kvh * p.n_vt * 16384);
+    const uint64_t vtbase = reinterpret_cast<uint64_t>(static_cast<const T*>(p.v) + (size_t)kvh * p.k_pad * 128);
     const uint32_t has_lse = __builtin_amdgcn_readfirstlane(p.lse ? 1u : 0u);
     const float c = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, p.scale_log2)));
     const uint32_t s_nt = __builtin_amdgcn_readfirstlane(nt);
@@ -225,7 +215,7 @@ __global__ __launch_bounds__(256, 1) void flash_sparse_r64(const Sparse64Params 
                            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ent);
 
 #define MAKO_SPARSE64_OPERANDS                                                                                  \
-    : [kr] "+v"(kr), [vr0] "+v"(vr0), [vr1] "+v"(vr1), [vr2] "+v"(vr2), [vr3] "+v"(vr3)                          \
+    : [kr] "+v"(kr), [vr0] "+v"(vr0), [vr1] "+v"(vr1)                                                           \
     : [kd0] "v"(kd0), [kd1] "v"(kd1), [kd2] "v"(kd2), [kd3] "v"(kd3), [kd4] "v"(kd4), [vd] "v"(vd),              \
       [lim0] "v"(lim0), [lim1] "v"(lim1), [kr0] "v"(kr0), [qo] "v"(qo), [lo0] "v"(lo0), [lo1] "v"(lo1),          \
       [swp] "v"(swp), [ew] "v"(ew), [er] "v"(er), [mp] "v"(mp), [ocol] "v"(ocol), [mlive] "v"(mlive),            \
@@ -258,38 +248,34 @@ __global__ __launch_bounds__(256, 1) void flash_sparse_r64(const Sparse64Params 
 bool sparse64_fits(const mako_sparse_args* a, const void* valid)
 {
     const uint32_t group = a->heads / a->kv_heads;
-    return MAKO_FWD64_DMA && a->sel_heads == a->kv_heads && group % 4 == 0 && a->dense0 % 64 == 0 &&
+    return a->sel_heads == a->kv_heads && group % 4 == 0 && a->dense0 % 64 == 0 &&
            (reinterpret_cast<uintptr_t>(valid) & 15u) == 0 && (uint64_t)a->q_pad * 256 < (1ull << 31) &&
            (uint64_t)a->heads * a->q_pad * 4 < (1ull << 32) && (uint64_t)a->k_pad * 256 < (1ull << 32);
 }
 
-// sparse_prep then flash_sparse_r64 on stream s, the V^T images and the pass table in the stream's cached
-// workspace. Returns 1 when launched, -1 when the workspace could not be had.
+// sparse_prep then flash_sparse_r64 on stream s, the pass table in the stream's cached workspace. Returns 1 when
+// launched, -1 when the workspace could not be had.
 template <class T, class TO>
 int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                     const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map, float* lse,
                     hipStream_t s)
 {
-    const uint32_t n_vt = a->k_pad / 64, n_qt = (a->n_q + 63) / 64;
+    const uint32_t n_qt = (a->n_q + 63) / 64;
     const uint32_t nd_c = a->dense1 > a->dense0 ? (a->dense1 - a->dense0 + 63) / 64 : 0u;
     const uint32_t nd_l = n_qt > a->n_cubes ? (a->n_k + 63) / 64 : 0u;
     const uint32_t n_ent = std::max(a->max_sel + nd_c, nd_l) + 4;
-    const size_t images = (size_t)a->kv_heads * n_vt * 16384;
     const size_t entries = (size_t)a->kv_heads * n_qt * n_ent;
-    char* ws = static_cast<char*>(stream_workspace(kWsVtImages, images + entries * 16, s));
-    if (!ws)
+    u32x4* table = static_cast<u32x4*>(stream_workspace(kWsVtImages, entries * 16, s));
+    if (!table)
         return -1;
-    u32x4* table = reinterpret_cast<u32x4*>(ws + images);
     const SparsePlan plan{sel, nsel, valid, table, a->kv_heads, n_qt, n_ent, a->n_cubes, a->max_sel, a->dense0,
                           a->dense1, a->n_k, a->causal ? 1u : 0u};
-    const uint32_t img_blocks = (n_vt + 1) / 2 * a->kv_heads;
     const uint32_t plan_blocks = (uint32_t)((entries + 255) / 256);
-    hipLaunchKernelGGL((sparse_prep<T>), dim3(img_blocks + plan_blocks), dim3(256), 0, s, static_cast<const T*>(v),
-                       reinterpret_cast<uint32_t*>(ws), a->k_pad, n_vt, img_blocks, plan);
+    hipLaunchKernelGGL(sparse_prep, dim3(plan_blocks), dim3(256), 0, s, plan);
     const uint32_t n_hg = a->heads / 4;
-    const Sparse64Params p{q, k, ws, o, lse, nsel, map, table, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads,
+    const Sparse64Params p{q, k, v, o, lse, nsel, map, table, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads,
                            a->kv_heads, a->width, scale_log2, a->n_cubes, a->max_sel, a->dense0, a->dense1,
-                           a->causal ? 1u : 0u, a->heads / a->kv_heads, n_hg, n_qt, n_vt, n_ent, n_hg * n_qt};
+                           a->causal ? 1u : 0u, a->heads / a->kv_heads, n_hg, n_qt, n_ent, n_hg * n_qt};
     const uint32_t grid = std::min<uint32_t>(p.n_items, std::max<uint32_t>(1, device_cus()));
     hipLaunchKernelGGL((flash_sparse_r64<T, TO>), dim3(grid), dim3(256), 0, s, p);
     return 1;

@@ -1,6 +1,6 @@
 // Pieces the r64 attention kernels share (attn_fwd64.hip: dense, attn_sparse64.hip: block-sparse): the LDS tile
-// geometry their generated stream assumes (gen_attn_fwd64.py), the K slot order, and the f16 V^T tile images they
-// stage from. Internal linkage: each file gets its own copies.
+// geometry their generated stream assumes (gen_attn_fwd64.py), the K slot order and V unit order, and the f16 V^T
+// tile images flash_fwd_d256 stages from. Internal linkage: each file gets its own copies.
 #pragma once
 
 #include "attn_fwd64_asm.inc"
@@ -16,7 +16,9 @@ template <int D>
 struct R64 {
     static constexpr uint32_t kKRow = 2 * D + 16;                    // LDS bytes of a K row: 2 D + 16 of padding
     static constexpr uint32_t kKTile = 64 * kKRow;                   // a K tile of 64 keys (17 or 9 KiB)
-    static constexpr uint32_t kVTile = D * 64 * 2;                   // a V^T tile: D head dims x 64 keys in f16
+    static constexpr uint32_t kVRow = 2 * D;                         // LDS bytes of a V row (r64 stream)
+    static constexpr uint32_t kVTile = D * 64 * 2;                   // a V tile: 64 rows (r64), or a V^T image
+                                                                     // tile of D head dims x 64 keys in f16 (d256)
     static constexpr uint32_t kNKP = (kKTile / 1024 - 1) / 4;        // K image KiB pieces a wave DMAs: w + 4 m
     static constexpr uint32_t kLdsBytes = kNBuf * (kKTile + kVTile);
 };
@@ -28,6 +30,21 @@ constexpr uint32_t kLdsBytes = R64<128>::kLdsBytes;
 __device__ __forceinline__ uint32_t slot_of(uint32_t row)
 {
     return (row & ~12u) | ((row & 4u) << 1) | ((row & 8u) >> 1);
+}
+
+// Where 32-byte unit u (head dims 16 u .. 16 u + 15) of V row k sits in that row's LDS image (the r64 stream): the
+// unit's low two bits XOR the row's, so the four rows a transpose read's 16-lane group addresses (k % 4 = 0 .. 3, one
+// unit each) cover the 128 bytes of banks once (gen_attn_fwd64.v_unit). Its own inverse for a given row.
+__device__ __forceinline__ uint32_t v_unit(uint32_t u, uint32_t k) { return (u & ~3u) | ((u & 3u) ^ (k & 3u)); }
+
+// The V byte, relative to a 1 KiB V image piece, that lane's LDS slot holds (byte 16 lane of the piece: row r,
+// unit p, half): unit v_unit(p, r) of that row. Pieces start on a multiple of 4 rows, so r % 4 is the tile row's.
+template <int D>
+__device__ __forceinline__ uint32_t vd_of(uint32_t lane)
+{
+    constexpr uint32_t rowb = 2 * D;
+    const uint32_t b = 16 * lane, r = b / rowb, pos = b % rowb;
+    return r * rowb + 32 * v_unit(pos / 32, r) + 16 * ((pos / 16) & 1u);
 }
 
 // XOR swizzle of the 16-byte key chunks in row d of a V^T tile: a bijection on d mod 8 (eight consecutive rows read

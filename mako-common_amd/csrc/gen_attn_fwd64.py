@@ -10,15 +10,21 @@ per-lane addresses and passes them in as operands.
 
 Per wave: rows q0 .. q0 + 63 as two 32-row blocks (rb 0, 1). Scores are S^T = K Q^T on v_mfma_f32_32x32x16 (K from
 LDS as the A operand, Q from the accumulator registers as B), so each lane holds one query row's scores for 16 keys
-of each 32-key half; P V is O^T += V^T P^T with V^T from LDS (f16) and the f16 probabilities as B. Every K / V^T
-operand read from LDS feeds both row blocks' MFMAs.
+of each 32-key half; P V is O^T += V^T P^T with V^T read from V's rows in LDS by transpose reads
+(ds_read_b64_tr_b16) and the probabilities, rounded to the input type (f16 or bf16), as B. Every K / V^T operand
+read from LDS feeds both row blocks' MFMAs.
 
-Keys go by tiles of 64 through four LDS buffers (a padded K image and a V^T image each). Staging is straight
-copies by LDS DMA, 16 bytes a lane, with no conversion: the K image from K as it lies in memory (five 1 KiB pieces a
-wave, each lane loading the 16 bytes its LDS slot holds), the V^T image from the f16 V^T tile images that vt_image
-(attn_fwd64.hip) writes before the kernel runs (four contiguous 1 KiB pieces a wave). Iteration j loads tile j + 3
-into the buffer of tile j - 1. Loads past the workgroup's keys lie outside the buffer descriptors and load zeros.
-(MAKO_FWD64_STAGING=reg stages through registers and three buffers instead: load tile j + 3, write tile j + 2.)
+Keys go by tiles of 64 through four LDS buffers (a K image and a V image each). Staging is straight copies by LDS DMA,
+16 bytes a lane, with no conversion, from K and V as they lie in memory: the K image (five 1 KiB pieces a wave) has
+rows padded to an odd number of 16-byte chunks, the V image (four 1 KiB pieces a wave) keeps 2 d-byte rows with
+their 32-byte units permuted by row (v_unit), each lane loading the 16 bytes its LDS slot holds. Iteration j loads
+tile j + 3 into the buffer of tile j - 1. Loads past the workgroup's keys lie outside the buffer descriptors and load
+zeros.
+
+ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane i receives element i % 4 of the 8 bytes that lanes
+i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4 address, in that order (checked on the GPU). So when lanes 4 y .. 4 y + 3
+of a group address the 16 head dims of one key row (8 bytes each), lane i receives head dim i of four keys: a column
+of V, which is what the MFMA's A operand holds (eight keys of one head dim a lane, two reads).
 
 Iteration j, with S_cur holding tile j's exponentials (f32, made against the running maximum known when they were
 made) and S_nxt receiving tile j + 1's scores:
@@ -39,7 +45,7 @@ The loop is unrolled twice so that S_cur and S_nxt swap registers statically.
 
 Register map: a0..a127 the outputs O[rb][db] (32 head dims a block), a128..a191 Q[rb][kk], a192..a223 the LDS
 operand ring; v0..v127 the two score tiles, v128..v159 P[rb], v160..v183 softmax state and temporaries,
-v184..v219 the staged tile; s60..s99 scalars. The C++ operands sit in the registers the clobber list leaves free.
+s60..s99 scalars. The C++ operands sit in the registers the clobber list leaves free.
 
 Run: python3 gen_attn_fwd64.py  (writes attn_fwd64_asm.inc beside this file; the Makefile reruns it when it changes)
 """
@@ -47,8 +53,7 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-STAGING = os.environ.get("MAKO_FWD64_STAGING", "dma")   # "dma": LDS DMA, "reg": through the staging registers
-NBUF = 4 if STAGING == "dma" else 3   # LDS tile buffers
+NBUF = 4                # LDS tile buffers
 RING = 8                # LDS operand ring slots
 AHEAD = 6               # operand reads in flight ahead of their MFMAs (a slot is refilled two fragments after its
                         # last MFMA was issued)
@@ -61,13 +66,15 @@ def set_dim(d):
             are conflict-free);
     K_TILE  the padded K image of a 64-key tile (17 or 9 pieces of 1 KiB: a wave DMAs pieces w + 4 m, m < NKP, and
             every wave the last, piece 4 NKP);
-    V_TILE  the f16 V^T image of a tile, d rows of 64 keys (a wave DMAs NVP KiB of it);
+    V_ROW   LDS bytes of a V row: 2 d, its 32-byte units permuted by row (v_unit);
+    V_TILE  the V image of a tile, 64 rows (a wave DMAs NVP KiB of it);
     NKK, NDB  16-wide head-dimension steps of Q K^T, 32-wide output blocks;
     BAR_AT  phase PV's fragment (of 4 NDB) after whose MFMAs the tile's barrier sits."""
-    global D, K_ROW, K_TILE, V_TILE, NKK, NDB, NKP, NVP, DMA_PER_TILE, BAR_AT
+    global D, K_ROW, V_ROW, K_TILE, V_TILE, NKK, NDB, NKP, NVP, DMA_PER_TILE, BAR_AT
     assert d in (64, 128)
     D = d
     K_ROW = 2 * d + 16
+    V_ROW = 2 * d
     K_TILE = 64 * K_ROW
     V_TILE = d * 64 * 2
     NKK, NDB = d // 16, d // 32
@@ -109,6 +116,12 @@ def RINGR(s):
     return f"a[{192 + 4 * s}:{192 + 4 * s + 3}]"
 
 
+def ring_fmt(text, s):
+    """An operand read's text with ring slot s filled in: {ring} the slot, {lo} / {hi} its halves."""
+    b = 192 + 4 * s
+    return text.format(ring=RINGR(s), lo=f"a[{b}:{b + 1}]", hi=f"a[{b + 2}:{b + 3}]")
+
+
 NEGMU = ("v160", "v161")   # -(running maximum) of the lane's row, 0 while it is -inf
 LSUM = ("v162", "v163")    # row sum over this lane's keys
 MAXV = ("v164", "v165")    # running maximum (base 2), -inf until a key was seen
@@ -131,7 +144,7 @@ SMASK = ("s[88:89]", "s[90:91]", "s[92:93]", "s[94:95]")  # lane masks of the ke
 SROT = {"k": "s96", "v": "s97", "wk": "s98", "wv": "s99"}   # rotation increments, by role
 SKW = "s66"       # DMA: LDS address of the K image of buffer SBW
 SKWW = "s67"      # DMA: SKW + 1 KiB x (wave index), this wave's first K piece
-SVWW = "s84"      # DMA: LDS address of this wave's 4 KiB of the V^T image of buffer SBW
+SVWW = "s84"      # DMA: LDS address of this wave's 4 KiB of the V image of buffer SBW
 SM0 = "s87"       # DMA: the compiler's M0, restored at the end
 
 # The block-sparse stream (body(..., sparse=True)): each tile's first key, and the validity of its keys, come from the
@@ -145,19 +158,11 @@ SEW_LO, SEW_HI = "s94", "s95"   # which the sparse stream's masks leave alone
 MAPV = "v184"           # the output row map[q0 + lane] (-1: dropped)
 
 
-def KSTG(m):      # staged K piece m (0..3: pieces w + 4 m; 4: piece 16)
-    return f"v[{184 + 4 * m}:{187 + 4 * m}]"
-
-
-def VSTG(i):      # staged V^T piece i of the wave's 4 KiB
-    return f"v[{204 + 4 * i}:{207 + 4 * i}]"
-
-
 def quad(r):
     return f"s[{r[0][1:]}:{r[3][1:]}]"
 
 
-CLOBBER_V = 184 if STAGING == "dma" else 220
+CLOBBER_V = 184
 CLOBBER_A = 224
 CLOBBER_S = (60, 100)
 CLOBBER_V_SPARSE = 185     # + MAPV
@@ -193,40 +198,7 @@ def rotate(sidx, role, regs, stride):
 
 
 KREGS = ["%[kr]"]
-VREGS = [f"%[vr{i}]" for i in range(4)]
-
-
-def stage_loads(kregs=KSTG, vregs=VSTG):
-    """Loads the next tile into the staging registers, then moves the sources on by a tile. K: the wave's pieces w,
-    w + 4, w + 8, w + 12 of the 17 KiB padded image (%[kd*]: the byte of K a lane's LDS slot holds) and piece 16
-    (every wave loads it; they write the same bytes to the same place). V^T: the wave's 4 KiB of the tile image, as
-    four 1 KiB loads. Record counts shrink by a tile and stop at zero, so tiles past the keys load zeros."""
-    ops = [f"buffer_load_dwordx4 {kregs(m)}, %[kd{m}], {quad(KRS)}, 0 offen" for m in range(5)]
-    ops += [f"buffer_load_dwordx4 {vregs(i)}, %[vd], {quad(VRS)}, 0 offen offset:{1024 * i}" for i in range(4)]
-    for r in (KRS, VRS):
-        ops += [f"s_add_u32 {r[0]}, {r[0]}, 0x4000", f"s_addc_u32 {r[1]}, {r[1]}, 0",
-                f"s_sub_u32 {r[2]}, {r[2]}, 0x4000", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
-    return ops
-
-
-WKREGS = ["%[kwa]", "%[kwb]"]
-WVREGS = ["%[vwa]"]
-
-
-def stage_writes(kregs=KSTG, vregs=VSTG):
-    """The staged tile into LDS buffer SBW (1 KiB a write, conflict-free), then the write addresses move to the next
-    buffer. %[kwa]: this wave's first K piece plus 16 bytes a lane, %[kwb]: piece 16; %[vwa]: its V^T 4 KiB."""
-    ops = [f"ds_write_b128 %[kwa], {kregs(m)} offset:{4096 * m}" for m in range(4)]
-    ops.append(f"ds_write_b128 %[kwb], {kregs(4)}")
-    ops += [f"ds_write_b128 %[vwa], {vregs(i)} offset:{1024 * i}" for i in range(4)]
-    wk, wv = SROT["wk"], SROT["wv"]
-    ops += [f"s_cmp_eq_u32 {SBW}, {NBUF - 1}",
-            f"s_cselect_b32 {wk}, {(-NBUF * K_TILE) & 0xFFFFFFFF:#x}, 0",
-            f"s_cselect_b32 {wv}, {(-NBUF * V_TILE) & 0xFFFFFFFF:#x}, 0",
-            f"s_add_u32 {wk}, {wk}, {K_TILE:#x}", f"s_add_u32 {wv}, {wv}, {V_TILE:#x}"]
-    ops += [f"v_add_u32 {r}, {wk}, {r}" for r in WKREGS] + [f"v_add_u32 {r}, {wv}, {r}" for r in WVREGS]
-    ops += [f"s_add_u32 {SBW}, {SBW}, 1", f"s_cmp_eq_u32 {SBW}, {NBUF}", f"s_cselect_b32 {SBW}, 0, {SBW}"]
-    return ops
+VREGS = ["%[vr0]", "%[vr1]"]
 
 
 def dma_issue():
@@ -238,11 +210,11 @@ def dma_issue():
 def dma_groups():
     """LDS DMA loads of the next tile into buffer SBW (lane l of a load writes 16 bytes at M0 + offset + 16 l), then
     the sources move on by a tile and the destinations to the next buffer. K: pieces w, w + 4, w + 8, w + 12 of the
-    17 KiB image at M0 = their LDS address, and piece 16 (every wave; the same bytes to the same place). V^T: the
-    wave's 4 KiB of the tile image, as four 1 KiB loads whose offset moves source and destination alike. A write of
-    M0 is read by an LDS load after one wait state. Record counts shrink by a tile and stop at zero. Sparse: the
-    sources are set from SD, the tile's first key (K rows and V^T images are both 256 bytes a key), one tile long, or
-    empty when SD is -1.
+    17 KiB image at M0 = their LDS address, and piece 16 (every wave; the same bytes to the same place). V: the
+    wave's 4 KiB of the tile image (rows 16 w .. 16 w + 15), as four 1 KiB loads whose offset moves source and
+    destination alike (%[vd]: the byte of V a lane's LDS slot holds, relative to the piece). A write of M0 is read by
+    an LDS load after one wait state. Record counts shrink by a tile and stop at zero. Sparse: the sources are set
+    from SD, the tile's first key (K and V rows are both 256 bytes a key), one tile long, or empty when SD is -1.
     Returns (groups, tail): a group per load (with the M0 write it needs), and the scalar work after the last load.
     A phase spreads the groups evenly between its MFMAs: a burst of these loads holds up the wave's vector and matrix
     instructions behind it (a timing probe of the plain iteration on one CU: 2654 cycles a tile with the loads at
@@ -265,7 +237,7 @@ def dma_groups():
                       [f"buffer_load_dwordx4 %[vd], {quad(VRS)}, 0 offen offset:{1024 * i} lds"])
     groups[0] = pre + groups[0]
     ops = []
-    step = 128 * D   # K rows and V^T images: 2 d bytes a key, 64 keys a tile
+    step = 128 * D   # K and V rows: 2 d bytes a key, 64 keys a tile
     for r in (KRS, VRS) if not SPARSE else ():
         ops += [f"s_add_u32 {r[0]}, {r[0]}, {step:#x}", f"s_addc_u32 {r[1]}, {r[1]}, 0",
                 f"s_sub_u32 {r[2]}, {r[2]}, {step:#x}", f"s_cselect_b32 {r[2]}, 0, {r[2]}"]
@@ -280,24 +252,20 @@ def dma_groups():
 
 
 def staging():
-    """A tile's staging in the loop. DMA: load tile j + 3 (waited for before barrier j + 2). Registers: wait for the
-    staged tile j + 2 (loaded an iteration ago), write it, load tile j + 3."""
-    if STAGING == "dma":
-        return dma_issue()
-    return ["s_waitcnt vmcnt(0)"] + stage_writes() + stage_loads()
+    """A tile's staging in the loop: load tile j + 3 (waited for before barrier j + 2)."""
+    return dma_issue()
 
 
 def barrier():
-    """The wave's staging of the tile before the last is in LDS and its LDS writes and reads are done (the buffer it
-    read last is written after the barrier); then the barrier."""
-    if STAGING == "dma":
-        return [f"s_waitcnt vmcnt({DMA_PER_TILE}) lgkmcnt(0)", "s_barrier"]
-    return ["s_waitcnt lgkmcnt(0)", "s_barrier"]
+    """The wave's staging of the tile before the last is in LDS and its LDS reads are done (the buffer it read last
+    is written after the barrier); then the barrier."""
+    return [f"s_waitcnt vmcnt({DMA_PER_TILE}) lgkmcnt(0)", "s_barrier"]
 
 
 def k_reads(addr):
-    """LDS reads of K fragment f = (kk, t) = (f // 2, f % 2): rows 32 t + c32 (slot order), head dims 16 kk + 8 g."""
-    return [f"ds_read_b128 {{ring}}, {addr} offset:{32 * K_ROW * (f % 2) + 32 * (f // 2)}" for f in range(2 * NKK)]
+    """LDS reads of K fragment f = (kk, t) = (f // 2, f % 2): rows 32 t + c32 (slot order), head dims 16 kk + 8 g.
+    Each fragment's reads are a list of instruction texts ({ring} the ring slot, {lo} / {hi} its halves)."""
+    return [[f"ds_read_b128 {{ring}}, {addr} offset:{32 * K_ROW * (f % 2) + 32 * (f // 2)}"] for f in range(2 * NKK)]
 
 
 def qk_mfmas(dtype, sbuf):
@@ -311,17 +279,35 @@ def qk_mfmas(dtype, sbuf):
     return out
 
 
+def v_unit(u, k):
+    """Where 32-byte unit u (head dims 16 u .. 16 u + 15) of V row k sits in the row's LDS image: the unit's low two
+    bits XOR the row's. The four rows a transpose read's 16-lane group addresses (k % 4 = 0 .. 3, one unit each) then
+    cover the 128 bytes of banks once."""
+    return (u & ~3) | ((u & 3) ^ (k & 3))
+
+
 def v_reads():
-    """LDS reads of V^T fragment f = (cc, db) = (f // 4, f % 4): head dims 32 db + c32, keys 16 cc + 8 g .. + 7."""
-    return [f"ds_read_b128 {{ring}}, %[vr{f // NDB}] offset:{4096 * (f % NDB)}" for f in range(4 * NDB)]
+    """LDS transpose reads of V^T fragment f = (cc, db) = (f // NDB, f % NDB), the A operand of O^T += V^T P^T: lane
+    l = 32 g + 16 h + i receives head dim 32 db + 16 h + i of keys 16 cc + 8 g .. + 7, in two ds_read_b64_tr_b16 of
+    four keys ({lo}: keys + 0 .. 3, {hi}: + 4 .. 7). In a read, lane i of the group addresses key 16 cc + 8 g + 4 r +
+    i / 4, head dims 16 (2 db + h) + 4 (i % 4) .. + 3: unit v_unit(2 db + h, i / 4) of that row. %[vr0] holds the
+    lane's address for even db (unit h ^ (i / 4)), %[vr1] for odd db (unit (2 + h) ^ (i / 4)); db / 2 adds 128
+    bytes, cc and r add whole rows."""
+    out = []
+    for f in range(4 * NDB):
+        cc, db = f // NDB, f % NDB
+        base = 16 * cc * V_ROW + 128 * (db >> 1)
+        out.append([f"ds_read_b64_tr_b16 {{{half}}}, %[vr{db & 1}] offset:{base + 4 * r * V_ROW}"
+                    for r, half in ((0, "lo"), (1, "hi"))])
+    return out
 
 
-def pv_mfmas():
+def pv_mfmas(dtype):
     out = []
     for f in range(4 * NDB):
         cc, db = f // NDB, f % NDB
         for rb in range(2):
-            out.append((f, f"v_mfma_f32_32x32x16_f16 {O(rb, db)}, {{ring}}, {P(rb, cc)}, {O(rb, db)}"))
+            out.append((f, f"v_mfma_f32_32x32x16_{dtype} {O(rb, db)}, {{ring}}, {P(rb, cc)}, {O(rb, db)}"))
     return out
 
 
@@ -335,13 +321,14 @@ def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=(), d
     MFMA i * n / len(groups) (after that MFMA's share of `valu`), the tail after the last MFMA's.
     Returns how many of the next phase's reads went out.
     LDS returns in order, so the wait for a read is lgkmcnt(LDS instructions issued after it); LDS instructions inside
-    `valu` are counted too."""
-    issued = [(kind, f) for f in range(pre)]
+    `valu` are counted too. A fragment's reads may be several instructions; its MFMAs wait for the last."""
+    issued = [(kind, f) for f in range(pre) for _ in reads[f]]
     nfr = len(reads)
 
-    def issue(k, f, text):
-        e(text.format(ring=RINGR(f % RING)))
-        issued.append((k, f))
+    def issue(k, f, texts):
+        for text in texts:
+            e(ring_fmt(text, f % RING))
+            issued.append((k, f))
 
     after = {}
     for f in range(max(pre, AHEAD), nfr):
@@ -372,9 +359,9 @@ def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=(), d
     vi = 0
     for i, (f, text) in enumerate(mfmas):
         if i == 0 or mfmas[i - 1][0] != f:
-            pos = issued.index((kind, f))
+            pos = len(issued) - 1 - issued[::-1].index((kind, f))
             e(f"s_waitcnt lgkmcnt({min(len(issued) - 1 - pos, 15)})")
-        e(text.format(ring=RINGR(f % RING)))
+        e(ring_fmt(text, f % RING))
         if i + 1 == n or mfmas[i + 1][0] != f:
             if gate_at == f:
                 for op in gate:
@@ -459,16 +446,18 @@ def exps(sbuf):
     return ops
 
 
-def pack_and_sum(sbuf):
-    """P[rb] = f16 pairs of tile S(sbuf)'s exponentials, and the sum a row block of the f32 exponentials (as the
-    reference sums them, ops.metal:326-331; P V multiplies their f16 roundings) into TMP[0] (rb 0) and TMP[4] (rb 1):
-    four chains of adds a row block, interleaved, so no add waits on the one before it."""
+def pack_and_sum(sbuf, dtype):
+    """P[rb] = pairs of tile S(sbuf)'s exponentials rounded to the input type dtype (to nearest even), and the sum a
+    row block of the f32 exponentials (as the reference sums them, ops.metal:326-331; P V multiplies their roundings)
+    into TMP[0] (rb 0) and TMP[4] (rb 1): four chains of adds a row block, interleaved, so no add waits on the one
+    before it."""
+    cvt = f"v_cvt_pk_{dtype}_f32"
     ops = []
     for rb in range(2):
         for cc in range(4):
             t, r0 = cc // 2, 8 * (cc % 2)
             for i in range(4):
-                ops.append(f"v_cvt_pk_f16_f32 {P(rb, cc, i)}, {S(sbuf, rb, t, r0 + 2 * i)}, "
+                ops.append(f"{cvt} {P(rb, cc, i)}, {S(sbuf, rb, t, r0 + 2 * i)}, "
                            f"{S(sbuf, rb, t, r0 + 2 * i + 1)}")
     vals = {rb: [S(sbuf, rb, t, r) for t in range(2) for r in range(16)] for rb in range(2)}
     for k in range(1, 8):       # chain c of row block rb sums values c, c + 4, c + 8, ...
@@ -536,8 +525,56 @@ def exact_tile(e, dtype, sbuf, kaddr, j0, first=False, w=None):
             e(f"v_accvgpr_read_b32 {tv}, {a}")
             e(f"v_mul_f32 {tv}, {tv}, {f}")
             e(f"v_accvgpr_write_b32 {a}, {tv}")
-    for op in exps(sbuf) + pack_and_sum(sbuf):
+    for op in exps(sbuf) + pack_and_sum(sbuf, dtype):
         e(op)
+
+
+def low_part_pass(e):
+    """bf16 inputs: tile 0's P V once more with the parts of the probabilities that bf16 P drops, when some row of
+    the wave may see few keys. P V multiplies probabilities rounded to bf16 (8 significant bits, relative error up to
+    2^-8); a row that sees many keys averages those roundings away, but a row that sees a handful does not (a few keys of comparable weight whose
+    values cancel leave errors of ~2^-9 |v| on a small output). In dense attention a row sees a prefix of the keys, so
+    a row that sees fewer than 64 sees only tile 0's: adding V^T(0) P_lo^T, P_lo = bf16(p - P) of tile 0's f32
+    exponentials p, gives those rows probabilities to ~16 bits. Taken when the wave's first row (the fewest keys: the
+    row limit grows with the row) sees fewer than 64 keys; sparse: when the stream's tile 0 is not a pass all of whose
+    64 keys every row sees (the order puts such a pass first when the list has one). Runs before iteration 0, in
+    S(1)'s registers (free until its phase QK), from buffer 0 (tile 0's V)."""
+    skip = lbl("L_nolo")
+    if SPARSE:
+        t = SROT["k"]
+        e(f"s_and_b32 {t}, s78, s79")
+        e(f"s_cmp_eq_u32 {t}, -1")
+        e(f"s_cbranch_scc0 {lbl('L_lo')}")
+        e(f"s_add_u32 {t}, s76, 64")
+        e(f"s_cmp_le_u32 {t}, %[lmin]")
+        e(f"s_cbranch_scc1 {skip}")
+        e.label("L_lo")
+    else:
+        e("s_cmp_ge_u32 %[lmin], 64")
+        e(f"s_cbranch_scc1 {skip}")
+    lo = {}
+    ops_a, ops_b, ops_c = [], [], []
+    k = 0
+    for rb in range(2):
+        for cc in range(4):
+            t, r0 = cc // 2, 8 * (cc % 2)
+            for i in range(4):
+                hi, lr, tr = P(rb, cc, i), f"v{64 + 16 * rb + 4 * cc + i}", f"v{96 + k}"
+                a, b = S(0, rb, t, r0 + 2 * i), S(0, rb, t, r0 + 2 * i + 1)
+                ops_a += [f"v_lshlrev_b32 {lr}, 16, {hi}", f"v_and_b32 {tr}, 0xffff0000, {hi}"]
+                ops_b += [f"v_sub_f32 {lr}, {a}, {lr}", f"v_sub_f32 {tr}, {b}, {tr}"]
+                ops_c.append(f"v_cvt_pk_bf16_f32 {lr}, {lr}, {tr}")
+                k += 1
+    for op in ops_a + ops_b + ops_c:
+        e(op)
+    mfmas = []
+    for f in range(4 * NDB):
+        cc, db = f // NDB, f % NDB
+        for rb in range(2):
+            plo = f"v[{64 + 16 * rb + 4 * cc}:{64 + 16 * rb + 4 * cc + 3}]"
+            mfmas.append((f, f"v_mfma_f32_32x32x16_bf16 {O(rb, db)}, {{ring}}, {plo}, {O(rb, db)}"))
+    interleave(e, v_reads(), mfmas, [])
+    e.label("L_nolo")
 
 
 def epilogue(e, out_dtype):
@@ -650,7 +687,7 @@ def body(in_dtype, out_dtype, sparse=False, d=128):
     """The stream for one item (a workgroup's rows) at head width d; sparse: the block-sparse one (tiles from the
     pass table, heads of 128)."""
     global SPARSE
-    assert d == 128 or (not sparse and STAGING == "dma")
+    assert d == 128 or not sparse
     SPARSE = sparse
     set_dim(d)
     try:
@@ -663,7 +700,6 @@ def body(in_dtype, out_dtype, sparse=False, d=128):
 def body_of(in_dtype, out_dtype):
     e = Emit()
     if SPARSE:
-        assert STAGING == "dma", "the sparse stream stages by LDS DMA"
         # the pass table's first entries: the first keys of tiles 0-3, entry 1 (iteration 0 masks tile 1), entry 0
         # (tile 0's exact path, in ST); and the row map
         for i, r in enumerate(("s88", "s89", "s90", "s91")):
@@ -691,48 +727,25 @@ def body_of(in_dtype, out_dtype):
     for rb in range(2):
         for kk in range(NKK):
             e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen offset:{32 * kk}")
-    if STAGING == "dma":
-        # M0 is the compiler's: kept in SM0 while the stream uses it, restored at the end
-        e(f"s_mov_b32 {SM0}, m0")
-        # tiles 0, 1, 2 into buffers 0, 1, 2; outputs zeroed meanwhile; the barrier waits for tiles 0 and 1
-        e(f"s_mov_b32 {SKW}, %[skw]")
-        e(f"s_mov_b32 {SKWW}, %[skww]")
-        e(f"s_mov_b32 {SVWW}, %[svww]")
+    # M0 is the compiler's: kept in SM0 while the stream uses it, restored at the end
+    e(f"s_mov_b32 {SM0}, m0")
+    # tiles 0, 1, 2 into buffers 0, 1, 2; outputs zeroed meanwhile; the barrier waits for tiles 0 and 1
+    e(f"s_mov_b32 {SKW}, %[skw]")
+    e(f"s_mov_b32 {SKWW}, %[skww]")
+    e(f"s_mov_b32 {SVWW}, %[svww]")
+    if SPARSE:
+        e("s_waitcnt lgkmcnt(0)")
+    for i in range(3):
         if SPARSE:
-            e("s_waitcnt lgkmcnt(0)")
-        for i in range(3):
-            if SPARSE:
-                e(f"s_mov_b32 {SD}, s{88 + i}")
-            for op in dma_issue():
-                e(op)
-        if SPARSE:
-            e(f"s_mov_b32 {SD}, s91")
-        for i in range(32 * NDB):
-            e(f"v_accvgpr_write_b32 a{i}, 0")
-    else:
-        # tiles 0 and 1 into the (still free) score registers, tile 2 into the staging registers; outputs zeroed
-        # meanwhile; tiles 0 and 1 written to buffers 0, 1
-        early_staging(e)
+            e(f"s_mov_b32 {SD}, s{88 + i}")
+        for op in dma_issue():
+            e(op)
+    if SPARSE:
+        e(f"s_mov_b32 {SD}, s91")
+    for i in range(32 * NDB):
+        e(f"v_accvgpr_write_b32 a{i}, 0")
     body_rest(e, in_dtype, out_dtype)
     return e.out
-
-
-def early_staging(e):
-
-    def early(t):
-        return (lambda m: f"v[{36 * t + 4 * m}:{36 * t + 4 * m + 3}]",
-                lambda i: f"v[{36 * t + 20 + 4 * i}:{36 * t + 23 + 4 * i}]")
-    for t in range(2):
-        for op in stage_loads(*early(t)):
-            e(op)
-    for op in stage_loads():
-        e(op)
-    for i in range(128):
-        e(f"v_accvgpr_write_b32 a{i}, 0")
-    e("s_waitcnt vmcnt(9)")
-    for t in range(2):
-        for op in stage_writes(*early(t)):
-            e(op)
 
 
 def body_rest(e, in_dtype, out_dtype):
@@ -751,6 +764,8 @@ def body_rest(e, in_dtype, out_dtype):
         exact_tile(e, in_dtype, 0, "%[kr]", SJX, first=True)
     e(f"v_add_f32 {LSUM[0]}, {LSUM[0]}, {TMP[0]}")
     e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
+    if in_dtype == "bf16":
+        low_part_pass(e)
 
     def iteration(par, variant, masked_next=False):
         """Iteration j with S_cur = S(par), S_nxt = S(1 - par). variant: 'plain' (tile j + 1 fully seen by the
@@ -762,10 +777,10 @@ def body_rest(e, in_dtype, out_dtype):
         cur, nxt = par, 1 - par
         tag = f"{variant}{par}"
         # the staging of tile j + 3: DMA loads spread between phase QK's MFMAs (register staging: in the list)
-        dma = dma_groups() if STAGING == "dma" and variant != "last" else None
-        valu = [] if dma else staging()
+        dma = dma_groups() if variant != "last" else None
+        valu = []
         if variant != "first":
-            valu += pack_and_sum(cur)
+            valu += pack_and_sum(cur, in_dtype)
         n_v = 0
         if variant != "last":
             n_v = phase(e, "K", k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu, pre=0 if variant == "first" else N_K_AHEAD,
@@ -796,7 +811,7 @@ def body_rest(e, in_dtype, out_dtype):
             valu = ["s_nop 7", "s_nop 7"] + m[:3] + loads + m[3:] + exps(nxt)
         elif SPARSE:
             valu = entry_loads()
-        n_k = phase(e, "V", v_reads(), pv_mfmas(), valu, pre=n_v, nxt=None if variant == "last" else ("K", k_reads("%[kr]")),
+        n_k = phase(e, "V", v_reads(), pv_mfmas(in_dtype), valu, pre=n_v, nxt=None if variant == "last" else ("K", k_reads("%[kr]")),
                     gate_at=BAR_AT, gate=barrier())
         assert variant == "last" or n_k == N_K_AHEAD
         for op in rotate(SBV, "v", VREGS, V_TILE):
@@ -824,7 +839,8 @@ def body_rest(e, in_dtype, out_dtype):
         # the V^T reads phase QK sent ahead (their ring slots were reused here), again, as the last LDS instructions
         reads = v_reads()
         for f in range(exact_v[tag]):
-            e(reads[f].format(ring=RINGR(f % RING)))
+            for text in reads[f]:
+                e(ring_fmt(text, f % RING))
         e(f"s_branch {lbl('L_back_' + tag)}")
 
     def dispatch(par, first=False):
@@ -872,7 +888,7 @@ def body_rest(e, in_dtype, out_dtype):
     e.label("L_last_first")
     for op in staging():
         e(op)
-    phase(e, "V", v_reads(), pv_mfmas(), [], gate_at=BAR_AT, gate=barrier())
+    phase(e, "V", v_reads(), pv_mfmas(in_dtype), [], gate_at=BAR_AT, gate=barrier())
     for op in rotate(SBV, "v", VREGS, V_TILE):
         e(op)
     e(f"s_add_u32 {SJ}, {SJ}, 1")
@@ -901,8 +917,7 @@ def body_rest(e, in_dtype, out_dtype):
     e(f"s_branch {lbl('L_tail')}")
     e.label("L_epi")
     epilogue(e, out_dtype)
-    if STAGING == "dma":
-        e(f"s_mov_b32 m0, {SM0}")
+    e(f"s_mov_b32 m0, {SM0}")
 
 
 def clobbers(sparse=False):
@@ -922,12 +937,13 @@ def check_registers(lines, sparse=False):
             limit = {"v": (0, CLOBBER_V_SPARSE if sparse else CLOBBER_V), "a": (0, CLOBBER_A),
                      "s": CLOBBER_S_SPARSE if sparse else CLOBBER_S}[kind]
             assert limit[0] <= bot and top < limit[1], f"{kind}{bot}..{top} outside the reserved registers: {ln}"
+            assert one or bot % 2 == 0, f"{kind}[{bot}:{top}]: a register tuple must start on an even register: {ln}"
 
 
 def main():
     out = ["// Generated by gen_attn_fwd64.py (the instruction stream of flash_fwd_r64; the design is described there).",
            "// Do not edit: change the generator and run it.", "#pragma once", ""]
-    kinds = [(False, 128), (True, 128), (False, 64)] if STAGING == "dma" else [(False, 128)]
+    kinds = [(False, 128), (True, 128), (False, 64)]
     for sparse, d in kinds:
         for ind in ("bf16", "f16"):
             for outd in ("f32", ind):
@@ -942,7 +958,6 @@ def main():
                 out.append("")
     out.append(f"#define MAKO_FWD64_CLOBBERS {clobbers()}")
     out.append(f"#define MAKO_SPARSE64_CLOBBERS {clobbers(True)}")
-    out.append(f"#define MAKO_FWD64_DMA {1 if STAGING == 'dma' else 0}")
     out.append(f"#define MAKO_FWD64_NBUF {NBUF}")
     out.append("")
     with open(os.path.join(HERE, "attn_fwd64_asm.inc"), "w") as f:

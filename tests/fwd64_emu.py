@@ -442,6 +442,28 @@ class Emu:
                     dst[i + q] = np.array([self.lds[x + 4 * q: x + 4 * q + 4].view(np.uint32)[0]
                                            if 0 <= x + 4 * q + 4 <= len(self.lds) else 0 for x in addr], np.uint32)
             w.lq.append(land)
+        elif mn == 'ds_read_b64_tr_b16':
+            # transpose read (gfx950, lane layout checked on the GPU): in each group of 16 lanes, lane i receives
+            # element i % 4 of the 8 bytes lanes i // 4, 4 + i // 4, 8 + i // 4 and 12 + i // 4 address, in that order
+            kind, i, n, _ = parse_reg(A[0])
+            addr = self.rd(w, A[1]).astype(np.int64) + op.mods.get('offset', 0)
+            self.bank(op, addr, 8)
+            dst = w.v if kind == 'v' else w.a
+            for q in range(2):
+                dst[i + q] = 0xFFFFFFFF
+
+            def land(dst=dst, i=i, addr=addr):
+                chunks = np.zeros((64, 4), np.uint32)
+                for l in range(64):
+                    x = int(addr[l])
+                    if 0 <= x and x + 8 <= len(self.lds):
+                        chunks[l] = self.lds[x:x + 8].view(np.uint16)
+                lane = np.arange(64)
+                grp, li = lane & ~15, lane & 15
+                el = np.stack([chunks[grp + 4 * y + li // 4, li % 4] for y in range(4)], axis=1)
+                dst[i] = el[:, 0] | (el[:, 1] << 16)
+                dst[i + 1] = el[:, 2] | (el[:, 3] << 16)
+            w.lq.append(land)
         elif mn in ('ds_write_b128', 'ds_write_b64'):
             kind, i, n, _ = parse_reg(A[1])
             addr = self.rd(w, A[0]).astype(np.int64) + op.mods.get('offset', 0)

@@ -12,7 +12,7 @@ import fwd64_emu as E  # noqa: E402
 import gen_attn_fwd64 as G  # noqa: E402
 import oracle as O  # noqa: E402
 
-VOPS = ['kr', 'vr0', 'vr1', 'vr2', 'vr3'] + ([] if G.STAGING == 'dma' else ['kwa', 'kwb', 'vwa']) + [
+VOPS = ['kr', 'vr0', 'vr1'] + [
     'kd0', 'kd1', 'kd2', 'kd3', 'kd4', 'vd', 'lim0', 'lim1', 'kr0', 'qo', 'lo0', 'lo1', 'swp', 'ew', 'er', 'og']
 SOPS = {'qrs': 's[0:3]', 'ors': 's[12:15]', 'lrs': 's[16:19]', 'c': 's20',
         'nt': 's21', 'ntw': 's22', 'lmin': 's23', 'has_lse': 's24', 'ogs': 's25', 'kb0': 's26', 'kb1': 's27',
@@ -41,28 +41,22 @@ def lim_of(pos, n_k, block):
     return n_k if pos >= block else min(n_k, pos + 1)
 
 
-def vt_swz(d):
-    return (d & 7) ^ ((d >> 3) & 3)
+def v_read_regs(vbase, d, lane):
+    """%[vr0] and %[vr1] (attn_fwd64.hip): lane l = 32 g + 16 h + i addresses key row 8 g + i // 4 of a V fragment,
+    bytes 8 (i % 4) of unit v_unit(2 db + h, i // 4) for db = 0 and 1."""
+    g, h, i = lane >> 5, (lane >> 4) & 1, lane & 15
+    return [vbase + (8 * g + i // 4) * 2 * d + 32 * np.array([G.v_unit(2 * db + hh, ii // 4) for hh, ii in zip(h, i)])
+            + 8 * (i % 4) for db in (0, 1)]
 
 
-def vt_images(vb, kv, n_k, k_pad, ind, dim=128):
-    """The f16 V^T tile images: [kv][tile][d dim][slot 8][8 keys], slot s of row d holding keys 8 (s ^ vt_swz(d))."""
-    nti = (n_k + 63) // 64
-    if ind == 'bf16':
-        f = vb.astype(np.uint32) << 16
-        vals = f.view(np.float32)
-        h = E.f16_rtz(vals).view(np.uint16).reshape(kv, k_pad, dim)
-    else:
-        h = vb.reshape(kv, k_pad, dim).astype(np.uint16)
-    img = np.zeros((kv, nti, dim, 8, 8), np.uint16)
-    for t in range(nti):
-        for d in range(dim):
-            for sl in range(8):
-                c = sl ^ vt_swz(d)
-                keys = t * 64 + 8 * c + np.arange(8)
-                ok = keys < n_k
-                img[:, t, d, sl, ok] = h[:, keys[ok], d]
-    return img, nti
+def vd_lane(d, lane):
+    """The V byte (relative to its 1 KiB piece) lane l's LDS slot of a V image piece holds: slot byte 16 l is row r,
+    unit p, half; it holds unit v_unit(p, r) of that row (v_unit is its own inverse for a given row)."""
+    rowb = 2 * d
+    b = 16 * lane
+    r, pos = b // rowb, b % rowb
+    u = np.array([G.v_unit(int(pp), int(rr)) for pp, rr in zip(pos // 32, r)])
+    return r * rowb + 32 * u + 16 * ((pos // 16) & 1)
 
 
 def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verbose=True, kgrow=0.0, d=128):
@@ -83,15 +77,13 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
     K_TILE, NKP, row_b = 64 * K_ROW, (64 * K_ROW // 1024 - 1) // 4, 2 * d
     so = 4 if outd == 'f32' else 2
     # global memory
-    img, nti = vt_images(vb, kv, S_k, k_pad, ind, d)
-    sizes = [qb.nbytes, kb.nbytes, vb.nbytes, S_q * width * so + 4096, heads * S_q * 4 + 4096, img.nbytes + 4096]
+    sizes = [qb.nbytes, kb.nbytes, vb.nbytes, S_q * width * so + 4096, heads * S_q * 4 + 4096]
     offs = np.cumsum([4096] + [((x + 4095) // 4096) * 4096 for x in sizes])
-    Q0, K0, V0, O0, L0, I0 = [int(x) for x in offs[:6]]
+    Q0, K0, V0, O0, L0 = [int(x) for x in offs[:5]]
     mem = E.Mem(int(offs[-1]) + 4096)
     mem.b[Q0:Q0 + qb.nbytes] = qb.view(np.uint8).ravel()
     mem.b[K0:K0 + kb.nbytes] = kb.view(np.uint8).ravel()
     mem.b[V0:V0 + vb.nbytes] = vb.view(np.uint8).ravel()
-    mem.b[I0:I0 + img.nbytes] = img.view(np.uint8).ravel()
     fill = np.full(S_q * width, np.nan, np.float32) if so == 4 else None
     if so == 4:
         mem.b[O0:O0 + fill.nbytes] = fill.view(np.uint8)
@@ -138,15 +130,14 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
             lim0 = np.array([lim_of(p0 + cc, S_k, block) for cc in c32]) - 8 * g
             lim1 = np.array([lim_of(p0 + 32 + cc, S_k, block) for cc in c32]) - 8 * g
             kr = lbase + c32 * K_ROW + 16 * g
-            sw = np.array([vt_swz(x) for x in c32])
-            vr = [vbase + c32 * 128 + ((((2 * cc + g) ^ sw) & 7) << 4) for cc in range(4)]
+            vr = v_read_regs(vbase, d, lane)
 
             def kd_of(i):
                 b = 1024 * i + 16 * lane
                 R, c = b // K_ROW, (b % K_ROW) // 16
                 return np.array([slot_of(int(r)) for r in R]) * row_b + 16 * np.where(c < d // 8, c, 0)
             kds = [kd_of(w + 4 * m) for m in range(NKP)] + [0] * (4 - NKP) + [kd_of(4 * NKP)]
-            vd = (V_TILE // 4) * w + 16 * lane
+            vd = (V_TILE // 4) * w + vd_lane(d, lane)
             qo = ((q0 + c32) * d + 8 * g) * 2
             orow = d * so
             lpr = orow // 16
@@ -161,12 +152,9 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
             lo0 = np.where(q0 + c32 < S_q, (h * S_q + q0 + c32) * 4, 0xffffffff)
             lo1 = np.where(q0 + 32 + c32 < S_q, (h * S_q + q0 + 32 + c32) * 4, 0xffffffff)
             swp = (lane ^ 32) * 4
-            vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], vr2=vr[2], vr3=vr[3], kd0=kds[0], kd1=kds[1], kd2=kds[2],
+            vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], kd0=kds[0], kd1=kds[1], kd2=kds[2],
                         kd3=kds[3], kd4=kds[4], vd=vd, lim0=lim0, lim1=lim1, kr0=kr, qo=qo, lo0=lo0, lo1=lo1, ew=ew, er=er, og=og,
                         swp=swp)
-            if G.STAGING != 'dma':
-                vals.update(kwa=lbase + 1024 * w + 16 * lane, kwb=lbase + 16384 + 16 * lane,
-                            vwa=vbase + 4096 * w + 16 * lane)
             for n, arr in vals.items():
                 W.v[int(VREG[n][1:])] = np.asarray(arr, np.int64).astype(np.uint32) if np.ndim(arr) else \
                     np.full(64, int(arr) & 0xFFFFFFFF, np.uint32)
@@ -178,9 +166,9 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
                 W.s[sidx + 3] = 0x00020000
             rs(0, Q0 + h * q_pad * row_b, S_q * row_b)
             kbase = K0 + kvh * k_pad * row_b
-            ibase = I0 + kvh * nti * V_TILE
+            vrow = V0 + kvh * k_pad * row_b
             W.s[26], W.s[27], W.s[28] = kbase & 0xFFFFFFFF, (kbase >> 32) & 0xFFFF, n_keys * row_b
-            W.s[29], W.s[30], W.s[31] = ibase & 0xFFFFFFFF, (ibase >> 32) & 0xFFFF, nt * V_TILE
+            W.s[29], W.s[30], W.s[31] = vrow & 0xFFFFFFFF, (vrow >> 32) & 0xFFFF, n_keys * row_b
             W.s[32], W.s[33], W.s[34] = lbase, lbase + 1024 * w, vbase + (V_TILE // 4) * w
             rs(12, O0, S_q * width * so)
             rs(16, L0, heads * S_q * 4)

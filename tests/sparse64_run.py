@@ -12,7 +12,7 @@ import oracle as O
 
 NONE = 0xFFFFFFFF
 
-VOPS = ['ocol', 'ocol_hi', 'kr', 'vr0', 'vr1', 'vr2', 'vr3', 'kd0', 'kd1', 'kd2', 'kd3', 'kd4', 'vd', 'lim0', 'lim1',
+VOPS = ['ocol', 'ocol_hi', 'kr', 'vr0', 'vr1', 'kd0', 'kd1', 'kd2', 'kd3', 'kd4', 'vd', 'lim0', 'lim1',
         'kr0', 'qo', 'lo0', 'lo1', 'swp', 'ew', 'er', 'mp', 'mlive', 'mo', 'g32']
 SOPS = {'qrs': 's[0:3]', 'lrs': 's[4:7]', 'mrs': 's[8:11]', 'ent': 's[12:13]', 'c': 's20', 'nt': 's21', 'ntw': 's22',
         'lmin': 's23', 'has_lse': 's24', 'ows': 's25', 'kb0': 's26', 'kb1': 's27', 'kn': 's28', 'vb0': 's29',
@@ -92,14 +92,13 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
     table, counts = pass_table(sel, nsel, valid, n_q=n_q, n_k=n_k, kv_heads=kv, n_cubes=n_cubes, max_sel=max_sel,
                                dense0=dense0, dense1=dense1, causal=causal)
     n_qt, n_ent = table.shape[1], table.shape[2]
-    img, nti = R.vt_images(vb, kv, k_pad, k_pad, ind)  # images of every key row: valid masks, not n_k
     mp32 = np.asarray(map_, np.int32)
-    sizes = [qb.nbytes, kb.nbytes, vb.nbytes, o_rows * width * so + 4096, heads * q_pad * 4 + 4096, img.nbytes + 4096,
+    sizes = [qb.nbytes, kb.nbytes, vb.nbytes, o_rows * width * so + 4096, heads * q_pad * 4 + 4096,
              table.nbytes + 4096, mp32.nbytes + 4096]
     offs = np.cumsum([4096] + [((x + 4095) // 4096) * 4096 for x in sizes])
-    Q0, K0, V0, O0, L0, I0, T0, M0 = [int(x) for x in offs[:8]]
+    Q0, K0, V0, O0, L0, T0, M0 = [int(x) for x in offs[:7]]
     mem = E.Mem(int(offs[-1]) + 4096)
-    for base, arr in ((Q0, qb), (K0, kb), (V0, vb), (I0, img), (T0, table), (M0, mp32)):
+    for base, arr in ((Q0, qb), (K0, kb), (V0, vb), (T0, table), (M0, mp32)):
         mem.b[base:base + arr.nbytes] = arr.view(np.uint8).ravel()
     sentinel = np.full(o_rows * width, 1234.5, np.float32) if so == 4 else conv(np.full(o_rows * width, 1234.5,
                                                                                         np.float32))
@@ -132,8 +131,7 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
                 else:
                     lim0, lim1, lmin = np.full(64, big), np.full(64, big), big
                 kr = lbase + c32 * G.K_ROW + 16 * g
-                sw = np.array([R.vt_swz(x) for x in c32])
-                vr = [vbase + c32 * 128 + ((((2 * cc + g) ^ sw) & 7) << 4) for cc in range(4)]
+                vr = R.v_read_regs(vbase, 128, lane)
 
                 def kd_of(i):
                     b = 1024 * i + 16 * lane
@@ -149,8 +147,8 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
                     ew = obase + c32 * orow + 8 * g + 16 * (c32 & 7)
                 er = obase + (lane // lpr) * orow + 16 * ((lane % lpr) ^ (lane // lpr))
                 ocol = O0 + h * orow + 16 * (lane % lpr)
-                vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], vr2=vr[2], vr3=vr[3], kd0=kds[0], kd1=kds[1], kd2=kds[2],
-                            kd3=kds[3], kd4=kds[4], vd=4096 * w + 16 * lane, lim0=lim0, lim1=lim1, kr0=kr,
+                vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], kd0=kds[0], kd1=kds[1], kd2=kds[2],
+                            kd3=kds[3], kd4=kds[4], vd=4096 * w + R.vd_lane(128, lane), lim0=lim0, lim1=lim1, kr0=kr,
                             qo=((q0 + c32) * 128 + 8 * g) * 2,
                             lo0=np.where(q0 + c32 < n_q, (h * q_pad + q0 + c32) * 4, NONE),
                             lo1=np.where(q0 + 32 + c32 < n_q, (h * q_pad + q0 + 32 + c32) * 4, NONE),
@@ -172,7 +170,7 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
                 ent = T0 + ((kvh * n_qt + qt) * n_ent) * 16
                 W.s[12], W.s[13] = ent & 0xFFFFFFFF, ent >> 32
                 kbase = K0 + kvh * k_pad * 256
-                ibase = I0 + kvh * nti * 16384
+                ibase = V0 + kvh * k_pad * 256
                 W.s[26], W.s[27], W.s[28] = kbase & 0xFFFFFFFF, (kbase >> 32) & 0xFFFF, 0
                 W.s[29], W.s[30], W.s[31] = ibase & 0xFFFFFFFF, (ibase >> 32) & 0xFFFF, 0
                 W.s[32], W.s[33], W.s[34] = lbase, lbase + 1024 * w, vbase + 4096 * w

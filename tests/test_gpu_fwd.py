@@ -172,3 +172,61 @@ def test_deterministic_and_row_independent():
     assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
     o3, _ = run_fwd(qb, kb, vb, O.BF16, O.F32, n_q=33, n_k=S, **args)
     assert np.array_equal(o3, o1[:33])
+
+
+@pytest.mark.parametrize("dim", [128, 64])
+def test_bf16_v_outside_the_f16_range(dim):
+    """bf16 V is used as it is (P V runs in bf16 for bf16 inputs): head-dimension columns of V scaled from 1e-7 to
+    1e5, beyond f16's range at both ends, come out with each column's relative L2 error (over all rows) within the
+    reference's 5e-3, and every element within the tolerance at the column's scale."""
+    rng = np.random.default_rng(100 + dim)
+    heads, kv, S = 4, 2, 300
+    scale = (10.0 ** np.linspace(-7, 5, dim)).astype(np.float32)
+    qb = G.randn_bits(rng, (heads, S, dim), O.BF16)
+    kb = G.randn_bits(rng, (kv, S, dim), O.BF16)
+    vb = G.bits(rng.standard_normal((kv, S, dim)).astype(np.float32) * scale, O.BF16)
+    args = dict(n_q=S, q_pad=(S + 63) // 64 * 64, n_k=S, k_pad=(S + 127) // 128 * 128, heads=heads, kv_heads=kv,
+                q_pos0=0, block=U32, dim=dim)
+    pad = lambda b, r: np.concatenate([b, np.zeros((b.shape[0], r - S, dim), b.dtype)], 1)
+    qb, kb, vb = pad(qb, args["q_pad"]), pad(kb, args["k_pad"]), pad(vb, args["k_pad"])
+    print(f"bf16 V over 1e-7 .. 1e5, D {dim}", flush=True)
+    o, _ = run_fwd(qb, kb, vb, O.BF16, O.F32, **args)
+    want, _ = O.attn_dense(qb, kb, vb, dtype=O.BF16, **args)
+    got, want = o.reshape(S, heads, dim), want.reshape(S, heads, dim)
+    rel = np.sqrt(((got - want) ** 2).sum((0, 1)) / (want ** 2).sum((0, 1)))
+    assert rel.max() < G.ROW_L2, f"worst column relative L2 {rel.max():.2e} at scale {scale[rel.argmax()]:.1e}"
+    G.assert_attn_close(got / scale, want / scale, "output at the column's scale")
+
+
+def test_bf16_probabilities_on_peaked_rows():
+    """P is rounded to the input type for P V: bf16 for bf16 inputs (8 significant bits, relative error <= 2^-8 a
+    probability), f16 for f16 inputs (the reference's half P). Scores of deviation 4 put each row's softmax on a few
+    keys, where those roundings do not average out: bf16 rows stay within the bound the rounding gives,
+    2^-8 sum_j w_j |v_j| (w the softmax weights) plus 2e-4 for the rest of the arithmetic; the same values as f16
+    inputs meet the element tolerance."""
+    rng = np.random.default_rng(44)
+    heads, kv, dim, S = 4, 2, 128, 256
+    qf = rng.standard_normal((heads, S, dim)).astype(np.float32) * 2
+    kf = rng.standard_normal((kv, S, dim)).astype(np.float32) * 2
+    vf = rng.standard_normal((kv, S, dim)).astype(np.float32)
+    args = dict(n_q=S, q_pad=S, n_k=S, k_pad=S, heads=heads, kv_heads=kv, q_pos0=0, block=0, dim=dim)
+    print("peaked rows, bf16 and f16", flush=True)
+    qb, kb, vb = (G.bits(x, O.BF16) for x in (qf, kf, vf))
+    o, _ = run_fwd(qb, kb, vb, O.BF16, O.F32, **args)
+    want, _ = O.attn_dense(qb, kb, vb, dtype=O.BF16, **args)
+    # the bound: w from the exact scores of the bf16 values
+    q64 = O.bits_to_f32(qb, O.BF16).astype(np.float64)
+    k64 = O.bits_to_f32(kb, O.BF16).astype(np.float64)
+    v64 = O.bits_to_f32(vb, O.BF16).astype(np.float64)
+    bound = np.empty((S, heads, dim))
+    for h in range(heads):
+        s = q64[h] @ k64[h // 2].T / np.sqrt(dim)
+        w = np.exp(s - s.max(1, keepdims=True))
+        w /= w.sum(1, keepdims=True)
+        bound[:, h] = w @ np.abs(v64[h // 2])
+    err = np.abs(o.reshape(S, heads, dim) - want.reshape(S, heads, dim))
+    assert np.all(err <= 2.0 ** -8 * bound + 2e-4), f"max err over the bound {(err - 2.0 ** -8 * bound).max():.2e}"
+    qh, kh, vh = (G.bits(x, O.F16) for x in (qf, kf, vf))
+    o16, _ = run_fwd(qh, kh, vh, O.F16, O.F32, **args)
+    want16, _ = O.attn_dense(qh, kh, vh, dtype=O.F16, **args)
+    G.assert_attn_close(o16, want16, "f16 output")

@@ -30,9 +30,11 @@ U32 = 0xFFFFFFFF
 
 def make(rng, *, T_q, T_k, heads, kv, dim, rope, rot, eps_q, eps_k, pad=0):
     """fp32 projection rows of q [T_q][heads dim + pad], k / v [T_k][kv dim + pad] (pad shifts col0), the angle
-    table for max(T_q, T_k) rows, and the norm weights."""
-    xq = rng.standard_normal((T_q, heads * dim + pad)).astype(np.float32) * 2
-    xk = rng.standard_normal((T_k, kv * dim + pad)).astype(np.float32) * 2
+    table for max(T_q, T_k) rows, and the norm weights. Rows are of unit scale, and of twice that where the head is
+    normed (so that the norm's division shows); un-normed q and k of scale 2 would make scores of deviation 4, a
+    softmax that sits on a few keys, whose bf16 probabilities test_gpu_fwd.py's peaked case checks."""
+    xq = rng.standard_normal((T_q, heads * dim + pad)).astype(np.float32) * (2 if eps_q else 1)
+    xk = rng.standard_normal((T_k, kv * dim + pad)).astype(np.float32) * (2 if eps_k else 1)
     xv = rng.standard_normal((T_k, kv * dim + pad)).astype(np.float32)
     ang = rng.uniform(-np.pi, np.pi, (max(T_q, T_k, 1), max(rot // 2, 1)))
     cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)

@@ -169,7 +169,9 @@ def test_all_cubes_equals_dense():
     M.attn_fwd(q, k, v, od, n_q=n, q_pad=n, n_k=n, k_pad=n, heads=heads, kv_heads=kv, q_pos0=0, block=0, dim=128,
                lse=ld)
     torch.cuda.synchronize()
-    np.testing.assert_allclose(o, G.to_host(od), rtol=1e-2, atol=5e-4)
+    # the two kernels visit the keys in other orders, so their running maxima, and with them the bf16 roundings of
+    # P, differ: the outputs agree within the attention tolerance, the LSE (sums of unrounded exponentials) closer
+    G.assert_attn_close(o, G.to_host(od), "sparse vs dense output")
     np.testing.assert_allclose(lse, ld.cpu().numpy(), atol=1e-4)
 
 
