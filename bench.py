@@ -38,9 +38,11 @@ WARM_SECONDS = 0.3    # least untimed GPU work before each timed region
 
 def time_launches(torch, fn, steps, warmup):
     """Times `steps` back-to-back launches of fn after `warmup` untimed ones, by HIP events on the current stream
-    (the stream the C ABI launches on). Returns (ms a step over the whole timed region, the mean of each launch's
-    own event pair): the first is the step time, the second the kernel duration the roofline divides. The untimed
-    warmup also runs for at least WARM_SECONDS, so the GPU's clocks have settled before the timed region."""
+    (the stream the C ABI launches on). Returns (ms a step over a timed region of `steps` calls with nothing
+    between them, the mean of each launch's own event pair over a second such region): the first is the step time,
+    the second the kernel duration the roofline divides (an event pair around every call adds its own gaps to the
+    stream, so the two regions are separate). The untimed warmup also runs for at least WARM_SECONDS, so the GPU's
+    clocks have settled before the timed regions."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -49,14 +51,17 @@ def time_launches(torch, fn, steps, warmup):
         for _ in range(8):
             fn()
         torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for a, b in ev:
         a.record()
         fn()
         b.record()
-    end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps, sum(a.elapsed_time(b) for a, b in ev) / steps
 

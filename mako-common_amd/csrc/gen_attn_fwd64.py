@@ -311,14 +311,15 @@ def pv_mfmas(dtype):
     return out
 
 
-def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=(), dma=None):
+def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=(), dma=None, fwait=None):
     """Emits the MFMAs of a phase, each tagged with the fragment it reads, fed by a ring of RING LDS reads, with the
     instructions of `valu` spread evenly between them. Fragment f lives in ring slot f % RING; its read goes out AHEAD
     fragments before its MFMAs (a slot is refilled two fragments after its previous occupant's last MFMA). The first
     `pre` reads were issued before the phase began, as the last LDS instructions before it. nxt = (kind, reads) of
     the next phase: its read m goes out after fragment len(reads) + m - AHEAD of this phase, and not before `gate`,
     the instructions emitted after fragment gate_at's MFMAs. dma = (groups, tail) of dma_groups(): group i after
-    MFMA i * n / len(groups) (after that MFMA's share of `valu`), the tail after the last MFMA's.
+    MFMA i * n / len(groups) (after that MFMA's share of `valu`), the tail after the last MFMA's. fwait: {fragment:
+    instructions} emitted before that fragment's first MFMA.
     Returns how many of the next phase's reads went out.
     LDS returns in order, so the wait for a read is lgkmcnt(LDS instructions issued after it); LDS instructions inside
     `valu` are counted too. A fragment's reads may be several instructions; its MFMAs wait for the last."""
@@ -361,6 +362,8 @@ def phase(e, kind, reads, mfmas, valu, pre=0, nxt=None, gate_at=None, gate=(), d
         if i == 0 or mfmas[i - 1][0] != f:
             pos = len(issued) - 1 - issued[::-1].index((kind, f))
             e(f"s_waitcnt lgkmcnt({min(len(issued) - 1 - pos, 15)})")
+            for op in (fwait or {}).get(f, []):
+                e(op)
         e(ring_fmt(text, f % RING))
         if i + 1 == n or mfmas[i + 1][0] != f:
             if gate_at == f:
@@ -478,12 +481,18 @@ def wait_mfma():
     return ["s_nop 7", "s_nop 7", "s_nop 4"]
 
 
+def q_waits():
+    """Tile 0's score MFMAs wait for the Q pair (both row blocks of a 16-dim step) they use: fragment 2 kk's MFMAs
+    read Q(., kk), loaded kk-th after tile 0 (tiles 1 and 2 behind them)."""
+    return {2 * kk: [f"s_waitcnt vmcnt({2 * (NKK - 1 - kk) + 2 * DMA_PER_TILE})"] for kk in range(NKK)}
+
+
 def exact_tile(e, dtype, sbuf, kaddr, j0, first=False, w=None):
     """The exact path for a tile (K at LDS address kaddr, first key in scalar j0): its raw scores into S(sbuf), the
     mask, each row's maximum, the reference's rule for moving the running maximum (outputs and sums rescaled when it
     moves), the exponentials, P and the sums (TMP[0], TMP[4]). first: the wave's first tile, where the outputs and
-    sums are still zero and need no rescaling."""
-    interleave(e, k_reads(kaddr), qk_mfmas(dtype, sbuf), [])
+    sums are still zero and need no rescaling, and Q is still arriving (q_waits)."""
+    phase(e, "X", k_reads(kaddr), qk_mfmas(dtype, sbuf), [], fwait=q_waits() if first else None)
     for op in wait_mfma() + (mask_general(sbuf, j0, w) if SPARSE else mask(sbuf, j0)):
         e(op)
     for rb in range(2):
@@ -709,6 +718,8 @@ def body_of(in_dtype, out_dtype):
         e(f"s_load_dwordx4 s[76:79], %[ent], 0")
         e(f"buffer_load_dword {MAPV}, %[mo], %[mrs], 0 offen")
     e(f"s_mov_b32 {S256}, 0x43800000")
+    for r in TMP[8:12]:   # zeros for the MFMAs that clear the outputs
+        e(f"v_mov_b32 {r}, 0")
     e(f"v_mov_b32 {NINF}, 0xff800000")
     e(f"v_mov_b32 {ZERO}, 0")
     for rb in range(2):
@@ -722,14 +733,11 @@ def body_of(in_dtype, out_dtype):
         e(f"s_mov_b32 {r[2]}, %[{pre}n]")
         e(f"s_mov_b32 {r[3]}, 0x20000")
     e(f"s_mov_b32 {SBW}, 0")
-    # Q into the accumulator registers (rows past n_q load as zeros)
-    e(f"v_add_u32 {TMP[0]}, {64 * D:#x}, %[qo]")   # row block 1: 32 rows of 2 d bytes on
-    for rb in range(2):
-        for kk in range(NKK):
-            e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen offset:{32 * kk}")
     # M0 is the compiler's: kept in SM0 while the stream uses it, restored at the end
     e(f"s_mov_b32 {SM0}, m0")
-    # tiles 0, 1, 2 into buffers 0, 1, 2; outputs zeroed meanwhile; the barrier waits for tiles 0 and 1
+    # tile 0 into buffer 0, then Q into the accumulator registers (rows past n_q load as zeros), then tiles 1 and 2
+    # into buffers 1 and 2; outputs zeroed meanwhile. Loads retire in order: the first barrier waits for tile 0
+    # only, tile 0's score MFMAs each wait for the Q pair they use (q_waits), and a barrier after tile 0 for tile 1.
     e(f"s_mov_b32 {SKW}, %[skw]")
     e(f"s_mov_b32 {SKWW}, %[skww]")
     e(f"s_mov_b32 {SVWW}, %[svww]")
@@ -740,10 +748,19 @@ def body_of(in_dtype, out_dtype):
             e(f"s_mov_b32 {SD}, s{88 + i}")
         for op in dma_issue():
             e(op)
+        if i == 0:
+            e(f"v_add_u32 {TMP[0]}, {64 * D:#x}, %[qo]")   # row block 1: 32 rows of 2 d bytes on
+            for kk in range(NKK):
+                for rb in range(2):
+                    e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen "
+                      f"offset:{32 * kk}")
     if SPARSE:
         e(f"s_mov_b32 {SD}, s91")
-    for i in range(32 * NDB):
-        e(f"v_accvgpr_write_b32 a{i}, 0")
+    # the outputs cleared by MFMAs of zero operands: a few issue slots, the matrix unit does the rest (128
+    # v_accvgpr_write took ~700 cycles of the prologue)
+    z = f"v[{TMP[8][1:]}:{TMP[11][1:]}]"
+    for i in range(2 * NDB):
+        e(f"v_mfma_f32_32x32x16_{in_dtype} a[{16 * i}:{16 * i + 15}], {z}, {z}, 0")
     body_rest(e, in_dtype, out_dtype)
     return e.out
 
@@ -752,10 +769,15 @@ def body_rest(e, in_dtype, out_dtype):
     e(f"s_mov_b32 {SJ}, 0")
     e(f"s_mov_b32 {SBK}, 0")
     e(f"s_mov_b32 {SBV}, 0")
-    for op in barrier():
-        e(op)
+    # the first barrier: every wave's loads of tile 0 have landed (Q and tiles 1 and 2 may still be in flight)
+    e(f"s_waitcnt vmcnt({2 * NKK + 2 * DMA_PER_TILE}) lgkmcnt(0)")
+    e("s_barrier")
     e("s_cmp_eq_u32 %[ntw], 0")
-    e(f"s_cbranch_scc1 {lbl('L_tail')}")
+    e(f"s_cbranch_scc0 {lbl('L_live')}")
+    for op in barrier():   # a wave with no rows: the barrier for tile 1 as the others, then the load-only loop
+        e(op)
+    e(f"s_branch {lbl('L_tail')}")
+    e.label("L_live")
     # tile 0 by the exact path
     if SPARSE:
         exact_tile(e, in_dtype, 0, "%[kr]", ST[0], first=True, w="s[78:79]")
@@ -766,6 +788,8 @@ def body_rest(e, in_dtype, out_dtype):
     e(f"v_add_f32 {LSUM[1]}, {LSUM[1]}, {TMP[4]}")
     if in_dtype == "bf16":
         low_part_pass(e)
+    for op in barrier():   # every wave's loads of tile 1 have landed
+        e(op)
 
     def iteration(par, variant, masked_next=False):
         """Iteration j with S_cur = S(par), S_nxt = S(1 - par). variant: 'plain' (tile j + 1 fully seen by the

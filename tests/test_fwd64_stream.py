@@ -176,3 +176,11 @@ def test_planted_missing_low_part_pass_is_found(monkeypatch):
     monkeypatch.setattr(G, "low_part_pass", lambda e: None)
     r = R.run(heads=8, kv=2, S_q=40, S_k=5, q_pos0=0, block=U32, seed=9, d=64, verbose=False)
     assert r["out_bad"] > 0
+
+
+def test_planted_missing_q_wait_is_found(monkeypatch):
+    """Tile 0's score MFMAs start while Q is still arriving: without the per-pair waits they read Q registers whose
+    loads have not landed."""
+    monkeypatch.setattr(G, "q_waits", lambda: {})
+    r = R.run(4, 1, 64, 200, 0, 0, seed=9, verbose=False)
+    assert r["out_bad"] > 0
