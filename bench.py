@@ -815,7 +815,33 @@ def main():
         line["parity"] = pre["parity"]
         line["decode"]["cpu_baseline"] = dec["cpu_baseline"]
         line["decode"]["parity"] = dec["parity"]
+    line["configs"] = configs_summary(line, pre, dec, few)
     print(json.dumps(line), flush=True)
+
+
+def configs_summary(line, pre, dec, few):
+    """The five configurations and the few-row route in a few numbers each, last in the JSON line (so a record that
+    keeps only the line's tail still holds them): value, unit, kernel ms, fraction of the roofline, and the parity of
+    the sampled rows (within tolerance, max abs error)."""
+    def par(p):
+        return {} if not p else {"within_tolerance": p["within_tolerance"], "max_abs_err": round(p["max_abs_err"], 6)}
+
+    def entry(value, unit, kernel_ms, frac, parity):
+        return dict({"value": round(value, 2), "unit": unit, "kernel_ms": round(kernel_ms, 4),
+                     "frac": round(frac, 4)}, **par(parity))
+    s512, bid, spa = line["prefill_s512"], line["bidirectional"], line["block_sparse"]
+    f1 = few["n_q=1"]
+    return {
+        "C1_causal_s512_f16": entry(s512["value"], "TFLOP/s", s512["roofline"]["kernel_ms"], s512["roofline"]["frac"],
+                                    s512.get("parity")),
+        "C2_causal_s4096_bf16": entry(pre["tflops"], "TFLOP/s", pre["kernel_ms"], pre["roofline"]["frac"],
+                                      pre.get("parity")),
+        "C3_decode_b16": entry(dec["gbps"], "GB/s", dec["kernel_ms"], dec["roofline"]["frac"], dec.get("parity")),
+        "C4_block_sparse_s16384": entry(spa["value"], "TFLOP/s", spa["kernel_ms"], spa["roofline"]["frac"],
+                                        spa.get("parity")),
+        "C5_bidirectional_s16384": entry(bid["value"], "TFLOP/s", bid["kernel_ms"], bid["frac"], bid.get("parity")),
+        "few_rows_n_q1": entry(f1["gbps"], "GB/s", f1["kernel_ms"], f1["roofline"]["frac"], f1.get("parity")),
+    }
 
 
 if __name__ == "__main__":

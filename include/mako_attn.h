@@ -95,12 +95,33 @@ const char* mako_last_error(void);
  * whose kernel converts bf16 V to f16 rounding toward zero (|v| above 65504 saturates, below 6.1e-5 loses bits).
  * The sums and the LSE add the unrounded f32 exponentials. Heads of 64 and 128 take one of two routes: a few query
  * rows (n_q x heads / kv_heads <= 64, as the reference's decode, attention with n_q = 1) split-K over the keys,
- * which keeps a workspace per (device, stream), allocated stream-ordered the first time a call needs it (or more of
- * it); more rows, the prefill kernel, one launch that allocates nothing. Heads of 256 first write V as f16 V^T tiles
- * into such a workspace.
+ * with its partials in a workspace; more rows, the prefill kernel, one launch with no workspace. Heads of 256 first
+ * write V as f16 V^T tiles into a workspace. mako_attn_fwd keeps that workspace itself, per (device, stream),
+ * allocated stream-ordered the first time a call needs it (or more of it) and held until mako_attn_release(stream);
+ * under graph capture a call that would grow it fails with MAKO_EWORKSPACE.
  */
 int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
                   const void* k, const void* v, void* o, float* lse, void* stream);
+
+/*
+ * mako_attn_fwd with the caller's workspace, for callers that own their scratch (the reference's Runtime owns it as
+ * named scratch buffers: src/gpu/runtime.cpp:117-125; TransformerRuntime::attention passes scratch("attn_fwd")).
+ * It allocates nothing; MAKO_EWORKSPACE when workspace_bytes is below mako_attn_fwd_workspace(a, dim) (0 for the
+ * prefill routes: workspace may then be NULL). The workspace's contents do not matter before or after a call;
+ * calls that overlap in time need separate workspaces.
+ */
+size_t mako_attn_fwd_workspace(const mako_attn_args* a, uint32_t dim);
+int mako_attn_fwd_ws(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
+                     const void* k, const void* v, void* o, float* lse, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * The workspaces the entry points without a workspace argument keep for a stream (on the current device): waits for
+ * the stream, then frees them. No counterpart in the reference (its Runtime frees its scratch at destruction).
+ * mako_attn_held_bytes: the bytes held on the current device, over all streams.
+ */
+int mako_attn_release(void* stream);
+size_t mako_attn_held_bytes(void);
 
 /*
  * Cube selection for block-sparse attention: per head and query cube, the topk key cubes by the dot product
@@ -126,14 +147,21 @@ int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, uint32_t n_
  * output goes to o row map[r] (dropped when map[r] < 0). Requires q_pad % 64 == 0, k_pad % 128 == 0,
  * dense0 % 32 == 0 (the reference's checks) and n_cubes * 64 <= k_pad. lse [heads][q_pad] by tile row (may be
  * NULL). Lists shared by a kv head's query heads (sel_heads == kv_heads) in groups of 4, with dense0 % 64 == 0
- * and valid 16-byte aligned, take a route that first writes a pass table into a workspace per (device, stream),
- * allocated stream-ordered the first time a call needs it (or more of it); P rounds as in mako_attn_fwd (bf16 P for
- * bf16 inputs; rows whose first pass is not a full one get tile-0 probabilities to ~16 bits). Other calls allocate
- * nothing and convert bf16 V and P to f16 (V rounding toward zero: |v| above 65504 saturates).
+ * and valid 16-byte aligned, take a route that first writes a pass table into a workspace (kept as mako_attn_fwd
+ * keeps its own); P rounds as in mako_attn_fwd (bf16 P for bf16 inputs; rows whose first pass is not a full one get
+ * tile-0 probabilities to ~16 bits). Other calls need no workspace and convert bf16 V and P to f16 (V rounding
+ * toward zero: |v| above 65504 saturates).
  */
 int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
                      const void* v, void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
                      const int32_t* map, float* lse, void* stream);
+
+/* mako_attn_sparse with the caller's workspace, as mako_attn_fwd_ws (TransformerRuntime::attention_sparse passes
+ * scratch("attn_sparse")); mako_attn_sparse_workspace(a) bytes (the pass table when the call can take that route). */
+size_t mako_attn_sparse_workspace(const mako_sparse_args* a);
+int mako_attn_sparse_ws(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                        const void* v, void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
+                        const int32_t* map, float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Batched single-token decode, split-K over each sequence's context with fp32 partials merged by their LSE.
@@ -215,13 +243,20 @@ int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const f
  * Heads of 64, 128 or 256 with 16-byte aligned rows (mako_heads' vector path), values neither normed nor rotated,
  * and more rows than the split-K route takes run as two launches: one that writes the query, key and value tiles
  * (heads of 256: the f16 V^T images their kernel stages from instead of the value tiles), then the prefill kernel.
- * Other calls run the four launches above. The tiles live in a workspace per device and stream, allocated
- * stream-ordered the first time a call needs it (or more of it).
+ * Other calls run the four launches above. The tiles live in a workspace (kept as mako_attn_fwd keeps its own).
  */
 int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
                        const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq, const float* xk,
                        const float* xv, const float* cs, const float* wq, const float* wk, void* o, float* lse,
                        void* stream);
+
+/* mako_attn_fwd_rows with the caller's workspace, as mako_attn_fwd_ws (TransformerRuntime::attention_rows passes
+ * scratch("attn_rows")): mako_attn_fwd_rows_workspace(a, dim) bytes, the head tiles and the attention's own. */
+size_t mako_attn_fwd_rows_workspace(const mako_attn_args* a, uint32_t dim);
+int mako_attn_fwd_rows_ws(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
+                          const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq, const float* xk,
+                          const float* xv, const float* cs, const float* wq, const float* wk, void* o, float* lse,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Split-K and gathered latent-cache primitives of the sparse latent decode (src/kernels/gemm.metal:683-870; no call

@@ -729,31 +729,51 @@ namespace mako {
 
 // mako_attn_fwd's route for a few query rows (heads of 128): when the columns (n_q rows x the GQA group) are at most
 // 64, decode_coop over each kv head's keys (those the last row sees), one workgroup a CU taking at least
-// kCoopMinRows keys, partials in the stream's cached workspace, then decode_merge into o [n_q][width] and lse
-// [heads][n_q]. With no key to see, only the merge runs (it writes zeros and lse = -inf). Returns 1 when launched, 0
-// when the case does not take this route (splitk_takes false), -1 when the workspace could not be had.
+// kCoopMinRows keys, partials in the call's workspace (splitk_workspace bytes), then decode_merge into o [n_q][width]
+// and lse [heads][n_q]. With no key to see, only the merge runs (it writes zeros and lse = -inf). Returns 1 when
+// launched, 0 when the case does not take this route (splitk_takes false), -1 when the workspace could not be had
+// (the error recorded).
 bool splitk_takes(const mako_attn_args* a, uint32_t dim)
 {
     return dim == 128 && a->n_q > 0 && (uint64_t)a->n_q * (a->heads / a->kv_heads) <= 64 &&
            (uint64_t)a->q_pos0 + a->n_q < 0xffffffffull;
 }
 
-int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
-                       const void* v, void* o, float* lse, hipStream_t s)
+namespace {
+constexpr uint32_t kCoopMinRows = kCoopWaves * 128;
+
+// The split-K route's shape: keys the last row sees, and workgroups (one a CU at most, each >= kCoopMinRows keys).
+void splitk_shape(const mako_attn_args* a, uint32_t cus, uint32_t& n_keys, uint32_t& n_wg)
 {
-    constexpr uint32_t kCoopMinRows = kCoopWaves * 128;
+    const uint32_t last = a->q_pos0 + a->n_q - 1;  // the last row's position: it sees the most keys
+    n_keys = last >= a->block ? a->n_k : std::min(a->n_k, last + 1);
+    const uint64_t rows = (uint64_t)a->kv_heads * n_keys;
+    n_wg = (uint32_t)std::min<uint64_t>(std::max<uint64_t>((rows + kCoopMinRows - 1) / kCoopMinRows, 1), cus);
+}
+}  // namespace
+
+size_t splitk_workspace(const mako_attn_args* a)
+{
+    const uint32_t cus = device_cus();
+    if (!splitk_takes(a, 128) || !cus)
+        return 0;
+    uint32_t n_keys, n_wg;
+    splitk_shape(a, cus, n_keys, n_wg);
+    return n_keys ? partials_bytes((size_t)n_wg + a->kv_heads, a->n_q * (a->heads / a->kv_heads)) : 0;
+}
+
+int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                       const void* v, void* o, float* lse, hipStream_t s, const Workspace& work)
+{
     const uint32_t group = a->heads / a->kv_heads, nc = a->n_q * group;
     if (!splitk_takes(a, 128))
         return 0;
-    const uint32_t last = a->q_pos0 + a->n_q - 1;  // the last row's position: it sees the most keys
-    const uint32_t n_keys = last >= a->block ? a->n_k : std::min(a->n_k, last + 1);
     const uint32_t ncg = (nc + 31) / 32, ncs = std::min(nc, 32u);
     const uint32_t cus = device_cus();
     if (!cus)
-        return -1;
-    const uint64_t rows = (uint64_t)a->kv_heads * n_keys;
-    const uint32_t n_wg =
-        (uint32_t)std::min<uint64_t>(std::max<uint64_t>((rows + kCoopMinRows - 1) / kCoopMinRows, 1), cus);
+        return fail(MAKO_EHIP, "attention: no device"), -1;
+    uint32_t n_keys, n_wg;
+    splitk_shape(a, cus, n_keys, n_wg);
     // one sequence of n_keys keys a kv head: q [heads][q_pad][kD], o [n_q][width], lse [heads][n_q]
     DecParams p{q, k, v, nullptr, nullptr, nullptr, 1u, a->heads, a->kv_heads, group, a->k_pad, n_keys,
                 n_wg, a->scale * kLog2e, a->n_q, ncg, ncs, a->q_pos0, a->block, a->n_k,
@@ -772,7 +792,7 @@ int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, c
         return 1;
     }
     const size_t pieces = (size_t)n_wg + a->kv_heads;
-    void* ws = stream_workspace(kWsSplitK, partials_bytes(pieces, nc), s);
+    void* ws = work.get(partials_bytes(pieces, nc), s);
     if (!ws)
         return -1;
     p.part_o = static_cast<float*>(ws);

@@ -619,29 +619,35 @@ uint32_t rows_per_wg(uint32_t dim, uint32_t hq) { return (dim == 256 ? 4u : (uin
 }  // namespace
 
 // The split-K route for a few query rows (attn_decode.hip): 1 launched, 0 when the case does not take it, -1 when
-// its workspace could not be allocated.
+// its workspace could not be had (the error recorded); splitk_workspace: the bytes it needs.
+bool splitk_takes(const mako_attn_args* a, uint32_t dim);
+size_t splitk_workspace(const mako_attn_args* a);
 int launch_attn_splitk(const mako_attn_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
-                       const void* v, void* o, float* lse, hipStream_t s);
+                       const void* v, void* o, float* lse, hipStream_t s, const Workspace& work);
 
 // flash_fwd_r64 (attn_fwd64.hip): heads of 128 and 64 with 64 rows a wave; 1 launched, 0 when a size does not fit
-// its offsets. flash_fwd_d256: heads of 256; the same, or -1 when its workspace could not be allocated.
+// its offsets. flash_fwd_d256: heads of 256; the same, or -1 when its workspace could not be had (the error
+// recorded); d256_workspace: the bytes it needs.
 template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                  float* lse, hipStream_t s);
+size_t d256_workspace(const mako_attn_args* a);
 template <class T, class TO>
 int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                    float* lse, hipStream_t s, const void* vt_ready = nullptr);
+                    float* lse, hipStream_t s, const void* vt_ready, const Workspace* work);
 
 namespace {
 
-// false when flash_fwd_d256's workspace could not be allocated (nothing was launched).
+// false when flash_fwd_d256's workspace could not be had (nothing was launched, the error recorded).
 template <class T, class TO>
-bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s)
+bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s,
+              const Workspace& work)
 {
     {
         const int r = dim == 128 ? launch_fwd64<T, TO, 128>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
                       : dim == 64 ? launch_fwd64<T, TO, 64>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
-                                  : launch_fwd_d256<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s);
+                                  : launch_fwd_d256<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s, nullptr,
+                                                           &work);
         if (r)
             return r > 0;
     }
@@ -701,10 +707,17 @@ int attn_check(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype 
     return MAKO_OK;
 }
 
-}  // namespace mako
+// The workspace a dense call needs: the split-K partials (heads of 128, a few rows) or the V^T images (heads of 256);
+// the prefill kernels for heads of 64 and 128 need none.
+size_t attn_fwd_workspace(const mako_attn_args* a, uint32_t dim)
+{
+    if (dim == 128 && splitk_takes(a, dim))
+        return splitk_workspace(a);
+    return dim == 256 ? d256_workspace(a) : 0;
+}
 
-extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
-                             const void* k, const void* v, void* o, float* lse, void* stream)
+int attn_fwd_core(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                  const void* v, void* o, float* lse, const Workspace& work, void* stream)
 {
     if (const int e = attn_check(a, dim, in, out, q, k, v, o))
         return e;
@@ -719,21 +732,43 @@ extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype i
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (dim == 128) {
         // a few query rows (the reference's decode is attention with n_q = 1): split-K over the keys
-        const int r = launch_attn_splitk(a, in, out, q, k, v, o, lse, s);
+        const int r = launch_attn_splitk(a, in, out, q, k, v, o, lse, s, work);
         if (r < 0)
-            return fail(MAKO_EHIP, "attention: no device memory for the split-K partials (%u rows)", a->n_q);
+            return last_code() != MAKO_OK ? last_code() : MAKO_EHIP;
         if (r > 0)
             return check_launch("attention");
     }
     bool launched;
     if (in == MAKO_BF16)
-        launched = out == MAKO_F32 ? launch_d<__bf16, float>(a, dim, p, grid, s)
-                                   : launch_d<__bf16, __bf16>(a, dim, p, grid, s);
+        launched = out == MAKO_F32 ? launch_d<__bf16, float>(a, dim, p, grid, s, work)
+                                   : launch_d<__bf16, __bf16>(a, dim, p, grid, s, work);
     else
-        launched = out == MAKO_F32 ? launch_d<_Float16, float>(a, dim, p, grid, s)
-                                   : launch_d<_Float16, _Float16>(a, dim, p, grid, s);
+        launched = out == MAKO_F32 ? launch_d<_Float16, float>(a, dim, p, grid, s, work)
+                                   : launch_d<_Float16, _Float16>(a, dim, p, grid, s, work);
     if (!launched)
-        return fail(MAKO_EHIP, "attention: no device memory for the V^T tile images (%u kv heads x %u keys)",
-                    a->kv_heads, a->n_k);
+        return last_code() != MAKO_OK ? last_code() : MAKO_EHIP;
     return check_launch("attention");
+}
+
+}  // namespace mako
+
+extern "C" size_t mako_attn_fwd_workspace(const mako_attn_args* a, uint32_t dim)
+{
+    return a ? mako::attn_fwd_workspace(a, dim) : 0;
+}
+
+extern "C" int mako_attn_fwd(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q,
+                             const void* k, const void* v, void* o, float* lse, void* stream)
+{
+    return mako::attn_fwd_core(a, dim, in, out, q, k, v, o, lse,
+                               mako::library_workspace(dim == 128 ? mako::kWsSplitK : mako::kWsVtImages, "attention"),
+                               stream);
+}
+
+extern "C" int mako_attn_fwd_ws(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out,
+                                const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                                size_t workspace_bytes, void* stream)
+{
+    return mako::attn_fwd_core(a, dim, in, out, q, k, v, o, lse,
+                               mako::caller_workspace(workspace, workspace_bytes, "attention"), stream);
 }

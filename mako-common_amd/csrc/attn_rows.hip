@@ -28,7 +28,11 @@ int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const
                  float* lse, hipStream_t s);
 template <class T, class TO>
 int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                    float* lse, hipStream_t s, const void* vt_ready);
+                    float* lse, hipStream_t s, const void* vt_ready, const Workspace* work);
+size_t d256_workspace(const mako_attn_args* a);
+size_t attn_fwd_workspace(const mako_attn_args* a, uint32_t dim);
+int attn_fwd_core(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                  const void* v, void* o, float* lse, const Workspace& work, void* stream);
 
 namespace {
 
@@ -66,18 +70,19 @@ __global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const Head
 size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // The fused route for heads of D: qkv_prep, then the attention kernel. pvt: the value producer (its tiles at pvt.y,
-// the V the attention kernel reads); heads of 256 write V^T images instead, in the stream's workspace.
+// the V the attention kernel reads); heads of 256 write V^T images instead, into images (d256_workspace bytes).
 template <class T, class TO, int D>
 int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParams& pk, const HeadsParams& pvt,
-                const mako_heads_args* hv, const float* xv, void* o, float* lse, hipStream_t s)
+                const mako_heads_args* hv, const float* xv, void* o, float* lse, hipStream_t s,
+                const Workspace& images)
 {
     using L = R64<D>;
     const uint32_t n_vt = (t->n_k + 63) / 64, nbx = (n_vt + 256 / D - 1) / (256 / D);
     void* vt = nullptr;
     if constexpr (D == 256) {
         const size_t vt_bytes = (size_t)t->kv_heads * n_vt * L::kVTile;
-        if (vt_bytes && !(vt = stream_workspace(kWsVtImages, vt_bytes, s)))
-            return fail(MAKO_EHIP, "attention from rows: no device memory for the V^T images (%zu bytes)", vt_bytes);
+        if (vt_bytes && !(vt = images.get(vt_bytes, s)))
+            return last_code();
     }
     const VtRowsParams pv{xv, static_cast<uint32_t*>(vt), hv->ld, hv->col0, hv->stride, t->n_k, n_vt, nbx};
     const uint64_t nbv = D == 256 ? (uint64_t)nbx * t->kv_heads : (pvt.n_items + kItems - 1) / kItems,
@@ -91,7 +96,7 @@ int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParam
     const float sl2 = t->scale * 1.4426950408889634f;
     int r;
     if constexpr (D == 256)
-        r = launch_fwd_d256<T, TO>(t, sl2, pq.y, pk.y, pk.y, o, lse, s, vt);
+        r = launch_fwd_d256<T, TO>(t, sl2, pq.y, pk.y, pk.y, o, lse, s, vt, &images);
     else
         r = launch_fwd64<T, TO, D>(t, sl2, pq.y, pk.y, pvt.y, o, lse, s);
     if (r <= 0)  // (the route was chosen where the kernel fits and its images are given)
@@ -102,11 +107,25 @@ int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParam
 template <class T, class TO>
 int launch_rows_dim(uint32_t dim, const mako_attn_args* t, const HeadsParams& pq, const HeadsParams& pk,
                     const HeadsParams& pvt, const mako_heads_args* hv, const float* xv, void* o, float* lse,
-                    hipStream_t s)
+                    hipStream_t s, const Workspace& images)
 {
-    return dim == 128  ? launch_rows<T, TO, 128>(t, pq, pk, pvt, hv, xv, o, lse, s)
-           : dim == 64 ? launch_rows<T, TO, 64>(t, pq, pk, pvt, hv, xv, o, lse, s)
-                       : launch_rows<T, TO, 256>(t, pq, pk, pvt, hv, xv, o, lse, s);
+    return dim == 128  ? launch_rows<T, TO, 128>(t, pq, pk, pvt, hv, xv, o, lse, s, images)
+           : dim == 64 ? launch_rows<T, TO, 64>(t, pq, pk, pvt, hv, xv, o, lse, s, images)
+                       : launch_rows<T, TO, 256>(t, pq, pk, pvt, hv, xv, o, lse, s, images);
+}
+
+// The call as mako_attn_fwd reads it (q_pad = n_q, k_pad = n_k), and the head tiles' bytes.
+mako_attn_args tiles_call(const mako_attn_args* a)
+{
+    mako_attn_args t = *a;
+    t.q_pad = a->n_q;
+    t.k_pad = a->n_k;
+    return t;
+}
+
+size_t tiles_bytes(const mako_attn_args* a, uint32_t dim)
+{
+    return round256((size_t)a->heads * a->n_q * dim * 2) + 2 * round256((size_t)a->kv_heads * a->n_k * dim * 2) + 256;
 }
 
 }  // namespace
@@ -114,10 +133,14 @@ int launch_rows_dim(uint32_t dim, const mako_attn_args* t, const HeadsParams& pq
 
 using namespace mako;
 
-extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
-                                  const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq,
-                                  const float* xk, const float* xv, const float* cs, const float* wq,
-                                  const float* wk, void* o, float* lse, void* stream)
+namespace {
+
+// tiles: the head tiles' workspace (tiles_bytes); rest: the attention's (the fused route's V^T images for heads of
+// 256, else what mako_attn_fwd needs for the tiles).
+int rows_core(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
+              const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq, const float* xk,
+              const float* xv, const float* cs, const float* wq, const float* wk, void* o, float* lse,
+              const Workspace& tiles, const Workspace& rest, void* stream)
 {
     if (!a || !hq || !hk || !hv || !o)
         return fail(MAKO_EINVAL, "attention from rows: a null argument");
@@ -169,10 +192,9 @@ extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args
     const bool fused = fits && !splitk_takes(&t, dim) && heads_vec_takes(&tq, xq, csq, wq, o) &&
                        heads_vec_takes(&tk, xk, cs, wk, o) && tv.rope == 0 && tv.eps == 0.0f &&
                        heads_vec_takes(&tv, xv, nullptr, nullptr, o);
-    char* ws = static_cast<char*>(stream_workspace(kWsRowTiles, q_bytes + 2 * k_bytes + 256, s));
+    char* ws = static_cast<char*>(tiles.get(tiles_bytes(&t, dim), s));
     if (!ws)
-        return fail(MAKO_EHIP, "attention from rows: no device memory for the head tiles (%zu bytes)",
-                    q_bytes + 2 * k_bytes);
+        return last_code();
     void *qt = ws, *kt = ws + q_bytes, *vt = ws + q_bytes + k_bytes;
     if (!fused) {
         // The producers and attention as separate launches (the same results).
@@ -181,14 +203,47 @@ extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args
             e = mako_heads(&tk, in, xk, cs, wk, nullptr, kt, stream);
         if (!e)
             e = mako_heads(&tv, in, xv, cs, nullptr, nullptr, vt, stream);
-        return e ? e : mako_attn_fwd(&t, dim, in, out, qt, kt, vt, o, lse, stream);
+        return e ? e : attn_fwd_core(&t, dim, in, out, qt, kt, vt, o, lse, rest, stream);
     }
     const HeadsParams pq = heads_params(&tq, xq, csq, wq, nullptr, qt, true);
     const HeadsParams pk = heads_params(&tk, xk, cs, wk, nullptr, kt, true);
     const HeadsParams pvt = heads_params(&tv, xv, nullptr, nullptr, nullptr, vt, true);
     if (in == MAKO_BF16)
-        return out == MAKO_F32 ? launch_rows_dim<__bf16, float>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s)
-                               : launch_rows_dim<__bf16, __bf16>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s);
-    return out == MAKO_F32 ? launch_rows_dim<_Float16, float>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s)
-                           : launch_rows_dim<_Float16, _Float16>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s);
+        return out == MAKO_F32 ? launch_rows_dim<__bf16, float>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s, rest)
+                               : launch_rows_dim<__bf16, __bf16>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s, rest);
+    return out == MAKO_F32 ? launch_rows_dim<_Float16, float>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s, rest)
+                           : launch_rows_dim<_Float16, _Float16>(dim, &t, pq, pk, pvt, &tv, xv, o, lse, s, rest);
+}
+
+}  // namespace
+
+extern "C" size_t mako_attn_fwd_rows_workspace(const mako_attn_args* a, uint32_t dim)
+{
+    if (!a || (dim != 64 && dim != 128 && dim != 256))
+        return 0;
+    const mako_attn_args t = tiles_call(a);
+    // the fused route's images or the separate calls' attention, whichever the call takes: the larger
+    return tiles_bytes(&t, dim) + std::max(dim == 256 ? d256_workspace(&t) : (size_t)0, attn_fwd_workspace(&t, dim));
+}
+
+extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
+                                  const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq,
+                                  const float* xk, const float* xv, const float* cs, const float* wq,
+                                  const float* wk, void* o, float* lse, void* stream)
+{
+    const uint32_t dim = hq ? hq->dim : 0;
+    return rows_core(a, hq, hk, hv, in, out, xq, xk, xv, cs, wq, wk, o, lse,
+                     library_workspace(kWsRowTiles, "attention from rows"),
+                     library_workspace(dim == 128 ? kWsSplitK : kWsVtImages, "attention from rows"), stream);
+}
+
+extern "C" int mako_attn_fwd_rows_ws(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
+                                     const mako_heads_args* hv, mako_dtype in, mako_dtype out, const float* xq,
+                                     const float* xk, const float* xv, const float* cs, const float* wq,
+                                     const float* wk, void* o, float* lse, void* workspace, size_t workspace_bytes,
+                                     void* stream)
+{
+    const Workspace w = caller_workspace(workspace, workspace_bytes, "attention from rows");
+    const size_t tb = a && hq ? tiles_bytes(a, hq->dim) : 0;
+    return rows_core(a, hq, hk, hv, in, out, xq, xk, xv, cs, wq, wk, o, lse, w, w.at(tb), stream);
 }

@@ -27,12 +27,14 @@
 
 namespace mako {
 
-// attn_sparse64.hip: the r64 route for lists shared in groups of 4.
+// attn_sparse64.hip: the r64 route for lists shared in groups of 4 (valid null: taken as aligned), the bytes of its
+// pass table, and its launch (-1: the workspace could not be had, the error recorded).
 bool sparse64_fits(const mako_sparse_args* a, const void* valid);
+size_t sparse64_workspace(const mako_sparse_args* a);
 template <class T, class TO>
 int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                     const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map, float* lse,
-                    hipStream_t s);
+                    hipStream_t s, const Workspace& work);
 
 namespace {
 
@@ -776,9 +778,11 @@ extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, 
     return check_launch("cube_select");
 }
 
-extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q,
-                                const void* k, const void* v, void* o, const uint16_t* sel, const uint16_t* nsel,
-                                const uint8_t* valid, const int32_t* map, float* lse, void* stream)
+namespace {
+
+int attn_sparse_core(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q, const void* k,
+                     const void* v, void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
+                     const int32_t* map, float* lse, const Workspace& work, void* stream)
 {
     if (!a || !q || !k || !v || !o || !valid || !map || ((!sel || !nsel) && a->n_cubes))
         return fail(MAKO_EINVAL, "attention_sparse: a null argument");
@@ -821,13 +825,15 @@ extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_d
         const float sl = a->scale * kLog2e;
         int r;
         if (in == MAKO_BF16)
-            r = out == MAKO_F32 ? launch_sparse64<__bf16, float>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s)
-                                : launch_sparse64<__bf16, __bf16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s);
+            r = out == MAKO_F32
+                    ? launch_sparse64<__bf16, float>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s, work)
+                    : launch_sparse64<__bf16, __bf16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s, work);
         else
-            r = out == MAKO_F32 ? launch_sparse64<_Float16, float>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s)
-                                : launch_sparse64<_Float16, _Float16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s);
+            r = out == MAKO_F32
+                    ? launch_sparse64<_Float16, float>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s, work)
+                    : launch_sparse64<_Float16, _Float16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s, work);
         if (r < 0)
-            return fail(MAKO_EHIP, "attention_sparse: no device memory for the V^T images and the pass table");
+            return last_code() != MAKO_OK ? last_code() : MAKO_EHIP;
         return check_launch("attention_sparse");
     }
     if (in == MAKO_BF16) {
@@ -842,4 +848,28 @@ extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_d
             launch_sparse<_Float16, _Float16>(p, s);
     }
     return check_launch("attention_sparse");
+}
+
+}  // namespace
+
+extern "C" size_t mako_attn_sparse_workspace(const mako_sparse_args* a)
+{
+    return a && a->n_q && sparse64_fits(a, nullptr) ? sparse64_workspace(a) : 0;
+}
+
+extern "C" int mako_attn_sparse(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q,
+                                const void* k, const void* v, void* o, const uint16_t* sel, const uint16_t* nsel,
+                                const uint8_t* valid, const int32_t* map, float* lse, void* stream)
+{
+    return attn_sparse_core(a, in, out, q, k, v, o, sel, nsel, valid, map, lse,
+                            library_workspace(kWsPassTable, "attention_sparse"), stream);
+}
+
+extern "C" int mako_attn_sparse_ws(const mako_sparse_args* a, mako_dtype in, mako_dtype out, const void* q,
+                                   const void* k, const void* v, void* o, const uint16_t* sel, const uint16_t* nsel,
+                                   const uint8_t* valid, const int32_t* map, float* lse, void* workspace,
+                                   size_t workspace_bytes, void* stream)
+{
+    return attn_sparse_core(a, in, out, q, k, v, o, sel, nsel, valid, map, lse,
+                            caller_workspace(workspace, workspace_bytes, "attention_sparse"), stream);
 }

@@ -244,28 +244,41 @@ __global__ __launch_bounds__(256, 1) void flash_sparse_r64(const Sparse64Params 
 
 }  // namespace
 
-// Whether flash_sparse_r64 takes the call (see the file comment for the conditions).
+// Whether flash_sparse_r64 takes the call (see the file comment for the conditions; valid null: taken as aligned).
 bool sparse64_fits(const mako_sparse_args* a, const void* valid)
 {
-    const uint32_t group = a->heads / a->kv_heads;
-    return a->sel_heads == a->kv_heads && group % 4 == 0 && a->dense0 % 64 == 0 &&
+    const uint32_t group = a->kv_heads ? a->heads / a->kv_heads : 0u;
+    return a->kv_heads && a->sel_heads == a->kv_heads && group % 4 == 0 && a->dense0 % 64 == 0 &&
            (reinterpret_cast<uintptr_t>(valid) & 15u) == 0 && (uint64_t)a->q_pad * 256 < (1ull << 31) &&
            (uint64_t)a->heads * a->q_pad * 4 < (1ull << 32) && (uint64_t)a->k_pad * 256 < (1ull << 32);
 }
 
-// sparse_prep then flash_sparse_r64 on stream s, the pass table in the stream's cached workspace. Returns 1 when
-// launched, -1 when the workspace could not be had.
-template <class T, class TO>
-int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
-                    const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map, float* lse,
-                    hipStream_t s)
+// Entries of a pass-table list: the passes a query tile can have, and four past them (the stream reads ahead).
+uint32_t pass_entries(const mako_sparse_args* a)
 {
     const uint32_t n_qt = (a->n_q + 63) / 64;
     const uint32_t nd_c = a->dense1 > a->dense0 ? (a->dense1 - a->dense0 + 63) / 64 : 0u;
     const uint32_t nd_l = n_qt > a->n_cubes ? (a->n_k + 63) / 64 : 0u;
-    const uint32_t n_ent = std::max(a->max_sel + nd_c, nd_l) + 4;
+    return std::max(a->max_sel + nd_c, nd_l) + 4;
+}
+
+// The pass table's bytes: 16 an entry, an entry list a (kv head, query tile).
+size_t sparse64_workspace(const mako_sparse_args* a)
+{
+    return (size_t)a->kv_heads * ((a->n_q + 63) / 64) * pass_entries(a) * 16;
+}
+
+// sparse_prep then flash_sparse_r64 on stream s, the pass table in the call's workspace (work). Returns 1 when
+// launched, -1 when the workspace could not be had (the error recorded).
+template <class T, class TO>
+int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+                    const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map, float* lse,
+                    hipStream_t s, const Workspace& work)
+{
+    const uint32_t n_qt = (a->n_q + 63) / 64;
+    const uint32_t n_ent = pass_entries(a);
     const size_t entries = (size_t)a->kv_heads * n_qt * n_ent;
-    u32x4* table = static_cast<u32x4*>(stream_workspace(kWsVtImages, entries * 16, s));
+    u32x4* table = static_cast<u32x4*>(work.get(entries * 16, s));
     if (!table)
         return -1;
     const SparsePlan plan{sel, nsel, valid, table, a->kv_heads, n_qt, n_ent, a->n_cubes, a->max_sel, a->dense0,
@@ -281,17 +294,14 @@ int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, 
     return 1;
 }
 
-template int launch_sparse64<__bf16, float>(const mako_sparse_args*, float, const void*, const void*, const void*,
-                                            void*, const uint16_t*, const uint16_t*, const uint8_t*, const int32_t*,
-                                            float*, hipStream_t);
-template int launch_sparse64<__bf16, __bf16>(const mako_sparse_args*, float, const void*, const void*, const void*,
-                                             void*, const uint16_t*, const uint16_t*, const uint8_t*, const int32_t*,
-                                             float*, hipStream_t);
-template int launch_sparse64<_Float16, float>(const mako_sparse_args*, float, const void*, const void*, const void*,
-                                              void*, const uint16_t*, const uint16_t*, const uint8_t*,
-                                              const int32_t*, float*, hipStream_t);
-template int launch_sparse64<_Float16, _Float16>(const mako_sparse_args*, float, const void*, const void*,
-                                                 const void*, void*, const uint16_t*, const uint16_t*,
-                                                 const uint8_t*, const int32_t*, float*, hipStream_t);
+#define MAKO_SPARSE64_INSTANCE(T, TO)                                                                            \
+    template int launch_sparse64<T, TO>(const mako_sparse_args*, float, const void*, const void*, const void*, void*, \
+                                        const uint16_t*, const uint16_t*, const uint8_t*, const int32_t*, float*,    \
+                                        hipStream_t, const Workspace&);
+MAKO_SPARSE64_INSTANCE(__bf16, float)
+MAKO_SPARSE64_INSTANCE(__bf16, __bf16)
+MAKO_SPARSE64_INSTANCE(_Float16, float)
+MAKO_SPARSE64_INSTANCE(_Float16, _Float16)
+#undef MAKO_SPARSE64_INSTANCE
 
 }  // namespace mako

@@ -180,6 +180,8 @@ namespace mako {
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Clears the message; returns MAKO_OK.
 int ok();
+// The code of the calling thread's last fail() (MAKO_OK after ok()).
+int last_code();
 // MAKO_OK, or MAKO_EHIP with the launch error recorded (hipGetLastError after a launch).
 int check_launch(const char* what);
 // Compute units of the current device (cached per device and thread); 0 when there is none.
@@ -187,10 +189,42 @@ uint32_t device_cus();
 
 // Workspaces the library keeps for callers that pass none: one buffer per (purpose, device, stream), grown (stream-
 // ordered) when a call needs more. Calls on one stream are ordered by the stream and calls on different streams use
-// different buffers, so no call waits on the host or inserts a GPU-side wait. A stream's buffers stay with its handle
-// (hipStreamDestroy waits for the stream's work, so a handle reused later may take them over). Returns null, with
-// nothing allocated, when the allocation fails.
-enum WorkspacePurpose { kWsVtImages = 0, kWsSplitK = 1, kWsRowTiles = 2 };
-void* stream_workspace(WorkspacePurpose purpose, size_t bytes, hipStream_t s);
+// different buffers, so no call waits on the host or inserts a GPU-side wait. A stream's buffers stay until
+// mako_attn_release(stream) frees them (a stream destroyed without it leaves them to a later stream with its
+// handle). Returns null, with nothing allocated and the error recorded, when the allocation fails (MAKO_EHIP) or
+// when the stream is capturing a graph and the buffer would have to grow (MAKO_EWORKSPACE: an allocation in a
+// capture would belong to the graph).
+enum WorkspacePurpose { kWsVtImages = 0, kWsSplitK = 1, kWsRowTiles = 2, kWsPassTable = 3, kWsPurposes = 4 };
+void* stream_workspace(WorkspacePurpose purpose, size_t bytes, hipStream_t s, const char* what);
+
+// A call's workspace: the caller's buffer (given, from an entry point that takes one: never allocates) or the
+// library's buffer for (purpose, device, stream). get(need) returns memory of at least need bytes, or null with the
+// error recorded (MAKO_EWORKSPACE when the caller's buffer is smaller, else as stream_workspace). Slices of a given
+// workspace are taken with at(offset).
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    bool given = false;
+    WorkspacePurpose purpose = kWsVtImages;
+    const char* what = "";
+    void* get(size_t need, hipStream_t s) const;
+    Workspace at(size_t offset) const;
+};
+inline Workspace caller_workspace(void* p, size_t bytes, const char* what)
+{
+    Workspace w;
+    w.ptr = p;
+    w.bytes = bytes;
+    w.given = true;
+    w.what = what;
+    return w;
+}
+inline Workspace library_workspace(WorkspacePurpose purpose, const char* what)
+{
+    Workspace w;
+    w.purpose = purpose;
+    w.what = what;
+    return w;
+}
 
 }  // namespace mako

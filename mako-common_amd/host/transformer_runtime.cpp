@@ -86,10 +86,14 @@ void TransformerRuntime::attention(gpu::Encoder*& enc, gpu::Buffer* q, gpu::Buff
     const mako_attn_args a{n_q, q_pad, n_k, k_pad, n_heads, kv_heads, q_pos0, block, n_heads * dim,
                            1.0f / std::sqrt(float(dim))};
     const char* label = dim == 64 ? "flash_fwd_64" : dim == 128 ? "flash_fwd_128" : "flash_fwd_256";
+    // the split-K partials (a few rows) or the V^T images (heads of 256) live in Runtime-owned scratch
+    const size_t need = mako_attn_fwd_workspace(&a, dim);
+    gpu::Buffer* ws = need ? scratch("attn_fwd", need) : nullptr;
     before(enc);
     for (int r = repeats(label); r > 0; --r)
-        check(mako_attn_fwd(&a, dim, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
-                            opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
+        check(mako_attn_fwd_ws(&a, dim, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
+                               opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, ws ? ws->ptr : nullptr,
+                               ws ? ws->bytes : 0, enc->stream));
     after(enc, label);
 }
 
@@ -110,10 +114,13 @@ void TransformerRuntime::attention_rows(gpu::Encoder*& enc, gpu::Buffer* xq, uin
     const mako_attn_args a{n_q, 0, n_k, 0, n_heads, kv_heads, q_pos0, block, n_heads * dim,
                            1.0f / std::sqrt(float(dim))};
     const auto f = [](gpu::Buffer* b) { return b ? static_cast<const float*>(b->ptr) : nullptr; };
+    const size_t need = mako_attn_fwd_rows_workspace(&a, dim);
+    gpu::Buffer* ws = need ? scratch("attn_rows", need) : nullptr;
     before(enc);
     for (int r = repeats("attention_rows"); r > 0; --r)
-        check(mako_attn_fwd_rows(&a, &hq, &hk, &hv, opt.in, opt.out, f(xq), f(xk), f(xv), f(cs), f(wq), f(wk),
-                                 o->ptr, opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
+        check(mako_attn_fwd_rows_ws(&a, &hq, &hk, &hv, opt.in, opt.out, f(xq), f(xk), f(xv), f(cs), f(wq), f(wk),
+                                    o->ptr, opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr,
+                                    ws ? ws->ptr : nullptr, ws ? ws->bytes : 0, enc->stream));
     after(enc, "attention_rows");
 }
 
@@ -149,13 +156,16 @@ void TransformerRuntime::attention_sparse(gpu::Encoder*& enc, gpu::Buffer* q, gp
     const mako_sparse_args a{n_q, q_pad, n_k, k_pad, heads, kv_heads, width, 1.0f / std::sqrt(float(kHeadDim)),
                              n_cubes, std::min(topk, n_cubes), dense0, dense1, opt.causal ? 1u : 0u,
                              opt.sel_per_kv_head ? kv_heads : heads};
+    const size_t need = mako_attn_sparse_workspace(&a);
+    gpu::Buffer* ws = need ? scratch("attn_sparse", need) : nullptr;
     before(enc);
     for (int r = repeats("flash_sparse_128"); r > 0; --r)
-        check(mako_attn_sparse(&a, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
-                               sel ? static_cast<const uint16_t*>(sel->ptr) : nullptr,
-                               nsel ? static_cast<const uint16_t*>(nsel->ptr) : nullptr,
-                               static_cast<const uint8_t*>(valid->ptr), static_cast<const int32_t*>(map->ptr),
-                               opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, enc->stream));
+        check(mako_attn_sparse_ws(&a, opt.in, opt.out, q->ptr, k->ptr, v->ptr, o->ptr,
+                                  sel ? static_cast<const uint16_t*>(sel->ptr) : nullptr,
+                                  nsel ? static_cast<const uint16_t*>(nsel->ptr) : nullptr,
+                                  static_cast<const uint8_t*>(valid->ptr), static_cast<const int32_t*>(map->ptr),
+                                  opt.lse ? static_cast<float*>(opt.lse->ptr) : nullptr, ws ? ws->ptr : nullptr,
+                                  ws ? ws->bytes : 0, enc->stream));
     after(enc, "flash_sparse_128");
 }
 

@@ -18,7 +18,9 @@ EXPORTS = ("mako_attn_abi_version", "mako_last_error", "mako_attn_fwd", "mako_cu
            "mako_cube_select", "mako_attn_sparse", "mako_attn_decode_workspace", "mako_attn_decode",
            "mako_attn_decode_noalloc", "mako_heads", "mako_attn_fwd_rows",
            "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots", "mako_proj_bf16",
-           "mako_kda_scan")
+           "mako_kda_scan", "mako_attn_fwd_workspace", "mako_attn_fwd_ws", "mako_attn_sparse_workspace",
+           "mako_attn_sparse_ws", "mako_attn_fwd_rows_workspace", "mako_attn_fwd_rows_ws", "mako_attn_release",
+           "mako_attn_held_bytes")
 
 
 class AttnArgs(ctypes.Structure):
@@ -99,8 +101,22 @@ def lib():
         L.mako_idx_dots.argtypes = [ctypes.POINTER(IdxDotArgs), U32, P, P, P, P]
         L.mako_proj_bf16.argtypes = [ctypes.POINTER(GemmArgs), I, I, P, P, P, P]
         L.mako_kda_scan.argtypes = [ctypes.POINTER(ScanArgs)] + [P] * 9
+        L.mako_attn_fwd_workspace.argtypes = [ctypes.POINTER(AttnArgs), U32]
+        L.mako_attn_fwd_workspace.restype = SZ
+        L.mako_attn_fwd_ws.argtypes = [ctypes.POINTER(AttnArgs), U32, I, I, P, P, P, P, P, P, SZ, P]
+        L.mako_attn_sparse_workspace.argtypes = [ctypes.POINTER(SparseArgs)]
+        L.mako_attn_sparse_workspace.restype = SZ
+        L.mako_attn_sparse_ws.argtypes = [ctypes.POINTER(SparseArgs), I, I] + [P] * 10 + [SZ, P]
+        L.mako_attn_fwd_rows_workspace.argtypes = [ctypes.POINTER(AttnArgs), U32]
+        L.mako_attn_fwd_rows_workspace.restype = SZ
+        L.mako_attn_fwd_rows_ws.argtypes = [ctypes.POINTER(AttnArgs)] + [ctypes.POINTER(HeadsArgs)] * 3 + \
+            [I, I] + [P] * 9 + [SZ, P]
+        L.mako_attn_release.argtypes = [P]
+        L.mako_attn_held_bytes.argtypes = []
+        L.mako_attn_held_bytes.restype = SZ
         for name in ("mako_attn_fwd", "mako_cube_select", "mako_attn_sparse", "mako_attn_decode",
-                     "mako_attn_decode_noalloc", "mako_heads", "mako_attn_fwd_rows",
+                     "mako_attn_decode_noalloc", "mako_heads", "mako_attn_fwd_rows", "mako_attn_fwd_ws",
+                     "mako_attn_sparse_ws", "mako_attn_fwd_rows_ws", "mako_attn_release",
                      "mako_attn_pv", "mako_attn_gather_scores", "mako_attn_gather_pv", "mako_idx_dots",
                      "mako_proj_bf16", "mako_kda_scan"):
             getattr(L, name).restype = I
@@ -131,14 +147,46 @@ def dtype_code(t):
     return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[t.dtype]
 
 
-def attn_fwd(q, k, v, o, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, lse=None, scale=None,
-             width=None, stream=None):
-    """mako_attn_fwd on torch tensors q [heads][q_pad][dim], k, v [kv_heads][k_pad][dim], o [n_q][width]."""
+LIBRARY = "library"  # workspace= default: the entry point without a workspace argument (the library keeps its own)
+
+
+def _nbytes(t):
+    return 0 if t is None else t.numel() * t.element_size()
+
+
+def attn_args(*, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, scale=None, width=None):
     width = heads * dim if width is None else width
     scale = 1.0 / dim ** 0.5 if scale is None else scale
-    a = AttnArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block & U32_MAX, width, scale)
-    _check(lib().mako_attn_fwd(ctypes.byref(a), dim, dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v),
-                               _ptr(o), _ptr(lse), _stream(stream)))
+    return AttnArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block & U32_MAX, width, scale)
+
+
+def attn_fwd_workspace(*, dim, **kw):
+    """mako_attn_fwd_workspace for the call attn_fwd would make with these arguments."""
+    return lib().mako_attn_fwd_workspace(ctypes.byref(attn_args(dim=dim, **kw)), dim)
+
+
+def attn_fwd(q, k, v, o, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, q_pos0, block, dim, lse=None, scale=None,
+             width=None, stream=None, workspace=LIBRARY):
+    """mako_attn_fwd on torch tensors q [heads][q_pad][dim], k, v [kv_heads][k_pad][dim], o [n_q][width]; with
+    workspace (a tensor, or None for none), mako_attn_fwd_ws."""
+    a = attn_args(n_q=n_q, q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads, kv_heads=kv_heads, q_pos0=q_pos0,
+                  block=block, dim=dim, scale=scale, width=width)
+    if isinstance(workspace, str):
+        _check(lib().mako_attn_fwd(ctypes.byref(a), dim, dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v),
+                                   _ptr(o), _ptr(lse), _stream(stream)))
+    else:
+        _check(lib().mako_attn_fwd_ws(ctypes.byref(a), dim, dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v),
+                                      _ptr(o), _ptr(lse), _ptr(workspace), _nbytes(workspace), _stream(stream)))
+
+
+def release(stream=None):
+    """mako_attn_release: frees the workspaces the library keeps for the stream."""
+    _check(lib().mako_attn_release(_stream(stream)))
+
+
+def held_bytes():
+    """mako_attn_held_bytes: bytes of the workspaces the library keeps on the current device."""
+    return lib().mako_attn_held_bytes()
 
 
 def cube_select_workspace(heads, n_cubes):
@@ -153,14 +201,28 @@ def cube_select(q, k, cnt, sel, nsel, workspace, *, heads, q_pad, k_pad, n_cubes
                                   _stream(stream)))
 
 
-def attn_sparse(q, k, v, o, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, n_cubes, max_sel,
-                dense0, dense1, causal=0, sel_heads=None, width=None, lse=None, stream=None):
+def sparse_args(*, n_q, q_pad, n_k, k_pad, heads, kv_heads, n_cubes, max_sel, dense0, dense1, causal=0,
+                sel_heads=None, width=None):
     width = heads * 128 if width is None else width
     sel_heads = heads if sel_heads is None else sel_heads
-    a = SparseArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, width, 1.0 / 128 ** 0.5, n_cubes, max_sel, dense0,
-                   dense1, causal, sel_heads)
-    _check(lib().mako_attn_sparse(ctypes.byref(a), dtype_code(q), dtype_code(o), _ptr(q), _ptr(k), _ptr(v), _ptr(o),
-                                  _ptr(sel), _ptr(nsel), _ptr(valid), _ptr(map_), _ptr(lse), _stream(stream)))
+    return SparseArgs(n_q, q_pad, n_k, k_pad, heads, kv_heads, width, 1.0 / 128 ** 0.5, n_cubes, max_sel, dense0,
+                      dense1, causal, sel_heads)
+
+
+def attn_sparse_workspace(**kw):
+    return lib().mako_attn_sparse_workspace(ctypes.byref(sparse_args(**kw)))
+
+
+def attn_sparse(q, k, v, o, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, heads, kv_heads, n_cubes, max_sel,
+                dense0, dense1, causal=0, sel_heads=None, width=None, lse=None, stream=None, workspace=LIBRARY):
+    a = sparse_args(n_q=n_q, q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads, kv_heads=kv_heads, n_cubes=n_cubes,
+                    max_sel=max_sel, dense0=dense0, dense1=dense1, causal=causal, sel_heads=sel_heads, width=width)
+    ptrs = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(sel), _ptr(nsel), _ptr(valid), _ptr(map_), _ptr(lse))
+    if isinstance(workspace, str):
+        _check(lib().mako_attn_sparse(ctypes.byref(a), dtype_code(q), dtype_code(o), *ptrs, _stream(stream)))
+    else:
+        _check(lib().mako_attn_sparse_ws(ctypes.byref(a), dtype_code(q), dtype_code(o), *ptrs, _ptr(workspace),
+                                         _nbytes(workspace), _stream(stream)))
 
 
 def decode_args(*, batch, heads, kv_heads, dim, cap, max_ctx, split=0, scale=None):
@@ -219,19 +281,28 @@ def heads(x, y, *, rows, ld, col0, stride, dim, heads, n_pad, row0=0, rope=0, ro
                             _stream(stream)))
 
 
+def attn_fwd_rows_workspace(*, n_q, n_k, heads, kv_heads, q_pos0, block, dim, scale=None, width=None):
+    a = attn_args(n_q=n_q, q_pad=0, n_k=n_k, k_pad=0, heads=heads, kv_heads=kv_heads, q_pos0=q_pos0, block=block,
+                  dim=dim, scale=scale, width=width)
+    return lib().mako_attn_fwd_rows_workspace(ctypes.byref(a), dim)
+
+
 def attn_fwd_rows(xq, xk, xv, o, hq, hk, hv, *, n_q, n_k, heads, kv_heads, q_pos0, block, in_dtype, cs=None,
-                  wq=None, wk=None, lse=None, scale=None, width=None, stream=None):
+                  wq=None, wk=None, lse=None, scale=None, width=None, stream=None, workspace=LIBRARY):
     """mako_attn_fwd_rows on torch tensors: xq, xk, xv float32 rows; hq, hk, hv dicts of mako_heads_args fields
-    (rows, ld, col0, stride, dim, heads, rope, rot, eps); o [n_q][width] of float32 or in_dtype (F16 / BF16)."""
+    (rows, ld, col0, stride, dim, heads, rope, rot, eps); o [n_q][width] of float32 or in_dtype (F16 / BF16); with
+    workspace (a tensor, or None), mako_attn_fwd_rows_ws."""
     dim = hq["dim"]
-    width = heads * dim if width is None else width
-    scale = 1.0 / dim ** 0.5 if scale is None else scale
-    a = AttnArgs(n_q, 0, n_k, 0, heads, kv_heads, q_pos0, block & U32_MAX, width, scale)
+    a = attn_args(n_q=n_q, q_pad=0, n_k=n_k, k_pad=0, heads=heads, kv_heads=kv_heads, q_pos0=q_pos0, block=block,
+                  dim=dim, scale=scale, width=width)
     fields = ("rows", "ld", "col0", "stride", "dim", "heads", "n_pad", "row0", "rope", "rot", "eps", "clear")
     hs = [HeadsArgs(*[h.get(f, 0) for f in fields]) for h in (hq, hk, hv)]
-    _check(lib().mako_attn_fwd_rows(ctypes.byref(a), *[ctypes.byref(h) for h in hs], in_dtype, dtype_code(o),
-                                    _ptr(xq), _ptr(xk), _ptr(xv), _ptr(cs), _ptr(wq), _ptr(wk), _ptr(o), _ptr(lse),
-                                    _stream(stream)))
+    args = [ctypes.byref(a), *[ctypes.byref(h) for h in hs], in_dtype, dtype_code(o), _ptr(xq), _ptr(xk), _ptr(xv),
+            _ptr(cs), _ptr(wq), _ptr(wk), _ptr(o), _ptr(lse)]
+    if isinstance(workspace, str):
+        _check(lib().mako_attn_fwd_rows(*args, _stream(stream)))
+    else:
+        _check(lib().mako_attn_fwd_rows_ws(*args, _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
 def attn_pv(p, kv, partial, *, heads, dim, n_kv, keys_per_split, stream=None):

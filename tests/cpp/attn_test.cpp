@@ -43,6 +43,7 @@ public:
     using TransformerRuntime::attention;
     using TransformerRuntime::attention_rows;
     using TransformerRuntime::attention_decode;
+    using TransformerRuntime::attention_sparse;
     using TransformerRuntime::heads;
     using TransformerRuntime::heads_partial;
     using TransformerRuntime::proj;
@@ -492,6 +493,46 @@ int main()
         for (size_t i = 0; i < want_s.size(); ++i)
             bad += !(std::fabs(got_s[i] - want_s[i]) <= 2e-5 + 1e-4 * std::fabs(want_s[i]));
         check(bad == 0, "kda_scan, 4 heads over 100 tokens: " + std::to_string(bad) + " values out of tolerance");
+    }
+    // Runtime-owned scratch: every workspace the attention calls need is the Runtime's named scratch (the
+    // reference's Runtime owns its scratch, src/gpu/runtime.cpp:117-125): after a warm-up, repeated calls allocate
+    // nothing (scratch_bytes() stable), and the library holds no buffer of its own.
+    {
+        const uint32_t H = 32, KV = 8, D = 128, S = 1024;
+        const auto q = random_tile(size_t(H) * S * D, ORACLE_BF16), k = random_tile(size_t(KV) * S * D, ORACLE_BF16);
+        auto qb = put(h, "wq", q), kb = put(h, "wk", k), vb = put(h, "wv", k);
+        auto ob = h.scratch("wo", size_t(S) * H * D * 4);
+        mako::models::AttnOptions opt;
+        opt.in = MAKO_BF16;
+        const uint32_t D2 = 256, H2 = 4, KV2 = 2, S2 = 200;
+        const auto q2 = random_tile(size_t(H2) * 256 * D2, ORACLE_BF16);
+        auto q2b = put(h, "wq2", q2), k2b = put(h, "wk2", q2);
+        // the sparse r64 route: lists per kv head, 4 query heads each; every cube sees itself
+        const uint32_t cubes = S / 64;
+        std::vector<uint16_t> sel(size_t(KV) * cubes), nsel(size_t(KV) * cubes, 1);
+        for (uint32_t i = 0; i < KV * cubes; ++i)
+            sel[i] = uint16_t(i % cubes);
+        std::vector<uint8_t> valid(S, 1);
+        std::vector<int32_t> map(S);
+        for (uint32_t i = 0; i < S; ++i)
+            map[i] = int32_t(i);
+        auto selb = put(h, "wsel", sel), nselb = put(h, "wnsel", nsel), validb = put(h, "wvalid", valid);
+        auto mapb = put(h, "wmap", map);
+        mako::models::AttnOptions sopt = opt;
+        sopt.sel_per_kv_head = true;
+        uint64_t bytes[3] = {0, 0, 0};
+        for (int round = 0; round < 3; ++round) {
+            auto* enc = h.encoder();
+            h.attention(enc, qb, kb, vb, ob, 2, 64, S, S, H, KV, S - 2, UINT32_MAX, D, opt);   // split-K partials
+            h.attention(enc, q2b, k2b, k2b, ob, S2, 256, S2, 256, H2, KV2, 0, UINT32_MAX, D2, opt);  // V^T images
+            h.attention_sparse(enc, qb, kb, vb, ob, S, S, S, S, H, KV, H * D, cubes, 1, S, S, selb, nselb, validb,
+                               mapb, sopt);                                                       // pass table
+            h.finish(enc);
+            bytes[round] = h.scratch_bytes();
+        }
+        check(bytes[1] == bytes[0] && bytes[2] == bytes[0] && mako_attn_held_bytes() == 0,
+              "Runtime-owned scratch: scratch bytes " + std::to_string(bytes[0]) + " / " + std::to_string(bytes[1]) +
+                  " / " + std::to_string(bytes[2]) + ", library-held " + std::to_string(mako_attn_held_bytes()));
     }
     for (const auto& kt : h.kernel_times())
         std::printf("  %-20s %3u launches %8.3f ms\n", kt.kernel.c_str(), kt.count, kt.ms);

@@ -286,3 +286,25 @@ def scan_rc(**kw):
 def test_kda_scan_refuses(kw, code, msg):
     rc, err = scan_rc(**kw)
     assert rc == code and msg in err, (rc, err)
+
+
+def test_workspace_entry_points_refuse_a_short_workspace():
+    """The *_ws entry points validate before the workspace; a workspace smaller than the call's query is refused
+    with MAKO_EWORKSPACE before any launch (the split-K route of a one-row call needs one)."""
+    args = M.attn_args(n_q=1, q_pad=64, n_k=4096, k_pad=4096, heads=32, kv_heads=8, q_pos0=4095, block=M.U32_MAX,
+                       dim=128)
+    need = M.lib().mako_attn_fwd_workspace(ctypes.byref(args), 128)
+    if need == 0:
+        pytest.skip("no GPU to size the split-K route (the query needs the compute-unit count)")
+    rc = M.lib().mako_attn_fwd_ws(ctypes.byref(args), 128, M.BF16, M.BF16, *([FAKE] * 4), None, FAKE, need - 1,
+                                  None)
+    assert rc == M.EWORKSPACE and "workspace" in M.lib().mako_last_error().decode()
+
+
+def test_workspace_queries_without_a_device():
+    """The prefill routes need no workspace: the queries say 0 for them (no device needed)."""
+    args = M.attn_args(n_q=4096, q_pad=4096, n_k=4096, k_pad=4096, heads=32, kv_heads=8, q_pos0=0, block=M.U32_MAX,
+                       dim=128)
+    assert M.lib().mako_attn_fwd_workspace(ctypes.byref(args), 128) == 0
+    assert M.lib().mako_attn_fwd_workspace(ctypes.byref(args), 64) == 0
+    assert M.lib().mako_attn_held_bytes() == 0

@@ -95,9 +95,9 @@ def test_split_invariance_and_dense_agreement():
         np.testing.assert_allclose(outs[1][1][b], lse.cpu().numpy()[:, 0], rtol=0, atol=1e-4)
 
 
-def test_batch16_contexts_1k_to_32k_sampled():
+def test_batch16_contexts_1k_to_32k():
     """Batch 16, 32 query heads over 8 kv heads, D 128, contexts drawn uniformly from [1024, 32768] (seed 2026),
-    f16 cache and query, f32 out: sampled (sequence, head) pairs against the oracle; every row finite."""
+    f16 cache and query, f32 out: every (sequence, head) pair, all 512, against the oracle."""
     batch, heads, kv = 16, 32, 8
     ctx = np.random.default_rng(2026).integers(1024, 32769, batch).astype(np.uint32)
     cap = int(ctx.max())
@@ -108,12 +108,12 @@ def test_batch16_contexts_1k_to_32k_sampled():
     print("decode batch 16", flush=True)
     o, lse = run_decode(q, k, v, ctx, batch=batch, heads=heads, kv_heads=kv, cap=cap)
     assert np.all(np.isfinite(o)) and np.all(np.isfinite(lse))
-    rng = np.random.default_rng(1)
-    pairs = np.stack([np.arange(batch).repeat(3), rng.integers(0, heads, 3 * batch)], 1).astype(np.uint32)
+    pairs = np.stack(np.meshgrid(np.arange(batch), np.arange(heads), indexing="ij"), -1).reshape(-1, 2)
+    pairs = pairs.astype(np.uint32)
     bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
     want_o, want_l = O.attn_decode_rows(bits(q), bits(k), bits(v), ctx, pairs, batch=batch, heads=heads,
                                         kv_heads=kv, dim=128, cap=cap, dtype=O.F16)
     got_o = np.stack([o[b, h * 128:(h + 1) * 128] for b, h in pairs])
-    G.assert_attn_close(got_o, want_o, "sampled output")
-    G.assert_rows_l2(got_o, want_o, "sampled output", 128)
-    G.assert_lse_close(np.array([lse[b, h] for b, h in pairs]), want_l, "sampled lse")
+    G.assert_attn_close(got_o, want_o, "output")
+    G.assert_rows_l2(got_o, want_o, "output", 128)
+    G.assert_lse_close(np.array([lse[b, h] for b, h in pairs]), want_l, "lse")

@@ -57,14 +57,19 @@ def test_noalloc_matches_workspace_entry_twice():
 
 
 def test_noalloc_refuses_partials_past_the_scratch():
-    # group 32 over 64 sequences: (resident waves + 64) pieces x 32 heads x 520 bytes exceeds 16 MiB on any GPU
-    # with at least 64 compute units; the refusal comes before any launch.
-    a = M.decode_args(batch=64, heads=32, kv_heads=1, dim=128, cap=1024, max_ctx=1024)
-    assert M.decode_workspace(a) > M.DECODE_SCRATCH_BYTES
-    q = torch.zeros((64, 32, 128), dtype=torch.float16, device="cuda")
-    k = torch.zeros((64, 1, 1024, 128), dtype=torch.float16, device="cuda")  # the full cache, in case of a launch
-    ctx = torch.ones(64, dtype=torch.int32, device="cuda")
-    o = torch.empty((64, 32 * 128), dtype=torch.float32, device="cuda")
+    # group 32: the partials grow with the batch ((resident waves + pieces) x 32 heads x 520 bytes), so the batch
+    # doubles until they exceed the static scratch on this GPU; the refusal comes before any launch.
+    batch = 64
+    while True:
+        a = M.decode_args(batch=batch, heads=32, kv_heads=1, dim=128, cap=1024, max_ctx=1024)
+        if M.decode_workspace(a) > M.DECODE_SCRATCH_BYTES:
+            break
+        batch *= 2
+        assert batch <= 1 << 16, "the partials never exceed the static scratch"
+    q = torch.zeros((batch, 32, 128), dtype=torch.float16, device="cuda")
+    k = torch.zeros((batch, 1, 1024, 128), dtype=torch.float16, device="cuda")  # the full cache, in case of a launch
+    ctx = torch.ones(batch, dtype=torch.int32, device="cuda")
+    o = torch.empty((batch, 32 * 128), dtype=torch.float32, device="cuda")
     with pytest.raises(M.MakoError) as e:
         M.attn_decode_noalloc(a, q, k, k, ctx, o)
     assert e.value.code == M.EWORKSPACE and "static scratch" in str(e.value)
