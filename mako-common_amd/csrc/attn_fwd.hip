@@ -27,6 +27,8 @@
 // flash_fwd (heads of 64 and 128) runs 8 waves in two groups that alternate matrix and vector phases; the
 // running maximum's exchange between the two halves of a wave happens only when some lane's maximum passes its
 // threshold. flash_fwd_wide (heads of 256) runs 4 waves with double-buffered tiles.
+#include <cstdlib>
+
 #include "device.hpp"
 
 namespace mako {
@@ -638,12 +640,21 @@ int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, co
 
 namespace {
 
+// MAKO_ATTN_FALLBACK=1 in the environment sends every dense call that reaches the prefill kernels to flash_fwd /
+// flash_fwd_wide, the kernels otherwise taken only past the r64 / d256 kernels' 32-bit offsets (calls of several GB),
+// so that tests reach them at ordinary sizes. Read at each call.
+bool force_fallback()
+{
+    const char* e = std::getenv("MAKO_ATTN_FALLBACK");
+    return e && e[0] == '1';
+}
+
 // false when flash_fwd_d256's workspace could not be had (nothing was launched, the error recorded).
 template <class T, class TO>
 bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 grid, hipStream_t s,
               const Workspace& work)
 {
-    {
+    if (!force_fallback()) {
         const int r = dim == 128 ? launch_fwd64<T, TO, 128>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
                       : dim == 64 ? launch_fwd64<T, TO, 64>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
                                   : launch_fwd_d256<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s, nullptr,

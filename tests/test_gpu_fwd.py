@@ -109,6 +109,39 @@ def test_sweep(case):
     assert np.all(o[n_q:] == 12288.0), "rows past n_q were written"
 
 
+@pytest.mark.parametrize("case", [c for c in SWEEP if not (c[2] == 128 and c[3] * (c[0] // c[1]) <= 64)],
+                         ids=lambda c: "h{}kv{}d{}q{}k{}p{}b{}".format(*c[:6], "c" if c[6] == U32 else c[6]))
+def test_sweep_fallback_kernels(case, monkeypatch):
+    """The sweep through flash_fwd / flash_fwd_wide, which calls past the r64 / d256 kernels' 32-bit offsets take
+    (MAKO_ATTN_FALLBACK=1 sends every call there; the split-K route of a few rows is not affected)."""
+    monkeypatch.setenv("MAKO_ATTN_FALLBACK", "1")
+    test_sweep(case)
+
+
+def test_wide_output_rows_take_the_fallback_kernel():
+    """o rows of 3.5M f32 (14 MB a row: 320 rows of o at this grid pass 2^32 bytes) leave flash_fwd_r64's 32-bit
+    offsets, so the call takes flash_fwd by itself; sampled rows against the oracle, the columns past the heads
+    untouched."""
+    heads, kv, dim, S = 2, 2, 128, 100
+    width = 3_500_000
+    rng = np.random.default_rng(77)
+    qb = G.randn_bits(rng, (heads, 128, dim), O.BF16)
+    kb = G.randn_bits(rng, (kv, 128, dim), O.BF16)
+    vb = G.randn_bits(rng, (kv, 128, dim), O.BF16)
+    q, k, v = G.to_dev(qb, O.BF16), G.to_dev(kb, O.BF16), G.to_dev(vb, O.BF16)
+    o = torch.full((S, width), 7.0, dtype=torch.float32, device="cuda")
+    print("wide o rows (flash_fwd)", flush=True)
+    M.attn_fwd(q, k, v, o, n_q=S, q_pad=128, n_k=S, k_pad=128, heads=heads, kv_heads=kv, q_pos0=0, block=U32,
+               dim=dim, width=width)
+    torch.cuda.synchronize()
+    got = o[:, :heads * dim].cpu().numpy().astype(np.float64)
+    assert bool((o[:, heads * dim:heads * dim + 1024] == 7.0).all())
+    del o
+    want, _ = O.attn_dense(qb, kb, vb, n_q=S, q_pad=128, n_k=S, k_pad=128, heads=heads, kv_heads=kv, q_pos0=0,
+                           block=U32, dim=dim, dtype=O.BF16)
+    G.assert_attn_close(got, want, "wide rows")
+
+
 def every_tile(rng, heads, S):
     """One random row of every (head, 64-row query tile): each workgroup item of the launch is compared."""
     h, t = np.meshgrid(np.arange(heads), np.arange(S // 64), indexing="ij")
