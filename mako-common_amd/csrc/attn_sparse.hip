@@ -10,7 +10,7 @@
 //   fused multiply-add), so the scores, and with them every comparison the top-k makes, are the check's bit for bit.
 // * cube_topk: the `local` cubes {qc, qc - stride, qc + stride} (those in range) first, their scores taken out of
 //   the running, then repeated argmax, the larger score first and the smaller index on ties; nsel = min(topk, n)
-//   (:957-1027).
+//   (:957-1027). Here one wave per (query cube, head) with the scores in registers and a shuffle argmax a pick.
 // * attention_sparse: query tile t (64 rows) < n_cubes visits the key cubes sel lists for it (64 keys each), then
 //   the dense rows [dense0, dense1); a later tile visits [0, n_k); keys with valid[j] == 0 are masked (:1079-1113);
 //   query row r's output goes to o row map[r], dropped when map[r] < 0 or r >= n_q (:1173-1184). Two fields the
@@ -323,70 +323,79 @@ __global__ __launch_bounds__(256) void cube_scores(const double* __restrict__ qp
 }
 
 // sel[h][qc][0 .. kk) (kk = min(topk, n)): the local cubes first, then repeated argmax (the larger score, the
-// smaller index on ties); nsel[h][qc] = kk. One workgroup of 256 threads per (qc, h); n <= 4096.
-__global__ __launch_bounds__(256) void cube_topk(const double* __restrict__ sc, uint16_t* __restrict__ sel,
-                                                 uint16_t* __restrict__ nsel, uint32_t n, uint32_t kk,
-                                                 uint32_t local, uint32_t stride)
+// smaller index on ties); nsel[h][qc] = kk. One wave per (qc, h), n <= 4096: lane l keeps scores l, l + 64, ...
+// (up to 64 doubles) in registers and the best of them (value, index: a strict > scan in index order keeps the
+// smaller index of equal values; no score yet: -inf at index 0). A pick is the wave's best pair by a butterfly of
+// shuffles (the larger value, the smaller index on ties); the lane that holds it drops that score (-inf) and rescans
+// its own. So a pick is six shuffle steps and one lane's rescan, with no LDS round trip or workgroup barrier. As
+// the reference's rule: a local cube's score is dropped once picked; when every remaining score is -inf the pick is
+// index 0.
+constexpr uint32_t kTopkPerLane = 4096 / 64;
+
+__device__ __forceinline__ void best_of(const double (&v)[kTopkPerLane], uint32_t lane, uint32_t n, double& bv,
+                                        uint32_t& bi)
 {
-    __shared__ double scores[4096];
-    __shared__ double best_v[4];
-    __shared__ uint32_t best_i[4];
-    __shared__ uint32_t n_local;
-    const uint32_t qc = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const double* rowp = sc + ((size_t)h * n + qc) * n;
-    for (uint32_t i = tid; i < n; i += 256)
-        scores[i] = rowp[i];
-    uint16_t* out = sel + ((size_t)h * n + qc) * kk;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t it = 0;
-        if (local) {
-            const uint32_t picks[3] = {qc, qc >= stride ? qc - stride : n, qc + stride < n ? qc + stride : n};
-            for (uint32_t j = 0; j < local && it < kk; ++j)
-                if (picks[j] < n) {
-                    out[it++] = (uint16_t)picks[j];
-                    scores[picks[j]] = -INFINITY;
-                }
+    bv = -INFINITY;
+    bi = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kTopkPerLane; ++j)
+        if (lane + 64 * j < n && v[j] > bv) {
+            bv = v[j];
+            bi = lane + 64 * j;
         }
-        n_local = it;
-    }
-    __syncthreads();
-    for (uint32_t it = n_local; it < kk; ++it) {
-        double v = -INFINITY;
-        uint32_t idx = 0;
-        for (uint32_t i = tid; i < n; i += 256)
-            if (scores[i] > v) {
-                v = scores[i];
-                idx = i;
+}
+
+__global__ __launch_bounds__(64) void cube_topk(const double* __restrict__ sc, uint16_t* __restrict__ sel,
+                                                uint16_t* __restrict__ nsel, uint32_t n, uint32_t kk, uint32_t local,
+                                                uint32_t stride)
+{
+    const uint32_t qc = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const double* rowp = sc + ((size_t)h * n + qc) * n;
+    double v[kTopkPerLane];
+#pragma unroll
+    for (uint32_t j = 0; j < kTopkPerLane; ++j)
+        v[j] = lane + 64 * j < n ? rowp[lane + 64 * j] : -INFINITY;
+    uint16_t* out = sel + ((size_t)h * n + qc) * kk;
+    const auto drop = [&](uint32_t idx) {  // the lane holding idx sets it to -inf
+#pragma unroll
+        for (uint32_t j = 0; j < kTopkPerLane; ++j)
+            if (lane + 64 * j == idx)
+                v[j] = -INFINITY;
+    };
+    uint32_t it = 0;
+    if (local) {
+        const uint32_t picks[3] = {qc, qc >= stride ? qc - stride : n, qc + stride < n ? qc + stride : n};
+        for (uint32_t j = 0; j < local && it < kk; ++j)
+            if (picks[j] < n) {
+                if (lane == 0)
+                    out[it] = (uint16_t)picks[j];
+                ++it;
+                drop(picks[j]);
             }
+    }
+    double bv;
+    uint32_t bi;
+    best_of(v, lane, n, bv, bi);
+    for (; it < kk; ++it) {
+        double wv = bv;
+        uint32_t wi = bi;
 #pragma unroll
         for (uint32_t o = 32; o > 0; o >>= 1) {
-            const double ov = __shfl_xor(v, o);
-            const uint32_t oi = __shfl_xor(idx, o);
-            if (ov > v || (ov == v && oi < idx)) {
-                v = ov;
-                idx = oi;
+            const double ov = __shfl_xor(wv, o);
+            const uint32_t oi = __shfl_xor(wi, o);
+            if (ov > wv || (ov == wv && oi < wi)) {
+                wv = ov;
+                wi = oi;
             }
         }
-        if (lane == 0) {
-            best_v[wv] = v;
-            best_i[wv] = idx;
+        if (lane == 0)
+            out[it] = (uint16_t)wi;
+        if (lane == wi % 64) {  // the holder drops the pick and finds its next best
+            drop(wi);
+            best_of(v, lane, n, bv, bi);
         }
-        __syncthreads();
-        if (tid == 0) {
-            double bv = best_v[0];
-            uint32_t bi = best_i[0];
-            for (uint32_t j = 1; j < 4; ++j)
-                if (best_v[j] > bv || (best_v[j] == bv && best_i[j] < bi)) {
-                    bv = best_v[j];
-                    bi = best_i[j];
-                }
-            out[it] = (uint16_t)bi;
-            scores[bi] = -INFINITY;
-        }
-        __syncthreads();
     }
-    if (tid == 0)
+    if (lane == 0)
         nsel[(size_t)h * n + qc] = (uint16_t)kk;
 }
 
@@ -773,7 +782,7 @@ extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, 
         hipLaunchKernelGGL(cube_pool<_Float16>, pgrid, dim3(kD), 0, s, static_cast<const _Float16*>(q),
                            static_cast<const _Float16*>(k), cnt, qp, kp, n_cubes, q_pad, k_pad);
     hipLaunchKernelGGL(cube_scores, sgrid, dim3(256), 0, s, qp, kp, sc, n_cubes);
-    hipLaunchKernelGGL(cube_topk, tgrid, dim3(256), 0, s, sc, sel, nsel, n_cubes, std::min(topk, n_cubes), local,
+    hipLaunchKernelGGL(cube_topk, tgrid, dim3(64), 0, s, sc, sel, nsel, n_cubes, std::min(topk, n_cubes), local,
                        stride);
     return check_launch("cube_select");
 }
