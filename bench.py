@@ -5,7 +5,9 @@ Headline (one JSON line): causal GQA prefill at the Qwen3-8B shape (batch 1, 32 
 D 128, S 4096, bf16 in and out, fp32 accumulate, LSE), in TFLOP/s counting only the unmasked pairs
 (4 * D * S (S + 1) / 2 * 32). Beside it: batch-16 decode against a contiguous f16 KV cache (contexts drawn
 uniformly from [1024, 32768], seed 2026) in GB/s of K + V read (sum of 4096 * ctx bytes), and the bidirectional
-S16384 24-head case and the S16384 causal block-sparse case in TFLOP/s, the head tiles of the prefill step
+S16384 24-head case, the S16384 causal block-sparse case, MiniMax-H3's block-sparse call (cube_select and
+per-head lists) and its dense 56-head S19308 bidirectional case (the reference's one published shape) in TFLOP/s,
+the head tiles of the prefill step
 (fp32 rows to normed, rotated bf16 tiles) in GB/s, the split-K / gathered latent-cache helpers of a sparse latent
 decode, each against its own roof, the output projection after attention (Qwen3-8B o_proj) in TFLOP/s, and the
 gated delta rule of the linear-attention layers in TFLOP/s. Inputs are synthetic N(0, 1), resident in
@@ -18,7 +20,7 @@ configuration, scaled to the metric's unit by the sample's share of the algorith
 the parity check of the GPU output against the oracle.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
-                  [--only prefill,s512,decode,bidir,sparse,heads,step,gather,proj,scan,copy]
+                  [--only prefill,s512,decode,bidir,sparse,h3_sparse,h3_bidir,heads,step,gather,proj,scan,copy]
 """
 import argparse
 import json
@@ -500,6 +502,174 @@ def bench_sparse(torch, M, steps, warmup, with_cpu):
     return out
 
 
+def h3_cubes(frames, ph, pw, dense):
+    """The row layout of MiniMax-H3's sparse attention (h3.cpp:510-547): the video rows of `frames` latent frames
+    of ph x pw patches in 4 x 4 x 4 cubes of (frame, patch row, patch column), the grid padded to multiples of 4 with
+    rows that are no token (valid 0, map -1), then the `dense` text, conditioning and audio rows. The model's rows
+    are the dense ones first, then the video frame by frame. Returns n_cubes, the attention rows, the cube-grid
+    stride of one latent frame step (yc * xc), map [rows] i32, valid [rows] u8 and the cubes' row counts."""
+    import numpy as np
+
+    fc, yc, xc = (-(-frames // 4), -(-ph // 4), -(-pw // 4))
+    n = fc * yc * xc
+    vrows = n * 64
+    rows = vrows + dense
+    map_ = np.full(rows, -1, np.int32)
+    valid = np.zeros(rows, np.uint8)
+    f, y, x = np.meshgrid(np.arange(frames), np.arange(ph), np.arange(pw), indexing="ij")
+    cube = ((f // 4) * yc + y // 4) * xc + x // 4
+    r = cube * 64 + ((f % 4) * 4 + y % 4) * 4 + x % 4
+    map_[r.ravel()] = (dense + (f * ph + y) * pw + x).ravel()
+    valid[r.ravel()] = 1
+    map_[vrows:] = np.arange(dense)
+    valid[vrows:] = 1
+    cnt = np.bincount(cube.ravel(), minlength=n).astype(np.uint32)
+    return n, rows, yc * xc, map_, valid, cnt
+
+
+def bench_h3_sparse(torch, M, steps, warmup, with_cpu):
+    """MiniMax-H3's block-sparse attention as its engine calls it (h3.cpp:342-366, 510-547; runtime.hpp:96-106):
+    56 heads of 128 (MHA), f16 tiles, f32 output through the row map; cube_select with per-head lists (top 1/8 of the
+    cubes, the local option 3: a cube and its neighbours one latent-frame step before and after lead each list),
+    then attention over the selected cubes plus the dense rows; tiles past the cubes see every key. The layout: a
+    960x544 video at 9 latent frames of 34 x 60 patches (18360 video rows in 405 cubes, 25920 rows padded) and 948
+    dense rows: the 19308 rows of the reference's own attention benchmark. Roofline: MFMA, over the pairs the
+    pass lists name (each visited 64-row tile times its keys, masked ones included, as the kernel computes them)."""
+    import numpy as np
+
+    H, D, dense, ratio, local = 56, 128, 948, 0.125, 3
+    n, rows, stride, map_h, valid_h, cnt_h = h3_cubes(9, 34, 60, dense)
+    S = int(map_h.max()) + 1
+    q_pad, k_pad = -(-rows // 64) * 64, -(-rows // 128) * 128
+    topk = max(1, int(np.ceil(ratio * n)))
+    gen = torch.Generator(device="cuda").manual_seed(19308)
+    live = torch.zeros(max(q_pad, k_pad), dtype=torch.float16, device="cuda")
+    live[:rows] = torch.from_numpy(valid_h).to("cuda").half()
+    q, k, v = ((torch.randn((H, p, D), generator=gen, device="cuda").half() * live[:p, None]).contiguous()
+               for p in (q_pad, k_pad, k_pad))
+    o = torch.zeros((S, H * D), dtype=torch.float32, device="cuda")
+    lse = torch.empty((H, q_pad), dtype=torch.float32, device="cuda")
+    sel = torch.zeros((H, n, topk), dtype=torch.int16, device="cuda")
+    nsel = torch.zeros((H, n), dtype=torch.int16, device="cuda")
+    ws = torch.empty(M.cube_select_workspace(H, n), dtype=torch.uint8, device="cuda")
+    cnt = torch.from_numpy(cnt_h.view(np.int32)).to("cuda")
+    valid = torch.zeros(k_pad, dtype=torch.uint8, device="cuda")
+    valid[:rows] = torch.from_numpy(valid_h).to("cuda")
+    map_ = torch.full((q_pad,), -1, dtype=torch.int32, device="cuda")
+    map_[:rows] = torch.from_numpy(map_h).to("cuda")
+    sargs = dict(heads=H, q_pad=q_pad, k_pad=k_pad, n_cubes=n, topk=topk, local=local, stride=stride)
+    args = dict(n_q=rows, q_pad=q_pad, n_k=rows, k_pad=k_pad, heads=H, kv_heads=H, n_cubes=n, max_sel=topk,
+                dense0=n * 64, dense1=rows, causal=0, sel_heads=H)
+
+    def select():
+        M.cube_select(q, k, cnt, sel, nsel, ws, **sargs)
+
+    def attend(lse_out=None):
+        M.attn_sparse(q, k, v, o, sel, nsel, valid, map_, lse=lse_out, **args)
+
+    def call():
+        select()
+        attend()
+
+    select()
+    torch.cuda.synchronize()
+    ns = nsel.cpu().numpy().view(np.uint16).astype(np.int64)
+    pairs = float(64 * (ns * 64 + dense).sum() + H * (rows - n * 64) * rows)
+    flop = 4.0 * D * pairs
+    ms_sel, kms_sel = time_launches(torch, select, steps, warmup)
+    ms_att, kms_att = time_launches(torch, attend, steps, warmup)
+    ms, _ = time_launches(torch, call, steps, warmup)
+    kt = flop / (kms_att * 1e-3) / 1e12
+    out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+           "attention": {"ms_per_step": round(ms_att, 4), "kernel_ms": round(kms_att, 4),
+                         "tflops": round(kt, 2), "frac": round(kt / PEAK_TFLOPS, 4)},
+           "cube_select": {"ms_per_step": round(ms_sel, 4), "kernel_ms": round(kms_sel, 4)},
+           "dtype": "f16",
+           "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_sparse_h3"),
+                        "kernel": "the attention of the call (per-head lists)", "kernel_ms": kms_att},
+           "config": {"workload": "MiniMax-H3 block-sparse attention at 960x544: 56 heads of 128 (MHA), 405 cubes "
+                                  f"of 64 rows, per-head lists of the top {topk} (1/8, local 3, stride {stride}), "
+                                  f"{dense} dense rows, {rows} attention rows mapped to {S} model rows, f16 in, f32 "
+                                  "out; value: cube_select + attention a step",
+                      "pairs": pairs, "flop": flop}}
+    if with_cpu:
+        import oracle as O
+
+        attend(lse)
+        torch.cuda.synchronize()
+        qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
+        sel_h, nsel_h = sel.cpu().numpy().view(np.uint16), nsel.cpu().numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        want_sel, want_nsel = O.cube_select(qb, kb, cnt_h, dim=D, dtype=O.F16, **sargs)
+        t_sel = time.perf_counter() - t0
+        gpu_o, gpu_l = o.cpu().numpy(), lse.cpu().numpy()
+        rng = np.random.default_rng(56)
+        live_rows = np.flatnonzero(map_h >= 0)
+        state = {}
+
+        def run(m):
+            hr = np.stack([rng.integers(0, H, m), live_rows[rng.integers(0, len(live_rows), m)]], 1)
+            hr = hr.astype(np.uint32)
+            want, wl = O.attn_sparse_rows(qb, kb, vb, sel_h, nsel_h, np.pad(valid_h, (0, k_pad - rows)), hr,
+                                          dtype=O.F16, nthreads=cpu_threads(), **args)
+            state["hr"], state["want"], state["wl"] = hr, want, wl
+
+        m, dt = cpu_sample(run, 64, CPU_SECONDS)
+        hr, want, wl = state["hr"], state["want"], state["wl"]
+        keys = [(int(ns[h, r // 64]) * 64 + dense) if r < n * 64 else rows for h, r in hr]
+        got = np.stack([gpu_o[map_h[r], h * D:(h + 1) * D] for h, r in hr])
+        out["cpu_baseline"] = {"value": 4.0 * D * sum(keys) / dt / 1e12, "unit": "TFLOP/s", "kind": "port",
+                               "extrapolated": True,
+                               "sample": f"{m} random (head, live row) pairs of the attention, double precision, "
+                                         f"{dt:.2f} s wall, over the GPU's lists; cube_select of all 56 heads "
+                                         f"{t_sel:.2f} s, one thread"}
+        out["cpu_baseline"].update(cpu_info())
+        out["parity"] = parity_of(got, want, D, np.array([gpu_l[h, r] for h, r in hr]), wl)
+        out["parity"]["cube_select_exact"] = bool(np.array_equal(sel_h, want_sel) and
+                                                  np.array_equal(nsel_h, want_nsel))
+    return out
+
+
+def bench_h3_bidir(torch, M, steps, warmup, with_cpu):
+    """The one shape the reference publishes a time for: its attention benchmark's default, MiniMax-H3's dense
+    sequence at 960x544 (bench/attn_bench.cpp:1-2, 36-39): 56 heads of 128, 19308 query rows over 19308 keys,
+    bidirectional, f16 in and f32 out, no LSE. The reference's figure, 302 ms for flash_attn_coop_128_32
+    (ops.metal:227-228), is from an Apple GPU, not from this hardware; vs_baseline is that time over this one."""
+    S, H, D = 19308, 56, 128
+    q_pad, k_pad = -(-S // 64) * 64, -(-S // 128) * 128
+    gen = torch.Generator(device="cuda").manual_seed(302)
+    q = torch.randn((H, q_pad, D), generator=gen, device="cuda").half()
+    k = torch.randn((H, k_pad, D), generator=gen, device="cuda").half()
+    v = torch.randn((H, k_pad, D), generator=gen, device="cuda").half()
+    o = torch.empty((S, H * D), dtype=torch.float32, device="cuda")
+    args = dict(n_q=S, q_pad=q_pad, n_k=S, k_pad=k_pad, heads=H, kv_heads=H, q_pos0=0, block=0, dim=D)
+    ms, kms = time_launches(torch, lambda: M.attn_fwd(q, k, v, o, **args), steps, warmup)
+    flop = 4.0 * D * S * S * H
+    kt = flop / (kms * 1e-3) / 1e12
+    ref_ms = 302.0
+    out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+           "kernel_ms": round(kms, 4), "frac": round(kt / PEAK_TFLOPS, 4), "dtype": "f16",
+           "vs_baseline": round(ref_ms / ms, 2),
+           "baseline": {"ms": ref_ms, "tflops": round(flop / (ref_ms * 1e-3) / 1e12, 2),
+                        "hardware": "Apple GPU (unnamed), the reference's published figure, not MI355X",
+                        "source": "src/kernels/ops.metal:227-228; bench/attn_bench.cpp:1-2"},
+           "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": kt / PEAK_TFLOPS, "traffic": traffic("flash_fwd_h3_s19308"),
+                        "kernel": "flash_fwd_r64<f16,f32> (one launch a call)", "kernel_ms": kms},
+           "config": {"workload": "MiniMax-H3 dense attention at 960x544: 56 heads of 128 (MHA), 19308 x 19308, "
+                                  "bidirectional, f16 in, f32 out, no LSE", "flop": flop}}
+    if with_cpu:
+        import oracle as O
+
+        lse = torch.empty((H, S), dtype=torch.float32, device="cuda")  # [heads][n_q]
+        M.attn_fwd(q, k, v, o, lse=lse, **args)
+        torch.cuda.synchronize()
+        out["cpu_baseline"], out["parity"], _ = dense_cpu_leg(torch, M, O, q, k, v, o, lse, args, O.F16, 19, 16,
+                                                              "the 56-head S19308 bidirectional case")
+    return out
+
+
 def bench_heads(torch, M, steps, warmup):
     """The head tiles of a Qwen3-8B prefill step (src/models/qwen_text.cpp:415-417): 4096 tokens, q 32 heads and
     k 8 heads of 128 RMS-normed and rotated over the whole head, v 8 heads sliced, from fp32 rows into bf16 tiles;
@@ -696,7 +866,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline and parity legs")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs to run alone (no CPU legs unless --cpu): prefill, s512, decode, "
-                         "few_rows, bidir, dims, sparse, heads, step, gather, proj, scan, copy; few_rows:N runs the n_q = N "
+                         "few_rows, bidir, dims, sparse, h3_sparse, h3_bidir, heads, step, gather, proj, scan, copy; "
+                         "few_rows:N runs the n_q = N "
                          "case alone, dims:NAME one head width (d256_causal, d64_bidir)")
     ap.add_argument("--cpu", action="store_true", help="with --only: run the legs' CPU-baseline and parity parts")
     args = ap.parse_args()
@@ -728,6 +899,8 @@ def main():
               "bidir": lambda: bench_bidir(torch, M, args.steps, args.warmup, c),
               "dims": lambda: bench_other_dims(torch, M, args.steps, args.warmup, c, sub.get("dims")),
               "sparse": lambda: bench_sparse(torch, M, args.steps, args.warmup, c),
+              "h3_sparse": lambda: bench_h3_sparse(torch, M, args.steps, args.warmup, c),
+              "h3_bidir": lambda: bench_h3_bidir(torch, M, args.steps, args.warmup, c),
               "heads": lambda: bench_heads(torch, M, args.steps, args.warmup),
               "step": lambda: bench_step(torch, M, args.steps, args.warmup),
               "gather": lambda: bench_gather(torch, M, args.steps, args.warmup),
@@ -747,6 +920,8 @@ def main():
     bid = bench_bidir(torch, M, max(1, args.steps // 4), max(1, args.warmup), with_cpu)
     dims = bench_other_dims(torch, M, max(1, args.steps // 2), args.warmup, with_cpu)
     spa = bench_sparse(torch, M, args.steps, args.warmup, with_cpu)
+    h3s = bench_h3_sparse(torch, M, max(1, args.steps // 4), max(1, args.warmup), with_cpu)
+    h3d = bench_h3_bidir(torch, M, max(1, args.steps // 8), max(1, args.warmup), with_cpu)
     hds = bench_heads(torch, M, args.steps, args.warmup)
     stp = bench_step(torch, M, args.steps, args.warmup)
     gat = bench_gather(torch, M, args.steps, args.warmup)
@@ -784,6 +959,8 @@ def main():
         "bidirectional": bid,
         "other_head_widths": dims,
         "block_sparse": spa,
+        "h3_block_sparse": h3s,
+        "h3_bidirectional": h3d,
         "head_tiles": {"value": round(hds["gbps"], 1), "unit": "GB/s", "ms_per_step": round(hds["ms"], 4),
                        "kernel_ms": round(hds["kernel_ms"], 4), "bound": "hbm", "frac": round(hds["frac"], 4),
                        "config": {"workload": "Qwen3-8B prefill head tiles: 4096 tokens, q 32 and k 8 heads of 128 "
@@ -830,6 +1007,7 @@ def configs_summary(line, pre, dec, few):
         return dict({"value": round(value, 2), "unit": unit, "kernel_ms": round(kernel_ms, 4),
                      "frac": round(frac, 4)}, **par(parity))
     s512, bid, spa = line["prefill_s512"], line["bidirectional"], line["block_sparse"]
+    h3s, h3d = line["h3_block_sparse"], line["h3_bidirectional"]
     f1 = few["n_q=1"]
     return {
         "C1_causal_s512_f16": entry(s512["value"], "TFLOP/s", s512["roofline"]["kernel_ms"], s512["roofline"]["frac"],
@@ -841,6 +1019,12 @@ def configs_summary(line, pre, dec, few):
                                         spa.get("parity")),
         "C5_bidirectional_s16384": entry(bid["value"], "TFLOP/s", bid["kernel_ms"], bid["frac"], bid.get("parity")),
         "few_rows_n_q1": entry(f1["gbps"], "GB/s", f1["kernel_ms"], f1["roofline"]["frac"], f1.get("parity")),
+        "h3_sparse_per_head_lists": entry(h3s["attention"]["tflops"], "TFLOP/s", h3s["attention"]["kernel_ms"],
+                                          h3s["roofline"]["frac"], h3s.get("parity")),
+        "h3_bidirectional_s19308_f16_f32": dict(entry(h3d["value"], "TFLOP/s", h3d["kernel_ms"], h3d["frac"],
+                                                      h3d.get("parity")),
+                                                vs_baseline=h3d["vs_baseline"],
+                                                baseline="302 ms on an Apple GPU (reference's published figure)"),
     }
 
 

@@ -3,6 +3,8 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <limits>
+#include <utility>
 #include <stdexcept>
 
 #include "mako_attn.h"
@@ -21,46 +23,61 @@ void hip_check(hipError_t e, const char* what)
 
 }  // namespace
 
+namespace {
+
+// The telemetry level names, in the order of the levels.
+constexpr std::pair<std::string_view, Telemetry> kTelemetryNames[] = {
+    {"off", Telemetry::off}, {"summary", Telemetry::summary}, {"steps", Telemetry::steps},
+    {"layers", Telemetry::layers}, {"kernels", Telemetry::kernels}};
+
+}  // namespace
+
 std::optional<Telemetry> parse_telemetry(std::string_view s)
 {
-    if (s == "off")
-        return Telemetry::off;
-    if (s == "summary")
-        return Telemetry::summary;
-    if (s == "steps")
-        return Telemetry::steps;
-    if (s == "layers")
-        return Telemetry::layers;
-    if (s == "kernels")
-        return Telemetry::kernels;
+    for (const auto& [name, level] : kTelemetryNames)
+        if (name == s)
+            return level;
     return std::nullopt;
+}
+
+RepeatSpec RepeatSpec::parse(std::string_view spec)
+{
+    const size_t colon = spec.rfind(':');
+    if (colon == std::string_view::npos)
+        throw std::runtime_error("MAKO_REPEAT wants <label substring>:<n>");
+    RepeatSpec r;
+    // The count: the integer that starts the text after the last ':' (leading blanks skipped); none, or below 0: 0.
+    const std::string count(spec.substr(colon + 1));
+    const long n = std::strtol(count.c_str(), nullptr, 10);
+    r.times = static_cast<int>(std::clamp<long>(n, 0, std::numeric_limits<int>::max()));
+    // The labels: the comma-separated parts before it; empty parts match nothing.
+    std::string_view rest = spec.substr(0, colon);
+    while (!rest.empty()) {
+        const std::string_view part = rest.substr(0, rest.find(','));
+        if (!part.empty())
+            r.labels.emplace_back(part);
+        rest.remove_prefix(std::min(rest.size(), part.size() + 1));
+    }
+    return r;
+}
+
+bool RepeatSpec::matches(std::string_view label) const
+{
+    return std::any_of(labels.begin(), labels.end(),
+                       [&](const std::string& sub) { return label.find(sub) != std::string_view::npos; });
 }
 
 Runtime::Runtime(Telemetry telemetry, int device) : device_(device), tel_(telemetry)
 {
-    if (const char* r = std::getenv("MAKO_REPEAT")) {  // src/gpu/runtime.cpp:52-59
-        const std::string spec(r);
-        const size_t colon = spec.rfind(':');
-        if (colon == std::string::npos)
-            throw std::runtime_error("MAKO_REPEAT wants <label substring>:<n>");
-        repeat_label_ = spec.substr(0, colon);
-        repeat_n_ = std::max(0, std::atoi(r + colon + 1));
-    }
+    if (const char* r = std::getenv("MAKO_REPEAT"))
+        repeat_ = RepeatSpec::parse(r);
     hip_check(hipSetDevice(device_), "hipSetDevice");
     hip_check(hipStreamCreateWithFlags(&enc_.stream, hipStreamNonBlocking), "hipStreamCreate");
 }
 
 int Runtime::repeats(std::string_view label) const
 {
-    if (repeat_n_ == 1)
-        return 1;
-    for (size_t p = 0; p <= repeat_label_.size();) {
-        const size_t e = std::min(repeat_label_.find(',', p), repeat_label_.size());
-        if (e > p && label.find(std::string_view(repeat_label_).substr(p, e - p)) != std::string_view::npos)
-            return repeat_n_;
-        p = e + 1;
-    }
-    return 1;
+    return repeat_.times != 1 && repeat_.matches(label) ? repeat_.times : 1;
 }
 
 Runtime::~Runtime()

@@ -23,6 +23,16 @@ namespace mako::gpu {
 enum class Telemetry { off, summary, steps, layers, kernels };
 std::optional<Telemetry> parse_telemetry(std::string_view s);
 
+// The value of MAKO_REPEAT, <label substrings, comma-separated>:<n> (src/gpu/runtime.cpp:52-59): the substrings and
+// the launch count. parse() throws std::runtime_error for a value with no ':'.
+struct RepeatSpec {
+    std::vector<std::string> labels;
+    int times = 1;
+    static RepeatSpec parse(std::string_view spec);
+    // Whether one of the substrings occurs in `label`.
+    bool matches(std::string_view label) const;
+};
+
 struct KernelTime {
     std::string kernel;
     double ms = 0;
@@ -152,8 +162,7 @@ private:
     Probe probe_;
     std::vector<PendingProbe> pending_probes_;
     std::vector<std::pair<float*, size_t>> spare_host_;  // pinned buffers (values) for later probes
-    std::string repeat_label_;
-    int repeat_n_ = 1;
+    RepeatSpec repeat_;
     std::vector<hipEvent_t> spare_events_;
     std::vector<KernelTime> kernels_;
     std::chrono::steady_clock::time_point step_start_;

@@ -291,6 +291,25 @@ int main()
                       kt[0].count == 1 && std::memcmp(o.data(), once.data(), n * 4) == 0,
                   "MAKO_REPEAT=flash_fwd:3: attention repeated inside one timed launch, output bit-equal");
         }
+        {
+            using mako::gpu::RepeatSpec;
+            const RepeatSpec a = RepeatSpec::parse("flash,,cube:select:4");
+            const RepeatSpec b = RepeatSpec::parse("attn:-2");
+            const RepeatSpec c = RepeatSpec::parse(":x");
+            bool threw = false;
+            try {
+                (void)RepeatSpec::parse("flash_fwd");
+            } catch (const std::runtime_error&) {
+                threw = true;
+            }
+            check(a.times == 4 && a.labels == std::vector<std::string>{"flash", "cube:select"} &&
+                      a.matches("flash_fwd_128") && a.matches("cube:select") && !a.matches("cube_select") &&
+                      b.times == 0 && c.times == 0 && c.labels.empty() && !c.matches("x") && threw &&
+                      mako::gpu::parse_telemetry("layers") == mako::gpu::Telemetry::layers &&
+                      !mako::gpu::parse_telemetry("Layers"),
+                  "MAKO_REPEAT parse: comma-separated labels split at the last ':', counts clamped at 0, no ':' "
+                  "throws; telemetry names exact");
+        }
     }
     // A head width the reference refuses.
     {
