@@ -31,6 +31,12 @@ namespace mako {
 // pass table, and its launch (-1: the workspace could not be had, the error recorded).
 bool sparse64_fits(const mako_sparse_args* a, const void* valid);
 size_t sparse64_workspace(const mako_sparse_args* a);
+// attn_sparse_lists.hip: the route for a list per query head with f16 inputs, and its launch.
+bool sparse_lists_fits(const mako_sparse_args* a, mako_dtype in, const void* valid);
+template <class TO>
+void launch_sparse_lists(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v,
+                         void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
+                         const int32_t* map, float* lse, hipStream_t s);
 template <class T, class TO>
 int launch_sparse64(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                     const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid, const int32_t* map, float* lse,
@@ -63,7 +69,27 @@ struct SparseParams {
     float scale_log2;
     uint32_t n_cubes, max_sel, dense0, dense1, causal, sel_heads;
     uint32_t group, hs, n_qt;
+    uint32_t n_hg, xcd_major;  // head groups (heads / hs); items dealt by XCD (n_hg % 8 == 0)
 };
+
+// Workgroup b's item (head group, query tile), head-group-major so that the chip streams the K / V of about one head
+// group at a time (per-head lists gather cubes from anywhere in a head's keys: with every head live at once the
+// gathered tiles come from HBM). With xcd_major, workgroup b runs on XCD b % 8 and XCD x takes head groups x, x + 8,
+// ... one after another, so each XCD's L2 serves one head group's keys. Query tiles run from the last (dense tiles,
+// which see every key) to the first. False past the last item.
+__device__ __forceinline__ bool sparse_item(const SparseParams& p, uint32_t b, uint32_t& hg, uint32_t& qt)
+{
+    uint32_t s = b;
+    hg = 0;
+    if (p.xcd_major) {
+        s = b / 8;
+        hg = b % 8 + 8 * (s / p.n_qt);
+    } else {
+        hg = s / p.n_qt;
+    }
+    qt = p.n_qt - 1 - s % p.n_qt;
+    return hg < p.n_hg;
+}
 
 template <class T, class TO, int NW>
 __global__ __launch_bounds__(NW * 64, 2) void flash_sparse(const SparseParams p)
@@ -83,8 +109,10 @@ __global__ __launch_bounds__(NW * 64, 2) void flash_sparse(const SparseParams p)
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t g = lane >> 5, c32 = lane & 31;
-    const uint32_t qt = p.n_qt - 1 - blockIdx.y;  // dense tiles (all keys) and late cubes first
-    const uint32_t h = blockIdx.x * p.hs + (w >> 1);
+    uint32_t hg, qt;
+    if (!sparse_item(p, blockIdx.x, hg, qt))
+        return;
+    const uint32_t h = hg * p.hs + (w >> 1);
     const uint32_t kvh = h / p.group;
     const uint32_t q0 = qt * kCube + (w & 1) * 32;  // this wave's first row
     const uint32_t row = q0 + c32;
@@ -301,64 +329,87 @@ __global__ __launch_bounds__(kD) void cube_pool(const T* __restrict__ q, const T
     (is_k ? kp : qp)[((size_t)h * n_cubes + cb) * kD + d] = n ? s / (double)n : 0.0;
 }
 
-// sc[h][qc][kc] = qp[h][qc] . kp[h][kc]: 16 x 16 output tiles through LDS. Grid (ceil(n / 16), ceil(n / 16),
-// heads), 256 threads.
+// sc[h][qc][kc] = qp[h][qc] . kp[h][kc]. A workgroup computes a 64 x 64 tile of scores, 4 x 4 a thread (16
+// independent sums), with the pooled rows staged through LDS 32 dimensions at a time; each sum still adds its
+// products in dimension order. Grid (ceil(n / 64), ceil(n / 64), heads), 256 threads.
+constexpr uint32_t kScoreTile = 64, kScoreChunk = 32;
+
 __global__ __launch_bounds__(256) void cube_scores(const double* __restrict__ qp, const double* __restrict__ kp,
                                                    double* __restrict__ sc, uint32_t n)
 {
-    __shared__ double qs[16][kD + 1], kt[16][kD + 1];
-    const uint32_t kc0 = blockIdx.x * 16, qc0 = blockIdx.y * 16, h = blockIdx.z, t = threadIdx.x;
-    for (uint32_t i = t; i < 16 * kD; i += 256) {
-        const uint32_t r = i / kD, d = i % kD;
-        qs[r][d] = qc0 + r < n ? qp[((size_t)h * n + qc0 + r) * kD + d] : 0.0;
-        kt[r][d] = kc0 + r < n ? kp[((size_t)h * n + kc0 + r) * kD + d] : 0.0;
+    // row stride 33 doubles: the 16 rows a read spans fall in distinct banks
+    __shared__ double qs[kScoreTile][kScoreChunk + 1], ks[kScoreTile][kScoreChunk + 1];
+    const uint32_t kc0 = blockIdx.x * kScoreTile, qc0 = blockIdx.y * kScoreTile, h = blockIdx.z, t = threadIdx.x;
+    const uint32_t qr = t / 16, kr = t % 16;  // rows qr + 16 i and columns kr + 16 j of the tile
+    const double* qh = qp + (size_t)h * n * kD;
+    const double* kh = kp + (size_t)h * n * kD;
+    double acc[4][4] = {};
+    for (uint32_t d0 = 0; d0 < kD; d0 += kScoreChunk) {
+        for (uint32_t e = t; e < kScoreTile * kScoreChunk; e += 256) {
+            const uint32_t r = e / kScoreChunk, d = e % kScoreChunk;
+            qs[r][d] = qc0 + r < n ? qh[(size_t)(qc0 + r) * kD + d0 + d] : 0.0;
+            ks[r][d] = kc0 + r < n ? kh[(size_t)(kc0 + r) * kD + d0 + d] : 0.0;
+        }
+        __syncthreads();
+        for (uint32_t d = 0; d < kScoreChunk; ++d) {
+            double a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = qs[qr + 16 * i][d];
+                b[i] = ks[kr + 16 * i][d];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    acc[i][jj] = __dadd_rn(acc[i][jj], __dmul_rn(a[i], b[jj]));  // no contraction
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    const uint32_t qr = t / 16, kr = t % 16;
-    double s = 0.0;
-    for (uint32_t d = 0; d < kD; ++d)
-        s = __dadd_rn(s, __dmul_rn(qs[qr][d], kt[kr][d]));  // separately rounded, in order: no contraction
-    if (qc0 + qr < n && kc0 + kr < n)
-        sc[((size_t)h * n + qc0 + qr) * n + kc0 + kr] = s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+            if (qc0 + qr + 16 * i < n && kc0 + kr + 16 * jj < n)
+                sc[((size_t)h * n + qc0 + qr + 16 * i) * n + kc0 + kr + 16 * jj] = acc[i][jj];
 }
 
 // sel[h][qc][0 .. kk) (kk = min(topk, n)): the local cubes first, then repeated argmax (the larger score, the
-// smaller index on ties); nsel[h][qc] = kk. One wave per (qc, h), n <= 4096: lane l keeps scores l, l + 64, ...
-// (up to 64 doubles) in registers and the best of them (value, index: a strict > scan in index order keeps the
-// smaller index of equal values; no score yet: -inf at index 0). A pick is the wave's best pair by a butterfly of
-// shuffles (the larger value, the smaller index on ties); the lane that holds it drops that score (-inf) and rescans
-// its own. So a pick is six shuffle steps and one lane's rescan, with no LDS round trip or workgroup barrier. As
-// the reference's rule: a local cube's score is dropped once picked; when every remaining score is -inf the pick is
-// index 0.
-constexpr uint32_t kTopkPerLane = 4096 / 64;
-
-__device__ __forceinline__ void best_of(const double (&v)[kTopkPerLane], uint32_t lane, uint32_t n, double& bv,
-                                        uint32_t& bi)
+// smaller index on ties); nsel[h][qc] = kk. One wave per (qc, h), n <= 64 P: lane l keeps scores l, l + 64, ...
+// (P doubles) in registers and the best of them (value, index: a strict > scan in index order keeps the smaller
+// index of equal values; no score yet: -inf at index 0). A pick is the wave's best pair by a butterfly of shuffles
+// (the larger value, the smaller index on ties); the lane that holds it drops that score (-inf) and rescans its own.
+// So a pick is six shuffle steps and one lane's rescan of P registers, with no LDS round trip or workgroup barrier.
+// As the reference's rule: a local cube's score is dropped once picked; when every remaining score is -inf the
+// pick is index 0.
+template <uint32_t P>
+__device__ __forceinline__ void best_of(const double (&v)[P], uint32_t lane, uint32_t n, double& bv, uint32_t& bi)
 {
     bv = -INFINITY;
     bi = 0;
 #pragma unroll
-    for (uint32_t j = 0; j < kTopkPerLane; ++j)
+    for (uint32_t j = 0; j < P; ++j)
         if (lane + 64 * j < n && v[j] > bv) {
             bv = v[j];
             bi = lane + 64 * j;
         }
 }
 
+template <uint32_t P>
 __global__ __launch_bounds__(64) void cube_topk(const double* __restrict__ sc, uint16_t* __restrict__ sel,
                                                 uint16_t* __restrict__ nsel, uint32_t n, uint32_t kk, uint32_t local,
                                                 uint32_t stride)
 {
     const uint32_t qc = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const double* rowp = sc + ((size_t)h * n + qc) * n;
-    double v[kTopkPerLane];
+    double v[P];
 #pragma unroll
-    for (uint32_t j = 0; j < kTopkPerLane; ++j)
+    for (uint32_t j = 0; j < P; ++j)
         v[j] = lane + 64 * j < n ? rowp[lane + 64 * j] : -INFINITY;
     uint16_t* out = sel + ((size_t)h * n + qc) * kk;
     const auto drop = [&](uint32_t idx) {  // the lane holding idx sets it to -inf
 #pragma unroll
-        for (uint32_t j = 0; j < kTopkPerLane; ++j)
+        for (uint32_t j = 0; j < P; ++j)
             if (lane + 64 * j == idx)
                 v[j] = -INFINITY;
     };
@@ -375,7 +426,7 @@ __global__ __launch_bounds__(64) void cube_topk(const double* __restrict__ sc, u
     }
     double bv;
     uint32_t bi;
-    best_of(v, lane, n, bv, bi);
+    best_of<P>(v, lane, n, bv, bi);
     for (; it < kk; ++it) {
         double wv = bv;
         uint32_t wi = bi;
@@ -392,11 +443,31 @@ __global__ __launch_bounds__(64) void cube_topk(const double* __restrict__ sc, u
             out[it] = (uint16_t)wi;
         if (lane == wi % 64) {  // the holder drops the pick and finds its next best
             drop(wi);
-            best_of(v, lane, n, bv, bi);
+            best_of<P>(v, lane, n, bv, bi);
         }
     }
     if (lane == 0)
         nsel[(size_t)h * n + qc] = (uint16_t)kk;
+}
+
+// The top-k launch with the smallest register array that holds n scores (n <= 4096).
+void launch_topk(const double* sc, uint16_t* sel, uint16_t* nsel, uint32_t n, uint32_t heads, uint32_t kk,
+                 uint32_t local, uint32_t stride, hipStream_t s)
+{
+    const dim3 grid(n, heads);
+#define MAKO_TOPK_CASE(PL)                                                                                         \
+    if (n <= 64 * (PL)) {                                                                                          \
+        hipLaunchKernelGGL(cube_topk<PL>, grid, dim3(64), 0, s, sc, sel, nsel, n, kk, local, stride);             \
+        return;                                                                                                    \
+    }
+    MAKO_TOPK_CASE(1)
+    MAKO_TOPK_CASE(2)
+    MAKO_TOPK_CASE(4)
+    MAKO_TOPK_CASE(8)
+    MAKO_TOPK_CASE(16)
+    MAKO_TOPK_CASE(32)
+    MAKO_TOPK_CASE(64)
+#undef MAKO_TOPK_CASE
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -734,7 +805,7 @@ void launch_sparse(const SparseParams& p, hipStream_t s)
         hipLaunchKernelGGL((flash_sparse8<T, TO>), dim3(p.heads / 4, p.n_qt), dim3(kWaves8 * 64), 0, s, p);
         return;
     }
-    const dim3 grid(p.heads / p.hs, p.n_qt);
+    const dim3 grid(p.n_hg * p.n_qt);
     if (p.hs == 2)
         hipLaunchKernelGGL((flash_sparse<T, TO, 4>), grid, dim3(256), 0, s, p);
     else
@@ -774,7 +845,8 @@ extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, 
     double* kp = reinterpret_cast<double*>(static_cast<char*>(workspace) + pooled_bytes(heads, n_cubes));
     double* sc = reinterpret_cast<double*>(static_cast<char*>(workspace) + 2 * pooled_bytes(heads, n_cubes));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 pgrid(n_cubes, heads, 2), sgrid((n_cubes + 15) / 16, (n_cubes + 15) / 16, heads), tgrid(n_cubes, heads);
+    const dim3 pgrid(n_cubes, heads, 2),
+        sgrid((n_cubes + kScoreTile - 1) / kScoreTile, (n_cubes + kScoreTile - 1) / kScoreTile, heads);
     if (in == MAKO_BF16)
         hipLaunchKernelGGL(cube_pool<__bf16>, pgrid, dim3(kD), 0, s, static_cast<const __bf16*>(q),
                            static_cast<const __bf16*>(k), cnt, qp, kp, n_cubes, q_pad, k_pad);
@@ -782,8 +854,7 @@ extern "C" int mako_cube_select(uint32_t heads, uint32_t q_pad, uint32_t k_pad, 
         hipLaunchKernelGGL(cube_pool<_Float16>, pgrid, dim3(kD), 0, s, static_cast<const _Float16*>(q),
                            static_cast<const _Float16*>(k), cnt, qp, kp, n_cubes, q_pad, k_pad);
     hipLaunchKernelGGL(cube_scores, sgrid, dim3(256), 0, s, qp, kp, sc, n_cubes);
-    hipLaunchKernelGGL(cube_topk, tgrid, dim3(64), 0, s, sc, sel, nsel, n_cubes, std::min(topk, n_cubes), local,
-                       stride);
+    launch_topk(sc, sel, nsel, n_cubes, heads, std::min(topk, n_cubes), local, stride, s);
     return check_launch("cube_select");
 }
 
@@ -826,7 +897,8 @@ int attn_sparse_core(const mako_sparse_args* a, mako_dtype in, mako_dtype out, c
     const uint32_t hs = (a->sel_heads == a->kv_heads && group % 2 == 0) ? 2 : 1;
     const SparseParams p{q, k, v, o, lse, sel, nsel, valid, map, a->n_q, a->q_pad, a->n_k, a->k_pad, a->heads,
                          a->kv_heads, a->width, a->scale * kLog2e, a->n_cubes, a->max_sel, a->dense0, a->dense1,
-                         a->causal ? 1u : 0u, a->sel_heads, group, hs, (a->n_q + kCube - 1) / kCube};
+                         a->causal ? 1u : 0u, a->sel_heads, group, hs, (a->n_q + kCube - 1) / kCube,
+                         a->heads / hs, (a->heads / hs) % 8 == 0 ? 1u : 0u};
     if (p.n_qt > 65535)
         return fail(MAKO_EINVAL, "attention_sparse: %u query tiles exceed the grid", p.n_qt);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -843,6 +915,13 @@ int attn_sparse_core(const mako_sparse_args* a, mako_dtype in, mako_dtype out, c
                     : launch_sparse64<_Float16, _Float16>(a, sl, q, k, v, o, sel, nsel, valid, map, lse, s, work);
         if (r < 0)
             return last_code() != MAKO_OK ? last_code() : MAKO_EHIP;
+        return check_launch("attention_sparse");
+    }
+    if (sparse_lists_fits(a, in, valid)) {
+        if (out == MAKO_F32)
+            launch_sparse_lists<float>(a, a->scale * kLog2e, q, k, v, o, sel, nsel, valid, map, lse, s);
+        else
+            launch_sparse_lists<_Float16>(a, a->scale * kLog2e, q, k, v, o, sel, nsel, valid, map, lse, s);
         return check_launch("attention_sparse");
     }
     if (in == MAKO_BF16) {

@@ -1,0 +1,319 @@
+// Block-sparse attention with one selection list per query head (sel_heads == heads: the lists cube_select writes,
+// as MiniMax-H3's engine calls it, src/models/h3.cpp:357-363) for f16 heads of 128: flash_sparse_lists. The
+// semantics are the reference's attention_sparse (src/kernels/ops.metal:1036-1185) as attn_sparse.hip states them:
+// query tile t (64 rows) < n_cubes visits the key cubes its list names, then the dense rows [dense0, dense1); a later
+// tile visits [0, n_k); keys with valid[j] == 0 are masked; causal: key j is seen by tile row r only when j <= r;
+// query row r's output goes to o row map[r], dropped when map[r] < 0 or r >= n_q; lse [heads][q_pad] by tile row.
+//
+// Why a kernel of its own: with a list per query head, no two query tiles of a head and no two heads visit the same
+// key tiles, so a staged K / V tile serves only the 64 rows of its own (head, query tile). The r64 route's sharing
+// (one staged tile for the 4 waves of a workgroup) does not exist here, and a 64-rows-a-wave stream would need a ring
+// of 64-key tiles per wave: more LDS than a CU holds for one wave a SIMD. So a workgroup is one (head, query tile):
+// 2 waves of 32 rows over 32-key tiles, 17 KiB a tile buffer and two buffers, so that 4 workgroups (8 waves, 2 a
+// SIMD) share a CU and one wave's softmax runs beside another's MFMAs.
+//
+// Staging is raw, by LDS DMA (16 bytes a lane, no conversion): the K image in slot order (slot s holds key
+// slot_of(s), so the exponentiated scores fall in the lanes and registers of the P V B operand) with rows padded to
+// 272 bytes (the 16 rows a b128 read spans start in distinct banks); the V image as the r64 stream lays it out
+// (32-byte units permuted by row) and read by ds_read_b64_tr_b16 as the V^T A operand; and the tile's 32 validity
+// bytes. S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16_f16, with P rounded to f16 (to nearest) as the
+// reference rounds it (ops.metal:329) and the sums of the unrounded exponentials (:330); the running maximum moves
+// only when a tile's passes it by more than 8 (base 2, :303-316). Tile t + 1 is in flight while tile t is computed.
+// Items (head, query tile) go head-major, with every head on one XCD at a time when the heads are a multiple of 8
+// (the head's K / V then stay in that XCD's L2), and the query tiles from the last (dense tiles, which see every key)
+// to the first.
+#include "fwd64_common.hpp"
+
+namespace mako {
+namespace {
+
+constexpr uint32_t kLD = 128;                     // head dims
+constexpr uint32_t kLKeys = 32;                   // keys a tile
+constexpr uint32_t kLKRow = 2 * kLD + 16;         // 272: LDS bytes of a K image row
+constexpr uint32_t kLKImg = 9 * 1024;             // the K image (8704 bytes) and what its ninth 1 KiB piece spills
+constexpr uint32_t kLVImg = kLKeys * 2 * kLD;     // 8 KiB: the V image
+constexpr uint32_t kLBuf = kLKImg + kLVImg + 64;  // and the tile's 32 validity bytes
+constexpr float kLRescale = 8.0f;
+
+struct ListsParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    const uint16_t* sel;
+    const uint16_t* nsel;
+    const uint8_t* valid;
+    const int32_t* map;
+    uint32_t n_q, q_pad, n_k, k_pad, heads, group, width;
+    float scale_log2;
+    uint32_t n_cubes, max_sel, dense0, dense1, causal, n_qt, xcd_major;
+};
+
+// An LDS DMA of 16 bytes a lane: rsrc + voff + soff to LDS m0 + 16 lane.
+__device__ __forceinline__ void dma16_at(uint32_t m0, uint32_t voff, uint32_t soff, u32x4 rsrc)
+{
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voff),
+                 "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Four f16 of V^T by a transpose read at LDS byte `at` of this wave's group pattern.
+__device__ __forceinline__ s16x4 tr_read(const unsigned char* at)
+{
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at));
+}
+
+template <class TO>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_sparse_lists(
+    const ListsParams p)
+{
+    using E = Elem<_Float16>;
+    using V8 = f16x8;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * kLBuf];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 5, c32 = lane & 31;
+    // The item: head-major, XCD b % 8 taking heads b % 8, b % 8 + 8, ... when xcd_major.
+    uint32_t h, qt;
+    {
+        const uint32_t b = blockIdx.x;
+        const uint32_t s = p.xcd_major ? b / 8 : b;
+        h = p.xcd_major ? b % 8 + 8 * (s / p.n_qt) : s / p.n_qt;
+        qt = p.n_qt - 1 - s % p.n_qt;
+        if (h >= p.heads)
+            return;
+    }
+    const uint32_t kvh = h / p.group;
+    const uint32_t q0 = qt * 64 + 32 * w, row = q0 + c32;  // this wave's first row, this lane's row
+    const bool live = q0 < p.n_q;
+
+    // The tiles: a cube tile's selected cubes (two tiles each), then its dense rows; a later tile's keys [0, n_k).
+    const bool cube = qt < p.n_cubes;
+    const uint16_t* my_sel = p.sel + ((size_t)h * p.n_cubes + (cube ? qt : 0u)) * p.max_sel;
+    const uint32_t ns = cube ? min(uniform_u16(p.nsel, (size_t)h * p.n_cubes + qt), p.max_sel) : 0u;
+    const uint32_t dlo = cube ? p.dense0 : 0u, dhi = cube ? p.dense1 : p.n_k;
+    const uint32_t nd = dhi > dlo ? (dhi - dlo + kLKeys - 1) / kLKeys : 0u;
+    const uint32_t nt = 2 * ns + nd;
+    auto tile_of = [&](uint32_t t, uint32_t& j0, uint32_t& hi) __attribute__((always_inline)) {
+        if (t < 2 * ns) {
+            const uint32_t c0 = uniform_u16(my_sel, t >> 1) * 64;
+            j0 = c0 + kLKeys * (t & 1);
+            hi = c0 + 64;
+        } else {
+            j0 = dlo + kLKeys * (t - 2 * ns);
+            hi = dhi;
+        }
+        j0 = __builtin_amdgcn_readfirstlane(j0);
+        hi = __builtin_amdgcn_readfirstlane(hi);
+    };
+
+    // Sources: the kv head's k_pad rows of K and V, the k_pad validity bytes (offsets past them load zeros).
+    u32x4 krs = rsrc_of(static_cast<const _Float16*>(p.k) + (size_t)kvh * p.k_pad * kLD, p.k_pad * 2 * kLD);
+    u32x4 vrs = rsrc_of(static_cast<const _Float16*>(p.v) + (size_t)kvh * p.k_pad * kLD, p.k_pad * 2 * kLD);
+    u32x4 brs = rsrc_of(p.valid, p.k_pad);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        krs[i] = __builtin_amdgcn_readfirstlane(krs[i]);
+        vrs[i] = __builtin_amdgcn_readfirstlane(vrs[i]);
+        brs[i] = __builtin_amdgcn_readfirstlane(brs[i]);
+    }
+    // K image piece i (1 KiB): lane l's 16 bytes are byte 1024 i + 16 l of the image, row R = that / 272 (key
+    // slot_of(R) of the tile), chunk (that % 272) / 16; chunk 16 (the row's padding) and rows past 31 (the spill of
+    // piece 8) load any bytes of the tile. Wave w DMAs pieces 4 w .. 4 w + 3 and piece 8 (both waves: the same bytes
+    // to the same place). V image piece i: keys 4 i .. 4 i + 3, lane l's slot holds unit v_unit(u, row) (vd_of).
+    auto kd_of = [&](uint32_t i) {
+        const uint32_t b = 1024 * i + 16 * lane, r = b / kLKRow, ch = b % kLKRow / 16;
+        return r < kLKeys && ch < 16 ? slot_of(r) * (2 * kLD) + 16 * ch : 0u;
+    };
+    uint32_t kd[5], vd[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        kd[m] = kd_of(4 * w + m);
+        vd[m] = 1024 * (4 * w + m) + vd_of<kLD>(lane);
+    }
+    kd[4] = kd_of(8);
+    const uint32_t lbase = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
+    auto dma_tile = [&](uint32_t t, uint32_t buf) __attribute__((always_inline)) {
+        uint32_t j0, hi;
+        tile_of(t, j0, hi);
+        const uint32_t kb = lbase + buf * kLBuf, vb = kb + kLKImg;
+        const uint32_t so = __builtin_amdgcn_readfirstlane(j0 * 2 * kLD);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            dma16_at(kb + 1024 * (4 * w + m), kd[m], so, krs);
+        dma16_at(kb + 1024 * 8, kd[4], so, krs);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            dma16_at(vb + 1024 * (4 * w + m), vd[m], so, vrs);
+        if (w == 0 && lane < 2)
+            dma16_at(vb + kLVImg, 16 * lane, j0, brs);
+    };
+
+    // Q: the B operand, lane (c32, g) holds row q0 + c32, head dims 16 kk + 8 g .. + 7 (rows past n_q load as 0).
+    V8 qreg[8];
+    {
+        const auto qrs = buffer_rsrc(static_cast<const _Float16*>(p.q) + (size_t)h * p.q_pad * kLD, p.n_q * 2 * kLD);
+        const uint32_t off = (row * kLD + 8 * g) * 2;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            qreg[kk] = __builtin_bit_cast(V8, buffer_load16(qrs, off + 32 * kk));
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            settle(qreg[kk]);
+    }
+    if (nt > 0)
+        dma_tile(0, 0);
+
+    // V^T reads: in each 16-lane group G, lane 4 j + y addresses head dims 16 (G % 2) + 4 y .. + 3 of key 8 (G / 2)
+    // + j (+ 4 for the second read, + 16 for keys 16 .. 31) of a 32-dim block, and receives those dims' values for
+    // four keys. Unit 2 db + G % 2 of key row j sits at v_unit(...): db even and odd differ in bit 1.
+    const uint32_t gj = (lane >> 2) & 3u, gy = lane & 3u, gg = (lane >> 4) & 1u;
+    const uint32_t v_even = (8 * g + gj) * (2 * kLD) + 32 * (gg ^ gj) + 8 * gy;
+    const uint32_t v_odd = (8 * g + gj) * (2 * kLD) + 32 * ((gg ^ gj) ^ 2u) + 8 * gy;
+
+    f32x16 oacc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+        oacc[db] = f32x16{};
+    float m = -INFINITY, l = 0.0f;  // running maximum (base-2 domain) and sum of this lane's keys
+    const float c = p.scale_log2;
+
+    for (uint32_t t = 0; t < nt; ++t) {
+        const uint32_t buf = t & 1;
+        // this wave's DMAs of tile t have landed; past the barrier, the other wave's too, and neither reads the
+        // buffer of tile t - 1 any more
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + 1 < nt)
+            dma_tile(t + 1, buf ^ 1);
+        uint32_t j0, hi;
+        tile_of(t, j0, hi);
+        const unsigned char* kbuf = lds + buf * kLBuf;
+        const unsigned char* vbuf = kbuf + kLKImg;
+        // bit i: key j0 + i valid and before the pass's end
+        const uint32_t vflag = vbuf[kLVImg + c32];
+        const uint32_t vmask = (uint32_t)__ballot(vflag != 0 && j0 + c32 < hi);
+        if (!live || vmask == 0 || (p.causal && j0 > q0 + 31))
+            continue;
+        // S^T for the tile: register r holds key j0 + 16 (r / 8) + 8 g + r % 8.
+        f32x16 s = f32x16{};
+        {
+            const unsigned char* kr = kbuf + c32 * kLKRow + 16 * g;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+                s = E::mfma32(*reinterpret_cast<const V8*>(kr + 32 * kk), qreg[kk], s);
+        }
+        if (vmask != 0xffffffffu || (p.causal && j0 + kLKeys - 1 > q0)) {
+            // this lane's 16 keys' bits, in register order
+            const uint32_t lm = ((vmask >> (8 * g)) & 0xffu) | (((vmask >> (16 + 8 * g)) & 0xffu) << 8);
+            const int lim = p.causal ? (int)row - (int)j0 : 1 << 30;  // keys j0 + kidx <= row
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int kidx = 16 * (r >> 3) + 8 * (int)g + (r & 7);
+                const bool seen = ((lm >> r) & 1u) && kidx <= lim;
+                s[r] = seen ? s[r] : -INFINITY;
+            }
+        }
+        float mx0 = fmaxf(s[0], s[1]), mx1 = fmaxf(s[2], s[3]), mx2 = fmaxf(s[4], s[5]), mx3 = fmaxf(s[6], s[7]);
+        mx0 = fmaxf(mx0, fmaxf(s[8], s[9]));
+        mx1 = fmaxf(mx1, fmaxf(s[10], s[11]));
+        mx2 = fmaxf(mx2, fmaxf(s[12], s[13]));
+        mx3 = fmaxf(mx3, fmaxf(s[14], s[15]));
+        float mx = fmaxf(fmaxf(mx0, mx1), fmaxf(mx2, mx3));
+        mx = fmaxf(mx, swap_halves(mx)) * c;
+        float f = 1.0f;
+        if (mx > m + kLRescale) {
+            f = exp2_fast(m - mx);
+            m = mx;
+        }
+        l *= f;
+        if (__any(f != 1.0f))
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[db][r] *= f;
+        const float mu = m == -INFINITY ? 0.0f : m;
+        V8 pb[2];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            f16x8 pv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = exp2_fast(fmaf(s[8 * cc + e], c, -mu));
+                l += x;
+                pv[e] = (_Float16)x;
+            }
+            pb[cc] = pv;
+        }
+        // O^T += V^T P^T: keys 16 cc .. 16 cc + 15, head dims 32 db .. 32 db + 31.
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const unsigned char* va = vbuf + ((db & 1) ? v_odd : v_even) + 128 * (db >> 1) + 16 * cc * (2 * kLD);
+                const s16x4 lo = tr_read(va), hi4 = tr_read(va + 4 * (2 * kLD));
+                const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                oacc[db] = E::mfma32(a, pb[cc], oacc[db]);
+            }
+    }
+
+    // Normalise and store through the row map; the LSE by tile row.
+    const float lt = l + swap_halves(l);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (live && row < p.n_q) {
+        const int32_t dst = p.map[row];
+        if (dst >= 0) {
+            TO* orow = static_cast<TO*>(p.o) + (size_t)dst * p.width + (size_t)h * kLD;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    store4<TO>(orow + 32 * db + 8 * r4 + 4 * g, oacc[db][4 * r4] * inv, oacc[db][4 * r4 + 1] * inv,
+                               oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
+            if (p.lse && g == 0)
+                p.lse[(size_t)h * p.q_pad + row] = lt > 0.0f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
+        }
+    }
+}
+
+}  // namespace
+
+// Whether a call takes flash_sparse_lists: f16 inputs, a list per query head, dense0 and k_pad multiples of 32 (so
+// every tile's validity bytes lie inside valid's k_pad), valid 16-byte aligned, and the offsets in range.
+bool sparse_lists_fits(const mako_sparse_args* a, mako_dtype in, const void* valid)
+{
+    return in == MAKO_F16 && a->kv_heads && a->heads % a->kv_heads == 0 && a->sel_heads == a->heads &&
+           a->dense0 % 32 == 0 && a->k_pad % 32 == 0 && (reinterpret_cast<uintptr_t>(valid) & 15u) == 0 &&
+           (uint64_t)a->q_pad * 256 < (1ull << 31) && (uint64_t)a->k_pad * 256 < (1ull << 32) &&
+           (uint64_t)a->heads * ((a->n_q + 63) / 64) < (1ull << 31);
+}
+
+template <class TO>
+void launch_sparse_lists(const mako_sparse_args* a, float scale_log2, const void* q, const void* k, const void* v,
+                         void* o, const uint16_t* sel, const uint16_t* nsel, const uint8_t* valid,
+                         const int32_t* map, float* lse, hipStream_t s)
+{
+    const uint32_t n_qt = (a->n_q + 63) / 64;
+    const ListsParams p{q,        k,          v,           o,         lse,       sel,       nsel,
+                        valid,    map,        a->n_q,      a->q_pad,  a->n_k,    a->k_pad,  a->heads,
+                        a->heads / a->kv_heads, a->width,  scale_log2, a->n_cubes, a->max_sel, a->dense0,
+                        a->dense1, a->causal ? 1u : 0u, n_qt, a->heads % 8 == 0 ? 1u : 0u};
+    hipLaunchKernelGGL(flash_sparse_lists<TO>, dim3(a->heads * n_qt), dim3(128), 0, s, p);
+}
+
+template void launch_sparse_lists<float>(const mako_sparse_args*, float, const void*, const void*, const void*,
+                                         void*, const uint16_t*, const uint16_t*, const uint8_t*, const int32_t*,
+                                         float*, hipStream_t);
+template void launch_sparse_lists<_Float16>(const mako_sparse_args*, float, const void*, const void*, const void*,
+                                            void*, const uint16_t*, const uint16_t*, const uint8_t*,
+                                            const int32_t*, float*, hipStream_t);
+
+}  // namespace mako

@@ -272,3 +272,55 @@ def test_shared_lists_grouped(heads, kv, causal, dt):
         assert np.all(o[~written] == SENTINEL), "rows outside the map were written"
         rows = np.nonzero(map_ >= 0)[0]
         G.assert_lse_close(lse[:, rows], want_l[:, rows], "lse")
+
+
+@pytest.mark.parametrize("heads,kv,causal,dt,cubes,dense,cut", [
+    (8, 8, 0, O.F16, 7, 70, 0),     # MHA, heads a multiple of 8 (items dealt by XCD), dense rows past a 32 boundary
+    (16, 4, 1, O.F16, 6, 45, 13),   # GQA with a list per query head, causal, rows past n_q
+    (3, 3, 0, O.F16, 5, 0, 0),      # no dense rows, heads not a multiple of 8
+    (2, 1, 0, O.BF16, 4, 33, 0),    # bf16: the per-head route of the compiled kernel
+])
+def test_per_head_lists(heads, kv, causal, dt, cubes, dense, cut):
+    """A list per query head (sel_heads == heads, as cube_select writes them and MiniMax-H3 calls it): random lists
+    of random lengths (some empty), cubes with invalid rows and one with none past its first half, dense rows, query
+    tiles past the cubes (every key), rows past n_q, and a map that permutes and drops rows, against the oracle in
+    f32 and the input type out."""
+    topk = 4
+    cnt = np.full(cubes, 64, np.uint32)
+    cnt[1], cnt[-1] = 37, 20  # the last cube's second 32-key tile has no valid key
+    n = cubes * 64 + dense
+    q_pad, k_pad = (n + 63) // 64 * 64, (n + 127) // 128 * 128
+    n_q = n - cut
+    valid = np.zeros(k_pad, np.uint8)
+    for c in range(cubes):
+        valid[c * 64:c * 64 + cnt[c]] = 1
+    valid[cubes * 64:n] = 1
+    rng = np.random.default_rng(100 + heads + causal)
+    keep = np.nonzero(valid[:n_q])[0]
+    map_ = np.full(q_pad, -1, np.int32)
+    map_[keep] = rng.permutation(len(keep)).astype(np.int32)
+    map_[keep[::9]] = -1
+    sel = np.zeros((heads, cubes, topk), np.uint16)
+    nsel = np.zeros((heads, cubes), np.uint16)
+    for h in range(heads):
+        for c in range(cubes):
+            pool = np.arange(c + 1) if causal else np.arange(cubes)
+            ch = rng.permutation(pool)[:rng.integers(0, topk + 1)]
+            sel[h, c, :len(ch)] = ch
+            nsel[h, c] = len(ch)
+    qb, kb, vb = (G.randn_bits(rng, (hh, pad, 128), dt) for hh, pad in ((heads, q_pad), (kv, k_pad), (kv, k_pad)))
+    args = dict(n_q=n_q, q_pad=q_pad, n_k=n, k_pad=k_pad, heads=heads, kv_heads=kv, n_cubes=cubes, max_sel=topk,
+                dense0=cubes * 64, dense1=n, causal=causal, sel_heads=heads)
+    print(f"per-head lists heads {heads} kv {kv} causal {causal} dtype {dt}", flush=True)
+    want_o, want_l = O.attn_sparse(qb, kb, vb, sel, nsel, valid, map_, dtype=dt, o_fill=np.full((q_pad, heads * 128),
+                                   SENTINEL), **args)
+    for out in (torch.float32, G.TORCH[dt]):
+        o, lse = run_sparse(G.to_dev(qb, dt), G.to_dev(kb, dt), G.to_dev(vb, dt), dev_u16(sel), dev_u16(nsel),
+                            dev(valid), dev(map_), out=out, **args)
+        written = np.zeros(q_pad, bool)
+        written[map_[map_ >= 0]] = True
+        G.assert_attn_close(o[written], want_o[written], "output")
+        G.assert_rows_l2(o[written], want_o[written], "output", 128)
+        assert np.all(o[~written] == SENTINEL), "rows outside the map were written"
+        rows = np.nonzero(map_ >= 0)[0]
+        G.assert_lse_close(lse[:, rows], want_l[:, rows], "lse")
