@@ -61,8 +61,43 @@ __device__ __forceinline__ void dma16_at(uint32_t m0, uint32_t voff, uint32_t so
 #pragma clang diagnostic pop
 }
 
+// Whether the 32 bytes at p (4-byte aligned, read-only in the kernel, a wave-uniform address) are all zero: one
+// scalar load.
+__device__ __forceinline__ bool bytes32_zero(const uint8_t* p)
+{
+    typedef uint32_t u32x8a __attribute__((ext_vector_type(8), aligned(4)));
+    typedef const __attribute__((address_space(4))) u32x8a const_u32x8;
+    const u32x8a x = *reinterpret_cast<const_u32x8*>(reinterpret_cast<uintptr_t>(p));
+    return ((x[0] | x[1]) | (x[2] | x[3]) | (x[4] | x[5]) | (x[6] | x[7])) == 0;
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// x over lanes l and l ^ 32 (the two halves of a wave hold the two key halves of a row): the larger and the sum,
+// both halves getting the same bits. v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
+// lower 32 of its second, so with x in both, one holds x of lanes 0-31 in every lane and the other x of lanes 32-63:
+// no LDS round trip. The instruction goes through inline asm because this compiler's builtin returns the first
+// operand for both results; the s_nop gives the preceding VALU write its wait states.
+__device__ __forceinline__ void lane_halves(float x, float& lo, float& hi)
+{
+    uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    lo = __builtin_bit_cast(float, a);
+    hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float pair_max(float x)
+{
+    float lo, hi;
+    lane_halves(x, lo, hi);
+    return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float pair_sum(float x)
+{
+    float lo, hi;
+    lane_halves(x, lo, hi);
+    return lo + hi;
+}
 
 // Four f16 of V^T by a transpose read at LDS byte `at` of this wave's group pattern.
 __device__ __forceinline__ s16x4 tr_read(const unsigned char* at)
@@ -70,7 +105,7 @@ __device__ __forceinline__ s16x4 tr_read(const unsigned char* at)
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at));
 }
 
-template <class TO>
+template <class TO, bool CAUSAL>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_sparse_lists(
     const ListsParams p)
 {
@@ -141,20 +176,23 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     kd[4] = kd_of(8);
     const uint32_t lbase = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
-    auto dma_tile = [&](uint32_t t, uint32_t buf) __attribute__((always_inline)) {
-        uint32_t j0, hi;
-        tile_of(t, j0, hi);
-        const uint32_t kb = lbase + buf * kLBuf, vb = kb + kLKImg;
+    // A tile's K image and validity bytes, and its V image, into buffer buf.
+    auto dma_k = [&](uint32_t j0, uint32_t buf) __attribute__((always_inline)) {
+        const uint32_t kb = lbase + buf * kLBuf;
         const uint32_t so = __builtin_amdgcn_readfirstlane(j0 * 2 * kLD);
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             dma16_at(kb + 1024 * (4 * w + m), kd[m], so, krs);
         dma16_at(kb + 1024 * 8, kd[4], so, krs);
+        if (w == 0 && lane < 2)
+            dma16_at(kb + kLKImg + kLVImg, 16 * lane, j0, brs);
+    };
+    auto dma_v = [&](uint32_t j0, uint32_t buf) __attribute__((always_inline)) {
+        const uint32_t vb = lbase + buf * kLBuf + kLKImg;
+        const uint32_t so = __builtin_amdgcn_readfirstlane(j0 * 2 * kLD);
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             dma16_at(vb + 1024 * (4 * w + m), vd[m], so, vrs);
-        if (w == 0 && lane < 2)
-            dma16_at(vb + kLVImg, 16 * lane, j0, brs);
     };
 
     // Q: the B operand, lane (c32, g) holds row q0 + c32, head dims 16 kk + 8 g .. + 7 (rows past n_q load as 0).
@@ -169,15 +207,58 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int kk = 0; kk < 8; ++kk)
             settle(qreg[kk]);
     }
-    if (nt > 0)
-        dma_tile(0, 0);
-
     // V^T reads: in each 16-lane group G, lane 4 j + y addresses head dims 16 (G % 2) + 4 y .. + 3 of key 8 (G / 2)
     // + j (+ 4 for the second read, + 16 for keys 16 .. 31) of a 32-dim block, and receives those dims' values for
     // four keys. Unit 2 db + G % 2 of key row j sits at v_unit(...): db even and odd differ in bit 1.
     const uint32_t gj = (lane >> 2) & 3u, gy = lane & 3u, gg = (lane >> 4) & 1u;
     const uint32_t v_even = (8 * g + gj) * (2 * kLD) + 32 * (gg ^ gj) + 8 * gy;
     const uint32_t v_odd = (8 * g + gj) * (2 * kLD) + 32 * ((gg ^ gj) ^ 2u) + 8 * gy;
+
+    // The tile sequence, leaving out cube tiles whose 32 keys are all invalid (the padding halves of partly filled
+    // cubes: one scalar load of their validity bytes) and, causal, tiles past the workgroup's last row. r: the raw
+    // index of the next candidate.
+    const uint32_t wg_last = qt * 64 + 63;
+    auto next_tile = [&](uint32_t& r, uint32_t& j0, uint32_t& hi) __attribute__((always_inline)) {
+        while (r < nt) {
+            const bool is_cube = r < 2 * ns;
+            tile_of(r, j0, hi);
+            ++r;
+            if (CAUSAL && j0 > wg_last)
+                continue;
+            if (is_cube && bytes32_zero(p.valid + j0))
+                continue;
+            return true;
+        }
+        return false;
+    };
+
+    // S^T of the tile whose K image is in buffer buf: register r holds key j0 + 16 (r / 8) + 8 g + r % 8.
+    auto k_scores = [&](uint32_t buf) __attribute__((always_inline)) {
+        f32x16 sc = f32x16{};
+        const unsigned char* kr = lds + buf * kLBuf + c32 * kLKRow + 16 * g;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            sc = E::mfma32(*reinterpret_cast<const V8*>(kr + 32 * kk), qreg[kk], sc);
+        return sc;
+    };
+    // bit i: key j0 + i of the tile in buffer buf valid and before the pass's end
+    auto tile_mask = [&](uint32_t j0, uint32_t hi, uint32_t buf) __attribute__((always_inline)) {
+        const uint32_t vflag = lds[buf * kLBuf + kLKImg + kLVImg + c32];
+        return (uint32_t)__ballot(vflag != 0 && j0 + c32 < hi);
+    };
+    // -inf for the scores of keys not seen: invalid, past the pass's end or (causal) past the lane's row
+    auto mask_scores = [&](f32x16& sc, uint32_t vmask, uint32_t j0) __attribute__((always_inline)) {
+        if (vmask != 0xffffffffu || (CAUSAL && j0 + kLKeys - 1 > q0)) {
+            const uint32_t lm = ((vmask >> (8 * g)) & 0xffu) | (((vmask >> (16 + 8 * g)) & 0xffu) << 8);
+            const int lim = CAUSAL ? (int)row - (int)j0 : 1 << 30;  // keys j0 + kidx <= row
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int kidx = 16 * (r >> 3) + 8 * (int)g + (r & 7);
+                const bool seen = ((lm >> r) & 1u) && (!CAUSAL || kidx <= lim);
+                sc[r] = seen ? sc[r] : -INFINITY;
+            }
+        }
+    };
 
     f32x16 oacc[4];
 #pragma unroll
@@ -186,48 +267,41 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float m = -INFINITY, l = 0.0f;  // running maximum (base-2 domain) and sum of this lane's keys
     const float c = p.scale_log2;
 
-    for (uint32_t t = 0; t < nt; ++t) {
-        const uint32_t buf = t & 1;
-        // this wave's DMAs of tile t have landed; past the barrier, the other wave's too, and neither reads the
-        // buffer of tile t - 1 any more
+    // Two stages: iteration t computes tile t + 1's scores (its K image, DMA'd an iteration ahead of V) beside
+    // tile t's exponentials and P V. Buffer t % 2 holds K(t) and V(t); at iteration t, K(t + 2) and its validity
+    // bytes go to the slot K(t) left and V(t + 1) to the slot V(t - 1) left.
+    uint32_t r = 0, ja = 0, ha = 0, jb = 0, hb = 0;
+    const bool ta = next_tile(r, ja, ha);
+    bool tb = ta && next_tile(r, jb, hb);
+    if (ta) {
+        dma_k(ja, 0);
+        dma_v(ja, 0);
+    }
+    if (tb)
+        dma_k(jb, 1);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    f32x16 s_cur = k_scores(0);
+    mask_scores(s_cur, tile_mask(ja, ha, 0), ja);
+    uint32_t b = 0;
+    bool have = ta;
+    while (have) {
+        uint32_t jc = 0, hc = 0;
+        const bool tc = tb && next_tile(r, jc, hc);
+        // this wave's DMAs of K(t + 1) and V(t) have landed; past the barrier, the other wave's too, and neither
+        // reads the slots of K(t) and V(t - 1) any more
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-        if (t + 1 < nt)
-            dma_tile(t + 1, buf ^ 1);
-        uint32_t j0, hi;
-        tile_of(t, j0, hi);
-        const unsigned char* kbuf = lds + buf * kLBuf;
-        const unsigned char* vbuf = kbuf + kLKImg;
-        // bit i: key j0 + i valid and before the pass's end
-        const uint32_t vflag = vbuf[kLVImg + c32];
-        const uint32_t vmask = (uint32_t)__ballot(vflag != 0 && j0 + c32 < hi);
-        if (!live || vmask == 0 || (p.causal && j0 > q0 + 31))
-            continue;
-        // S^T for the tile: register r holds key j0 + 16 (r / 8) + 8 g + r % 8.
-        f32x16 s = f32x16{};
-        {
-            const unsigned char* kr = kbuf + c32 * kLKRow + 16 * g;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
-                s = E::mfma32(*reinterpret_cast<const V8*>(kr + 32 * kk), qreg[kk], s);
-        }
-        if (vmask != 0xffffffffu || (p.causal && j0 + kLKeys - 1 > q0)) {
-            // this lane's 16 keys' bits, in register order
-            const uint32_t lm = ((vmask >> (8 * g)) & 0xffu) | (((vmask >> (16 + 8 * g)) & 0xffu) << 8);
-            const int lim = p.causal ? (int)row - (int)j0 : 1 << 30;  // keys j0 + kidx <= row
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int kidx = 16 * (r >> 3) + 8 * (int)g + (r & 7);
-                const bool seen = ((lm >> r) & 1u) && kidx <= lim;
-                s[r] = seen ? s[r] : -INFINITY;
-            }
-        }
-        float mx0 = fmaxf(s[0], s[1]), mx1 = fmaxf(s[2], s[3]), mx2 = fmaxf(s[4], s[5]), mx3 = fmaxf(s[6], s[7]);
-        mx0 = fmaxf(mx0, fmaxf(s[8], s[9]));
-        mx1 = fmaxf(mx1, fmaxf(s[10], s[11]));
-        mx2 = fmaxf(mx2, fmaxf(s[12], s[13]));
-        mx3 = fmaxf(mx3, fmaxf(s[14], s[15]));
-        float mx = fmaxf(fmaxf(mx0, mx1), fmaxf(mx2, mx3));
-        mx = fmaxf(mx, swap_halves(mx)) * c;
+        if (tc)
+            dma_k(jc, b);
+        if (tb)
+            dma_v(jb, b ^ 1);
+        // tile t's row maxima and the rescale decision
+        float mx0 = fmaxf(s_cur[0], s_cur[1]), mx1 = fmaxf(s_cur[2], s_cur[3]);
+        float mx2 = fmaxf(s_cur[4], s_cur[5]), mx3 = fmaxf(s_cur[6], s_cur[7]);
+        mx0 = fmaxf(mx0, fmaxf(s_cur[8], s_cur[9]));
+        mx1 = fmaxf(mx1, fmaxf(s_cur[10], s_cur[11]));
+        mx2 = fmaxf(mx2, fmaxf(s_cur[12], s_cur[13]));
+        mx3 = fmaxf(mx3, fmaxf(s_cur[14], s_cur[15]));
+        const float mx = pair_max(fmaxf(fmaxf(mx0, mx1), fmaxf(mx2, mx3))) * c;
         float f = 1.0f;
         if (mx > m + kLRescale) {
             f = exp2_fast(m - mx);
@@ -238,22 +312,28 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    oacc[db][r] *= f;
+                for (int rr = 0; rr < 16; ++rr)
+                    oacc[db][rr] *= f;
+        // tile t + 1's scores (stale bytes when there is none: never used) beside tile t's exponentials
+        const uint32_t vmask_n = tile_mask(jb, hb, b ^ 1);
+        f32x16 s_nxt = k_scores(b ^ 1);
         const float mu = m == -INFINITY ? 0.0f : m;
         V8 pb[2];
+        float l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four chains of the row sum
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             f16x8 pv;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float x = exp2_fast(fmaf(s[8 * cc + e], c, -mu));
-                l += x;
+                const float x = exp2_fast(fmaf(s_cur[8 * cc + e], c, -mu));
+                l4[e & 3] += x;
                 pv[e] = (_Float16)x;
             }
             pb[cc] = pv;
         }
-        // O^T += V^T P^T: keys 16 cc .. 16 cc + 15, head dims 32 db .. 32 db + 31.
+        l += (l4[0] + l4[1]) + (l4[2] + l4[3]);
+        // O^T += V^T P^T for tile t: keys 16 cc .. 16 cc + 15, head dims 32 db .. 32 db + 31.
+        const unsigned char* vbuf = lds + b * kLBuf + kLKImg;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
@@ -263,10 +343,17 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
                 oacc[db] = E::mfma32(a, pb[cc], oacc[db]);
             }
+        mask_scores(s_nxt, vmask_n, jb);
+        s_cur = s_nxt;
+        have = tb;
+        tb = tc;
+        jb = jc;
+        hb = hc;
+        b ^= 1;
     }
 
     // Normalise and store through the row map; the LSE by tile row.
-    const float lt = l + swap_halves(l);
+    const float lt = pair_sum(l);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (live && row < p.n_q) {
         const int32_t dst = p.map[row];
@@ -306,7 +393,10 @@ void launch_sparse_lists(const mako_sparse_args* a, float scale_log2, const void
                         valid,    map,        a->n_q,      a->q_pad,  a->n_k,    a->k_pad,  a->heads,
                         a->heads / a->kv_heads, a->width,  scale_log2, a->n_cubes, a->max_sel, a->dense0,
                         a->dense1, a->causal ? 1u : 0u, n_qt, a->heads % 8 == 0 ? 1u : 0u};
-    hipLaunchKernelGGL(flash_sparse_lists<TO>, dim3(a->heads * n_qt), dim3(128), 0, s, p);
+    if (a->causal)
+        hipLaunchKernelGGL((flash_sparse_lists<TO, true>), dim3(a->heads * n_qt), dim3(128), 0, s, p);
+    else
+        hipLaunchKernelGGL((flash_sparse_lists<TO, false>), dim3(a->heads * n_qt), dim3(128), 0, s, p);
 }
 
 template void launch_sparse_lists<float>(const mako_sparse_args*, float, const void*, const void*, const void*,
