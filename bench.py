@@ -533,8 +533,8 @@ def bench_h3_sparse(torch, M, steps, warmup, with_cpu):
     cubes, the local option 3: a cube and its neighbours one latent-frame step before and after lead each list),
     then attention over the selected cubes plus the dense rows; tiles past the cubes see every key. The layout: a
     960x544 video at 9 latent frames of 34 x 60 patches (18360 video rows in 405 cubes, 25920 rows padded) and 948
-    dense rows: the 19308 rows of the reference's own attention benchmark. Roofline: MFMA, over the pairs the
-    pass lists name (each visited 64-row tile times its keys, masked ones included, as the kernel computes them)."""
+    dense rows: the 19308 rows of the reference's own attention benchmark. Roofline: MFMA, over the unmasked pairs
+    (valid rows against the valid keys of their passes); the pairs of the visited tiles are reported beside them."""
     import numpy as np
 
     H, D, dense, ratio, local = 56, 128, 948, 0.125, 3
@@ -574,15 +574,26 @@ def bench_h3_sparse(torch, M, steps, warmup, with_cpu):
     select()
     torch.cuda.synchronize()
     ns = nsel.cpu().numpy().view(np.uint16).astype(np.int64)
-    pairs = float(64 * (ns * 64 + dense).sum() + H * (rows - n * 64) * rows)
+    sl = sel.cpu().numpy().view(np.uint16).astype(np.int64)
+    # algorithmic work: the unmasked (query row, key) pairs, valid rows against the valid keys of their lists and
+    # the dense rows (the tiles past the cubes: every valid key); the pairs of the visited tiles as information
+    cnt64 = cnt_h.astype(np.int64)
+    kvalid = np.where(np.arange(topk)[None, None, :] < ns[:, :, None], cnt64[sl], 0).sum(-1) + dense
+    pairs = float((cnt64[None, :] * kvalid).sum() + H * (rows - n * 64) * int(valid_h.sum()))
+    # the tiles the kernel computes: 32-key halves of the listed cubes that hold a valid key, the dense rows
+    halves = valid_h[:n * 64].reshape(n, 2, 32).any(-1).sum(-1).astype(np.int64)
+    n_halves = np.where(np.arange(topk)[None, None, :] < ns[:, :, None], halves[sl], 0).sum(-1)
+    visited = float(64 * (32 * n_halves + dense).sum() + H * (rows - n * 64) * rows)
     flop = 4.0 * D * pairs
     ms_sel, kms_sel = time_launches(torch, select, steps, warmup)
     ms_att, kms_att = time_launches(torch, attend, steps, warmup)
     ms, _ = time_launches(torch, call, steps, warmup)
     kt = flop / (kms_att * 1e-3) / 1e12
+    vt = 4.0 * D * visited / (kms_att * 1e-3) / 1e12
     out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
            "attention": {"ms_per_step": round(ms_att, 4), "kernel_ms": round(kms_att, 4),
-                         "tflops": round(kt, 2), "frac": round(kt / PEAK_TFLOPS, 4)},
+                         "tflops": round(kt, 2), "frac": round(kt / PEAK_TFLOPS, 4),
+                         "visited_tflops": round(vt, 2), "visited_frac": round(vt / PEAK_TFLOPS, 4)},
            "cube_select": {"ms_per_step": round(ms_sel, 4), "kernel_ms": round(kms_sel, 4)},
            "dtype": "f16",
            "roofline": {"bound": "mfma", "achieved": kt, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -592,7 +603,10 @@ def bench_h3_sparse(torch, M, steps, warmup, with_cpu):
                                   f"of 64 rows, per-head lists of the top {topk} (1/8, local 3, stride {stride}), "
                                   f"{dense} dense rows, {rows} attention rows mapped to {S} model rows, f16 in, f32 "
                                   "out; value: cube_select + attention a step",
-                      "pairs": pairs, "flop": flop}}
+                      "pairs": pairs, "flop": flop, "visited_pairs": visited,
+                      "flop_note": "unmasked pairs only (valid rows x valid keys); the kernel also computes the "
+                                   "masked rows and keys inside the 32-key tiles it visits (visited_pairs: the "
+                                   "cube padding of the layout)"}}
     if with_cpu:
         import oracle as O
 
