@@ -71,6 +71,22 @@ __device__ __forceinline__ bool bytes32_zero(const uint8_t* p)
     return ((x[0] | x[1]) | (x[2] | x[3]) | (x[4] | x[5]) | (x[6] | x[7])) == 0;
 }
 
+// Where 32-byte unit u (head dims 16 u .. 16 u + 15) of V row k sits in its LDS row: u ^ (k % 4) ^ 4 (u % 2), a
+// bijection of the row's 8 units for each k. A transpose read's 32-lane pass addresses units 2 db and 2 db + 1 of
+// four rows k % 4 = 0 .. 3: the XOR with k % 4 spreads the rows over four units and the 4 (u % 2) term puts the odd
+// unit's group in the other half of the row, so the pass covers the 64 banks once (without it, twice the 32 of one
+// half: a 2-way conflict).
+__device__ __forceinline__ uint32_t lv_unit(uint32_t u, uint32_t k) { return u ^ (k & 3u) ^ (4u * (u & 1u)); }
+// The V byte, relative to a 1 KiB V image piece, that lane's LDS slot holds (byte 16 lane of the piece: row r,
+// physical unit pu, half): the unit lv_unit places at pu, its own inverse up to the parity term.
+__device__ __forceinline__ uint32_t lv_src(uint32_t lane)
+{
+    const uint32_t b = 16 * lane, r = b / 256, pos = b % 256, pu = pos / 32;
+    const uint32_t x = pu ^ (r & 3u);
+    const uint32_t u = x ^ (4u * (x & 1u));
+    return r * 256 + 32 * u + 16 * ((pos / 16) & 1u);
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -163,7 +179,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // K image piece i (1 KiB): lane l's 16 bytes are byte 1024 i + 16 l of the image, row R = that / 272 (key
     // slot_of(R) of the tile), chunk (that % 272) / 16; chunk 16 (the row's padding) and rows past 31 (the spill of
     // piece 8) load any bytes of the tile. Wave w DMAs pieces 4 w .. 4 w + 3 and piece 8 (both waves: the same bytes
-    // to the same place). V image piece i: keys 4 i .. 4 i + 3, lane l's slot holds unit v_unit(u, row) (vd_of).
+    // to the same place). V image piece i: keys 4 i .. 4 i + 3, lane l's slot holds the unit lv_unit places there.
     auto kd_of = [&](uint32_t i) {
         const uint32_t b = 1024 * i + 16 * lane, r = b / kLKRow, ch = b % kLKRow / 16;
         return r < kLKeys && ch < 16 ? slot_of(r) * (2 * kLD) + 16 * ch : 0u;
@@ -172,7 +188,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         kd[m] = kd_of(4 * w + m);
-        vd[m] = 1024 * (4 * w + m) + vd_of<kLD>(lane);
+        vd[m] = 1024 * (4 * w + m) + lv_src(lane);
     }
     kd[4] = kd_of(8);
     const uint32_t lbase = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
@@ -208,11 +224,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             settle(qreg[kk]);
     }
     // V^T reads: in each 16-lane group G, lane 4 j + y addresses head dims 16 (G % 2) + 4 y .. + 3 of key 8 (G / 2)
-    // + j (+ 4 for the second read, + 16 for keys 16 .. 31) of a 32-dim block, and receives those dims' values for
-    // four keys. Unit 2 db + G % 2 of key row j sits at v_unit(...): db even and odd differ in bit 1.
+    // + j (+ 4 for the second read, + 16 for keys 16 .. 31) of 32-dim block db, and receives those dims' values for
+    // four keys: unit u = 2 db + G % 2 of key row j, at lv_unit(u, j) = 4 ((db / 2) ^ (G % 2)) + ((2 (db % 2) + G % 2)
+    // ^ j). Four bases, one for each db % 4; db / 4 is an immediate (none at 128 dims).
     const uint32_t gj = (lane >> 2) & 3u, gy = lane & 3u, gg = (lane >> 4) & 1u;
-    const uint32_t v_even = (8 * g + gj) * (2 * kLD) + 32 * (gg ^ gj) + 8 * gy;
-    const uint32_t v_odd = (8 * g + gj) * (2 * kLD) + 32 * ((gg ^ gj) ^ 2u) + 8 * gy;
+    uint32_t vbase[4];
+#pragma unroll
+    for (int d4 = 0; d4 < 4; ++d4)
+        vbase[d4] = (8 * g + gj) * (2 * kLD) + 32 * lv_unit(2 * d4 + gg, gj) + 8 * gy;
 
     // The tile sequence, leaving out cube tiles whose 32 keys are all invalid (the padding halves of partly filled
     // cubes: one scalar load of their validity bytes) and, causal, tiles past the workgroup's last row. r: the raw
@@ -338,7 +357,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const unsigned char* va = vbuf + ((db & 1) ? v_odd : v_even) + 128 * (db >> 1) + 16 * cc * (2 * kLD);
+                const unsigned char* va = vbuf + vbase[db] + 16 * cc * (2 * kLD);
                 const s16x4 lo = tr_read(va), hi4 = tr_read(va + 4 * (2 * kLD));
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
                 oacc[db] = E::mfma32(a, pb[cc], oacc[db]);
