@@ -481,18 +481,43 @@ def wait_mfma():
     return ["s_nop 7", "s_nop 7", "s_nop 4"]
 
 
-def q_waits():
+def q_waits(mfmas, n_groups):
     """Tile 0's score MFMAs wait for the Q pair (both row blocks of a 16-dim step) they use: fragment 2 kk's MFMAs
-    read Q(., kk), loaded kk-th after tile 0 (tiles 1 and 2 behind them)."""
-    return {2 * kk: [f"s_waitcnt vmcnt({2 * (NKK - 1 - kk) + 2 * DMA_PER_TILE})"] for kk in range(NKK)}
+    read Q(., kk), loaded kk-th after tile 0. Behind Q are the loads still to come of later Q pairs and the LDS DMA
+    loads of tiles 1 and 2 that this phase has issued before the fragment's first MFMA: n_groups loads (one a group),
+    group i after MFMA i * n / n_groups (phase's placement)."""
+    n = len(mfmas)
+    out = {}
+    for kk in range(NKK):
+        first = next(i for i, (f, _) in enumerate(mfmas) if f == 2 * kk)
+        issued = sum(1 for g in range(n_groups) if g * n // n_groups < first)
+        out[2 * kk] = [f"s_waitcnt vmcnt({2 * (NKK - 1 - kk) + issued})"]
+    return out
+
+
+def early_dma():
+    """The LDS DMA loads of tiles 1 and 2 as one (groups, tail) for tile 0's exact path: they are not needed before
+    the first iteration, so they go out between tile 0's score MFMAs instead of ahead of them (issuing them held the
+    prologue for ~4000 cycles). Sparse: each tile's first key (SD) from the pass table's entries 1 and 2, then entry
+    3's for the loop's first staging."""
+    g1, t1 = dma_groups()
+    g2, t2 = dma_groups()
+    if SPARSE:
+        g1 = [["s_mov_b32 %s, s89" % SD] + g1[0]] + g1[1:]
+        g2 = [["s_mov_b32 %s, s90" % SD] + g2[0]] + g2[1:]
+        t2 = t2 + ["s_mov_b32 %s, s91" % SD]
+    return g1 + [t1 + g2[0]] + g2[1:], t2
 
 
 def exact_tile(e, dtype, sbuf, kaddr, j0, first=False, w=None):
     """The exact path for a tile (K at LDS address kaddr, first key in scalar j0): its raw scores into S(sbuf), the
     mask, each row's maximum, the reference's rule for moving the running maximum (outputs and sums rescaled when it
     moves), the exponentials, P and the sums (TMP[0], TMP[4]). first: the wave's first tile, where the outputs and
-    sums are still zero and need no rescaling, and Q is still arriving (q_waits)."""
-    phase(e, "X", k_reads(kaddr), qk_mfmas(dtype, sbuf), [], fwait=q_waits() if first else None)
+    sums are still zero and need no rescaling, Q is still arriving (q_waits), and tiles 1 and 2 are staged
+    between its MFMAs (early_dma)."""
+    mfmas = qk_mfmas(dtype, sbuf)
+    dma = early_dma() if first else None
+    phase(e, "X", k_reads(kaddr), mfmas, [], fwait=q_waits(mfmas, len(dma[0])) if first else None, dma=dma)
     for op in wait_mfma() + (mask_general(sbuf, j0, w) if SPARSE else mask(sbuf, j0)):
         e(op)
     for rb in range(2):
@@ -735,27 +760,24 @@ def body_of(in_dtype, out_dtype):
     e(f"s_mov_b32 {SBW}, 0")
     # M0 is the compiler's: kept in SM0 while the stream uses it, restored at the end
     e(f"s_mov_b32 {SM0}, m0")
-    # tile 0 into buffer 0, then Q into the accumulator registers (rows past n_q load as zeros), then tiles 1 and 2
-    # into buffers 1 and 2; outputs zeroed meanwhile. Loads retire in order: the first barrier waits for tile 0
-    # only, tile 0's score MFMAs each wait for the Q pair they use (q_waits), and a barrier after tile 0 for tile 1.
+    # tile 0 into buffer 0, then Q into the accumulator registers (rows past n_q load as zeros); outputs zeroed
+    # meanwhile; tiles 1 and 2 go into buffers 1 and 2 between tile 0's score MFMAs (early_dma). Loads retire in
+    # order: the first barrier waits for tile 0 only, tile 0's score MFMAs each wait for the Q pair they use
+    # (q_waits), and a barrier after tile 0 for tile 1.
     e(f"s_mov_b32 {SKW}, %[skw]")
     e(f"s_mov_b32 {SKWW}, %[skww]")
     e(f"s_mov_b32 {SVWW}, %[svww]")
     if SPARSE:
         e("s_waitcnt lgkmcnt(0)")
-    for i in range(3):
-        if SPARSE:
-            e(f"s_mov_b32 {SD}, s{88 + i}")
-        for op in dma_issue():
-            e(op)
-        if i == 0:
-            e(f"v_add_u32 {TMP[0]}, {64 * D:#x}, %[qo]")   # row block 1: 32 rows of 2 d bytes on
-            for kk in range(NKK):
-                for rb in range(2):
-                    e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen "
-                      f"offset:{32 * kk}")
     if SPARSE:
-        e(f"s_mov_b32 {SD}, s91")
+        e(f"s_mov_b32 {SD}, s88")
+    for op in dma_issue():
+        e(op)
+    e(f"v_add_u32 {TMP[0]}, {64 * D:#x}, %[qo]")   # row block 1: 32 rows of 2 d bytes on
+    for kk in range(NKK):
+        for rb in range(2):
+            e(f"buffer_load_dwordx4 {Q(rb, kk)}, {'%[qo]' if rb == 0 else TMP[0]}, %[qrs], 0 offen "
+              f"offset:{32 * kk}")
     # the outputs cleared by MFMAs of zero operands: a few issue slots, the matrix unit does the rest (128
     # v_accvgpr_write took ~700 cycles of the prologue)
     z = f"v[{TMP[8][1:]}:{TMP[11][1:]}]"
@@ -769,12 +791,14 @@ def body_rest(e, in_dtype, out_dtype):
     e(f"s_mov_b32 {SJ}, 0")
     e(f"s_mov_b32 {SBK}, 0")
     e(f"s_mov_b32 {SBV}, 0")
-    # the first barrier: every wave's loads of tile 0 have landed (Q and tiles 1 and 2 may still be in flight)
-    e(f"s_waitcnt vmcnt({2 * NKK + 2 * DMA_PER_TILE}) lgkmcnt(0)")
+    # the first barrier: every wave's loads of tile 0 have landed (Q may still be in flight)
+    e(f"s_waitcnt vmcnt({2 * NKK}) lgkmcnt(0)")
     e("s_barrier")
     e("s_cmp_eq_u32 %[ntw], 0")
     e(f"s_cbranch_scc0 {lbl('L_live')}")
-    for op in barrier():   # a wave with no rows: the barrier for tile 1 as the others, then the load-only loop
+    # a wave with no rows: its share of tiles 1 and 2, the barrier for tile 1 as the others, then the load-only loop
+    groups, tail = early_dma()
+    for op in sum(groups, []) + tail + barrier():
         e(op)
     e(f"s_branch {lbl('L_tail')}")
     e.label("L_live")

@@ -181,6 +181,15 @@ def test_planted_missing_low_part_pass_is_found(monkeypatch):
 def test_planted_missing_q_wait_is_found(monkeypatch):
     """Tile 0's score MFMAs start while Q is still arriving: without the per-pair waits they read Q registers whose
     loads have not landed."""
-    monkeypatch.setattr(G, "q_waits", lambda: {})
+    monkeypatch.setattr(G, "q_waits", lambda mfmas, n_groups: {})
+    r = R.run(4, 1, 64, 200, 0, 0, seed=9, verbose=False)
+    assert r["out_bad"] > 0
+
+
+def test_planted_q_waits_that_miscount_the_early_dma_are_found(monkeypatch):
+    """Tiles 1 and 2 are staged between tile 0's score MFMAs, so a Q wait counts only the DMA loads issued before
+    it. Waits that count all of them (as when both tiles went out ahead of Q) let MFMAs read Q before it lands."""
+    monkeypatch.setattr(G, "q_waits", lambda mfmas, n_groups: {
+        2 * kk: [f"s_waitcnt vmcnt({2 * (G.NKK - 1 - kk) + n_groups})"] for kk in range(G.NKK)})
     r = R.run(4, 1, 64, 200, 0, 0, seed=9, verbose=False)
     assert r["out_bad"] > 0
