@@ -377,11 +377,56 @@ __global__ __launch_bounds__(256) void cube_scores(const double* __restrict__ qp
 // sel[h][qc][0 .. kk) (kk = min(topk, n)): the local cubes first, then repeated argmax (the larger score, the
 // smaller index on ties); nsel[h][qc] = kk. One wave per (qc, h), n <= 64 P: lane l keeps scores l, l + 64, ...
 // (P doubles) in registers and the best of them (value, index: a strict > scan in index order keeps the smaller
-// index of equal values; no score yet: -inf at index 0). A pick is the wave's best pair by a butterfly of shuffles
-// (the larger value, the smaller index on ties); the lane that holds it drops that score (-inf) and rescans its own.
-// So a pick is six shuffle steps and one lane's rescan of P registers, with no LDS round trip or workgroup barrier.
+// index of equal values; no score yet: -inf at index 0). A pick is the wave's best pair by six pairing steps (the
+// larger value, the smaller index on ties): four DPP moves inside 16-lane rows, then the row and half swaps; the
+// lane that holds it drops that score (-inf) and rescans its own. So a pick is a few dozen vector instructions and
+// one lane's rescan of P registers, with no LDS round trip or workgroup barrier.
 // As the reference's rule: a local cube's score is dropped once picked; when every remaining score is -inf the
 // pick is index 0.
+// Folds (ov, oi) into (v, i): the larger value, the smaller index on ties (the selection's order).
+__device__ __forceinline__ void take_better(double& v, uint32_t& i, double ov, uint32_t oi)
+{
+    const bool take = ov > v || (ov == v && oi < i);
+    v = take ? ov : v;
+    i = take ? oi : i;
+}
+
+// One step of the wave's argmax on the DPP path: each lane takes the better of its pair and its partner's, the
+// partner given by CTRL (quad_perm [1, 0, 3, 2]: lane ^ 1; [2, 3, 0, 1]: lane ^ 2; row half-mirror: 7 - lane within
+// 8; row mirror: 15 - lane within 16), all moves inside a 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(double& v, uint32_t& i)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+    const uint32_t oi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)i, CTRL, 0xf, 0xf, false);
+    take_better(v, i, __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo), oi);
+}
+
+// The steps across rows: v_permlane16_swap exchanges the odd rows of its first operand with the even rows of its
+// second, v_permlane32_swap the upper half of the first with the lower half of the second; given the pair twice,
+// the two results hold the values of the two rows (halves) being joined, in the same order in every lane of both,
+// so both end with the same pair. Inline asm: this compiler's builtins return the first operand for both results;
+// the s_nops give the preceding VALU writes, and the swaps' own results, their wait states.
+template <bool HALVES>
+__device__ __forceinline__ void argmax_swap(double& v, uint32_t& i)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    uint32_t l0 = (uint32_t)b, l1 = l0, h0 = (uint32_t)(b >> 32), h1 = h0, i0 = i, i1 = i;
+    if (HALVES)
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\tv_permlane32_swap_b32 %2, %3\n\t"
+                     "v_permlane32_swap_b32 %4, %5\n\ts_nop 1"
+                     : "+v"(l0), "+v"(l1), "+v"(h0), "+v"(h1), "+v"(i0), "+v"(i1));
+    else
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_permlane16_swap_b32 %2, %3\n\t"
+                     "v_permlane16_swap_b32 %4, %5\n\ts_nop 1"
+                     : "+v"(l0), "+v"(l1), "+v"(h0), "+v"(h1), "+v"(i0), "+v"(i1));
+    v = __builtin_bit_cast(double, ((uint64_t)h0 << 32) | l0);
+    i = i0;
+    take_better(v, i, __builtin_bit_cast(double, ((uint64_t)h1 << 32) | l1), i1);
+}
+
 template <uint32_t P>
 __device__ __forceinline__ void best_of(const double (&v)[P], uint32_t lane, uint32_t n, double& bv, uint32_t& bi)
 {
@@ -430,15 +475,12 @@ __global__ __launch_bounds__(64) void cube_topk(const double* __restrict__ sc, u
     for (; it < kk; ++it) {
         double wv = bv;
         uint32_t wi = bi;
-#pragma unroll
-        for (uint32_t o = 32; o > 0; o >>= 1) {
-            const double ov = __shfl_xor(wv, o);
-            const uint32_t oi = __shfl_xor(wi, o);
-            if (ov > wv || (ov == wv && oi < wi)) {
-                wv = ov;
-                wi = oi;
-            }
-        }
+        argmax_dpp<0xb1>(wv, wi);    // quad_perm [1, 0, 3, 2]
+        argmax_dpp<0x4e>(wv, wi);    // quad_perm [2, 3, 0, 1]
+        argmax_dpp<0x141>(wv, wi);   // row half-mirror
+        argmax_dpp<0x140>(wv, wi);   // row mirror
+        argmax_swap<false>(wv, wi);  // rows 0 / 1 and 2 / 3
+        argmax_swap<true>(wv, wi);   // halves
         if (lane == 0)
             out[it] = (uint16_t)wi;
         if (lane == wi % 64) {  // the holder drops the pick and finds its next best
