@@ -218,67 +218,66 @@ __global__ __launch_bounds__(256, 1) void proj_tiles(const ProjParams a)
     }
 }
 
-// bf16 activations: both operands go global -> LDS by the LDS DMA (global_load_lds_dwordx4: lane l of a wave writes
-// 16 bytes at the wave's LDS base + 16 l, from any address of its choosing), with no register staging, through a
-// ring of four 32-wide K stages (128 KB); a stage is refilled three chunks ahead. LDS rows are 64 bytes here: run c of
-// row r sits at position c ^ ((r / 4) % 4), so the 16 lanes of a ds_read_b128 (16 consecutive rows, one run) hit 64
-// distinct banks; a DMA instruction writes 16 rows (1 KB), lane l taking row l / 4 at position l % 4.
-constexpr int kDK = 32, kStages = 4;
-
-__device__ __forceinline__ uint32_t dpos(uint32_t row, uint32_t run) { return row * kDK + ((run ^ ((row >> 2) & 3u)) << 3); }
-
-// s_waitcnt vmcnt(n) (this wave's DMA of all but the last n / 8 chunks issued is in LDS), then the workgroup barrier.
-// The compiler's own barrier would also wait for the chunks still in flight.
-template <int N>
-__device__ __forceinline__ void dma_barrier()
+// A raw buffer descriptor over the rows of a tile's panel from `base` (rows of ld values, `rows` of them left in the
+// operand): reads at or past the end return zeros.
+__device__ __forceinline__ u32x4 panel_rsrc(const __bf16* base, uint32_t rows, uint32_t ld)
 {
-    if constexpr (N == 24)
-        asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 16)
-        asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 8)
-        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint64_t a = reinterpret_cast<uint64_t>(base), bytes = (uint64_t)rows * ld * 2;
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, (uint32_t)min(bytes, (uint64_t)0xffffffffu), 0x00020000u};
 }
+
+// bf16 activations: both operands go global -> LDS by the LDS DMA (buffer_load_dwordx4 ... lds: lane l of a wave
+// writes 16 bytes at the wave's LDS base + 16 l, from any offset of its choosing in the tile's panel), with no
+// register staging. A stage holds 64 K values of the tile's 256 x rows and 256 w rows (128 bytes a row, so the DMA of
+// a row reads whole 128-byte lines; 32-wide stages, which read half lines, ran 3 % slower), two stages (128 KB), one
+// barrier a stage: the DMA of stage q + 1 goes out in the first 16 MFMA slots after barrier q, the fragment reads one
+// every other slot, a K step ahead of their MFMAs. LDS rows are 128 bytes; the 16-byte run c of row r sits at
+// position c ^ ((r / 2) % 8), so the 16 lanes of a ds_read_b128 (16 consecutive rows, one run) hit 64 distinct banks.
+// A DMA instruction writes 8 rows (1 KB), lane l taking row l / 8 at position l % 8.
+constexpr int kEK = 64;
+
+__device__ __forceinline__ uint32_t epos(uint32_t row, uint32_t run) { return row * kEK + ((run ^ ((row >> 1) & 7u)) << 3); }
 
 __global__ __launch_bounds__(256, 1) void proj_dma(const ProjParams a)
 {
-    __shared__ __attribute__((aligned(16))) __bf16 as[kStages][kBN * kDK];
-    __shared__ __attribute__((aligned(16))) __bf16 bs[kStages][kBN * kDK];
+    __shared__ __attribute__((aligned(16))) __bf16 as[2][kBN * kEK];
+    __shared__ __attribute__((aligned(16))) __bf16 bs[2][kBN * kEK];
     uint32_t tm, tn;
     if (!tile_of(a, tm, tn))
         return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, c32 = lane & 31;
     const uint32_t t0 = tm * kBN, n0 = tn * kBN;
     const __bf16* x = static_cast<const __bf16*>(a.x);
-    // DMA: wave w moves tile rows 64 w .. 64 w + 63 of both operands, four instructions of 16 rows each
-    uint32_t xo[4], wo[4];
+    uint32_t xo[8], wo[8];
     #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t row = 64 * w + 16 * i + (lane >> 2), run = (lane & 3) ^ ((row >> 2) & 3);
-        xo[i] = min(t0 + row, a.t - 1) * a.ldx + 8 * run;
-        wo[i] = min(n0 + row, a.n - 1) * a.k + 8 * run;
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t row = 64 * w + 8 * i + (lane >> 3), run = (lane & 7) ^ ((row >> 1) & 7);
+        xo[i] = (min(t0 + row, a.t - 1) - t0) * a.ldx * 2 + 16 * run;
+        wo[i] = (min(n0 + row, a.n - 1) - n0) * a.k * 2 + 16 * run;
     }
-    // The DMA is issued as inline asm: the compiler, seeing the builtin, waits for every DMA in flight before any
-    // LDS read (it cannot tell the stages apart), which would leave nothing in flight. Here the only waits are
-    // dma_barrier's, which count this wave's DMA instructions (8 a chunk).
-    const uint32_t wl = __builtin_amdgcn_readfirstlane(64 * w * kDK * 2);  // this wave's first row, LDS byte offset
-    // M0 (the DMA's LDS base) is listed as clobbered; nothing else in this kernel uses it.
-    auto dma = [&](const __bf16* src, const __bf16* lds) __attribute__((always_inline)) {
-        const uint32_t base = (uint32_t)(uintptr_t)lds;
+    const u32x4 xrs = panel_rsrc(x + (size_t)t0 * a.ldx, a.t - t0, a.ldx);
+    const u32x4 wrs = panel_rsrc(a.w + (size_t)n0 * a.k, a.n - n0, a.k);
+    const uint32_t wl = __builtin_amdgcn_readfirstlane(64 * w * kEK * 2);  // this wave's first row, LDS bytes
+    // The DMA is issued as inline asm: the compiler, seeing the builtin, waits for every DMA in flight before any LDS
+    // read (it cannot tell the stages apart). Here the only waits are the stage barriers'. M0 (the DMA's LDS base) is
+    // listed as clobbered; nothing else in this kernel uses it.
+    auto dma = [&](uint32_t voff, uint32_t soff, u32x4 rs, uint32_t lds) __attribute__((always_inline)) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src) : "memory", "m0");
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff),
+                     "s"(rs), "s"(soff)
+                     : "memory", "m0");
 #pragma clang diagnostic pop
     };
-    auto issue = [&](uint32_t c) __attribute__((always_inline)) {
-        const uint32_t s = c & (kStages - 1), k0 = c * kDK;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            dma(x + (size_t)xo[i] + k0, reinterpret_cast<const __bf16*>(reinterpret_cast<const char*>(as[s]) + wl) + 16 * i * kDK);
-            dma(a.w + (size_t)wo[i] + k0, reinterpret_cast<const __bf16*>(reinterpret_cast<const char*>(bs[s]) + wl) + 16 * i * kDK);
-        }
+    const uint32_t abase = (uint32_t)(uintptr_t)&as[0][0] + wl, bbase = (uint32_t)(uintptr_t)&bs[0][0] + wl;
+    // DMA instruction i (0 .. 15) of K stage q (values 64 q .. 64 q + 63) into LDS stage q % 2: x piece i / 2 (8 rows)
+    // for even i, w piece i / 2 for odd
+    auto dma1 = [&](uint32_t q, int i) __attribute__((always_inline)) {
+        const uint32_t so = 2 * kEK * q, st = (q & 1) * (kBN * kEK * 2) + 1024 * (i / 2);
+        if (i % 2 == 0)
+            dma(xo[i / 2], so, xrs, abase + st);
+        else
+            dma(wo[i / 2], so, wrs, bbase + st);
     };
     f32x16 acc[4][4];
     #pragma unroll
@@ -290,84 +289,74 @@ __global__ __launch_bounds__(256, 1) void proj_dma(const ProjParams a)
     struct Frag {
         bf16x8 x[4], w[4];
     };
-    auto read = [&](Frag& f, uint32_t s, int kk) __attribute__((always_inline)) {
+    // pieces 0 .. 7 of a fragment: x0, w0, w1, w2, w3, x1, x2, x3, the order the MFMAs (bi outer, bj inner) use them
+    auto read1 = [&](Frag& f, uint32_t st, int kk, int piece) __attribute__((always_inline)) {
         const uint32_t rn = 2 * kk + g;
-        #pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
-            f.x[bi] = *reinterpret_cast<const bf16x8*>(as[s] + dpos(ra + 32 * bi + c32, rn));
-        #pragma unroll
-        for (int bj = 0; bj < 4; ++bj)
-            f.w[bj] = *reinterpret_cast<const bf16x8*>(bs[s] + dpos(rb + 32 * bj + c32, rn));
-    };
-    auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
-        #pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
-            #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
-                acc[bi][bj] = Elem<__bf16>::mfma32(f.x[bi], f.w[bj], acc[bi][bj]);
-    };
-    // Software-pipelined by one K step across the barrier: the barrier that admits chunk j + 1 sits between the
-    // two MFMA steps of chunk j, so the first step's operands of chunk j + 1 are read while chunk j's second step
-    // runs, and its second step's operands while chunk j + 1's first step runs. At that barrier every wave has its
-    // chunk-j operands in registers, so stage j % 4 is free and takes chunk j + 4.
-    const uint32_t nk = a.k / kDK;
-    for (uint32_t c = 0; c < kStages && c < nk; ++c)
-        issue(c);
-    // The 8 LDS reads of a step go out one behind each of the first 8 of the 16 MFMAs they overlap, not as a burst
-    // ahead of them.
-    auto interleave = []() __attribute__((always_inline)) {
-        #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        if (piece == 0 || piece >= 5) {
+            const int bi = piece == 0 ? 0 : piece - 4;
+            f.x[bi] = *reinterpret_cast<const bf16x8*>(as[st] + epos(ra + 32 * bi + c32, rn));
+        } else {
+            const int bj = piece - 1;
+            f.w[bj] = *reinterpret_cast<const bf16x8*>(bs[st] + epos(rb + 32 * bj + c32, rn));
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     };
+    // 16 MFMAs on `use`; the reads of `next` (LDS stage st, K step kk of its four) on the even slots; with DMA, the 16
+    // instructions of K stage q, one a slot
+    auto half = [&](const Frag& use, Frag& next, uint32_t st, int kk, auto DMA, uint32_t q) __attribute__((always_inline)) {
+        #pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[i / 4][i % 4] = Elem<__bf16>::mfma32(use.x[i / 4], use.w[i % 4], acc[i / 4][i % 4]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i % 2 == 0 && kk >= 0)
+                read1(next, st, kk, i / 2);
+            if constexpr (decltype(DMA)::value)
+                dma1(q, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using Y = std::true_type;
+    using N = std::false_type;
+    const uint32_t nq = a.k / kEK;  // >= 1
     Frag fa, fb;
-    if (nk > 3)
-        dma_barrier<24>();
-    else if (nk > 2)
-        dma_barrier<16>();
-    else
-        dma_barrier<8>();  // nk >= 2 (k a multiple of 64)
-    read(fa, 0, 0);
-    read(fb, 0, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa);
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t j = 0;
-    for (; j + 4 < nk; ++j) {  // steady: chunks j + 2 .. j + 3 may be in flight at the barrier
-        dma_barrier<16>();
-        issue(j + 4);
-        __builtin_amdgcn_sched_barrier(0);
-        read(fa, (j + 1) & (kStages - 1), 0);
-        mfmas(fb);
-        interleave();
-        __builtin_amdgcn_sched_barrier(0);
-        read(fb, (j + 1) & (kStages - 1), 1);
-        mfmas(fa);
-        interleave();
-        __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+    for (int i = 0; i < 16; ++i)
+        dma1(0, i);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    #pragma unroll
+    for (int i = 0; i < 8; ++i)
+        read1(fa, 0, 0, i);
+    if (nq > 1) {
+        #pragma unroll
+        for (int i = 0; i < 16; ++i)
+            dma1(1, i);
     }
-    for (; j + 1 < nk; ++j) {  // the last chunks: nothing more to issue
-        if (j + 3 < nk)
-            dma_barrier<16>();
-        else if (j + 2 < nk)
-            dma_barrier<8>();
-        else
-            dma_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    half(fa, fb, 0, 1, N{}, 0);
+    half(fb, fa, 0, 2, N{}, 0);
+    half(fa, fb, 0, 3, N{}, 0);
+    // K stage q: its LDS stage has landed (this wave's DMA by the wait, every wave's by the barrier) and the reads of
+    // stage q - 1 are done, so stage q + 1 goes to the other LDS stage while the last K step of q - 1 and the first
+    // three of q run. The last K stage has nothing to fetch.
+    uint32_t q = 1;
+    for (; q + 1 < nq; ++q) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        read(fa, (j + 1) & (kStages - 1), 0);
-        mfmas(fb);
-        interleave();
-        __builtin_amdgcn_sched_barrier(0);
-        read(fb, (j + 1) & (kStages - 1), 1);
-        mfmas(fa);
-        interleave();
-        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t st = q & 1;
+        half(fb, fa, st, 0, Y{}, q + 1);
+        half(fa, fb, st, 1, N{}, 0);
+        half(fb, fa, st, 2, N{}, 0);
+        half(fa, fb, st, 3, N{}, 0);
     }
-    mfmas(fb);
-    // acc[bi][bj] register r of lane (c32, g): row t0 + ra + 32 bi + 8 (r / 4) + 4 g + r % 4, column n0 + rb + 32 bj + c32
+    if (q < nq) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t st = q & 1;
+        half(fb, fa, st, 0, N{}, 0);
+        half(fa, fb, st, 1, N{}, 0);
+        half(fb, fa, st, 2, N{}, 0);
+        half(fa, fb, st, 3, N{}, 0);
+    }
+    half(fb, fa, 0, -1, N{}, 0);
     #pragma unroll
     for (int bj = 0; bj < 4; ++bj) {
         const uint32_t c = n0 + rb + 32 * bj + c32;

@@ -253,6 +253,7 @@ def proj_rc(**kw):
     (dict(args=dict(ldx=4100)), M.EINVAL, "ldx a multiple of 8"),
     (dict(x=ctypes.c_void_p(FAKE.value + 8)), M.EINVAL, "16-byte aligned"),
     (dict(args=dict(t=1 << 20, ldx=8192)), M.EINVAL, "exceed 2^32"),
+    (dict(args=dict(t=256, ldx=1 << 23)), M.EINVAL, "too long for 32-bit tile offsets"),
     (dict(w=None), M.EINVAL, "null"),
 ])
 def test_proj_refuses(kw, code, msg):
