@@ -314,7 +314,7 @@ int mako_idx_dots(const mako_idx_dot_args* a, uint32_t tokens, const float* q, c
  * src/models/qwen_text.cpp:271): the rounding's remainder bf16(x - bf16(x)) goes through the GEMM too and adds into
  * y. k a multiple of 64 (the reference's "BF16 {k}x{n}: k must be a multiple of 64"); w and x 16-byte aligned, ldx a
  * multiple of 8 elements; t x ldx and n x k at most 2^32 elements, and with bf16 x, 256 rows of x (of w) plus 2 k + 128
- * bytes within 2^32 bytes (ldx and k below about 8.4M): MAKO_EINVAL otherwise.
+ * bytes within 2^32 bytes (ldx and k below about 8.4M elements): MAKO_EINVAL otherwise.
  */
 typedef struct mako_gemm_args {
     uint32_t t, k, n, row_bytes;

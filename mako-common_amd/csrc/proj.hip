@@ -417,6 +417,13 @@ extern "C" int mako_proj_bf16(const mako_gemm_args* a, int x_dtype, int split, c
     ProjParams p{static_cast<const __bf16*>(w), x, y, a->t, a->k, a->n, ldy, ldx, 0, 0, 0, 0};
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (x_dtype == MAKO_BF16) {
+        // a tile's DMA addresses its panels by 32-bit offsets (up to 256 rows, a row's k values, a margin)
+        const auto span = [&](uint32_t rows, uint32_t ld) {
+            return (uint64_t)std::min(rows, 256u) * ld * 2 + 2ull * a->k + 128;
+        };
+        if (span(a->t, ldx) > 0xffffffffu || span(a->n, a->k) > 0xffffffffu)
+            return fail(MAKO_EINVAL, "proj: rows of %u (x) and %u (w) values are too long for 32-bit tile offsets", ldx,
+                        a->k);
         p.tiles_m = (p.t + kBN - 1) / kBN;
         p.tiles_n = (p.n + kBN - 1) / kBN;
         p.tiles = p.tiles_m * p.tiles_n;
