@@ -102,11 +102,28 @@ __device__ __forceinline__ void lane_halves(float x, float& lo, float& hi)
     lo = __builtin_bit_cast(float, a);
     hi = __builtin_bit_cast(float, b);
 }
+// max(a, b, c) by one v_max3_f32: fmaxf on values the compiler cannot prove canonical (MFMA results) is a
+// canonicalising v_max per operand and then the v_max, three instructions for two values.
+__device__ __forceinline__ float max3(float a, float b, float c)
+{
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// x where the lane's bit of the wave mask `keep` is set, -inf elsewhere: one v_cndmask on a scalar lane mask.
+__device__ __forceinline__ float keep_or_ninf(float x, uint64_t keep)
+{
+    float r;
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(-INFINITY), "v"(x), "s"(keep));
+    return r;
+}
+
 __device__ __forceinline__ float pair_max(float x)
 {
     float lo, hi;
     lane_halves(x, lo, hi);
-    return fmaxf(lo, hi);
+    return max3(lo, hi, -INFINITY);
 }
 __device__ __forceinline__ float pair_sum(float x)
 {
@@ -265,9 +282,19 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const uint32_t vflag = lds[buf * kLBuf + kLKImg + kLVImg + c32];
         return (uint32_t)__ballot(vflag != 0 && j0 + c32 < hi);
     };
-    // -inf for the scores of keys not seen: invalid, past the pass's end or (causal) past the lane's row
+    // -inf for the scores of keys not seen: invalid, past the pass's end or (causal) past the lane's row. Without
+    // the causal limit, register r's key is a wave-uniform bit of vmask for each lane half (8 g + r % 8 + 16 (r / 8)),
+    // so its lane mask is two bit tests on the scalar unit and the masking one v_cndmask a register.
     auto mask_scores = [&](f32x16& sc, uint32_t vmask, uint32_t j0) __attribute__((always_inline)) {
-        if (vmask != 0xffffffffu || (CAUSAL && j0 + kLKeys - 1 > q0)) {
+        if (!CAUSAL && vmask != 0xffffffffu) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int b = 16 * (r >> 3) + (r & 7);
+                const uint64_t keep = (((vmask >> b) & 1u) ? 0x00000000ffffffffull : 0ull) |
+                                      (((vmask >> (b + 8)) & 1u) ? 0xffffffff00000000ull : 0ull);
+                sc[r] = keep_or_ninf(sc[r], keep);
+            }
+        } else if (CAUSAL && (vmask != 0xffffffffu || j0 + kLKeys - 1 > q0)) {
             const uint32_t lm = ((vmask >> (8 * g)) & 0xffu) | (((vmask >> (16 + 8 * g)) & 0xffu) << 8);
             const int lim = CAUSAL ? (int)row - (int)j0 : 1 << 30;  // keys j0 + kidx <= row
 #pragma unroll
@@ -314,13 +341,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (tb)
             dma_v(jb, b ^ 1);
         // tile t's row maxima and the rescale decision
-        float mx0 = fmaxf(s_cur[0], s_cur[1]), mx1 = fmaxf(s_cur[2], s_cur[3]);
-        float mx2 = fmaxf(s_cur[4], s_cur[5]), mx3 = fmaxf(s_cur[6], s_cur[7]);
-        mx0 = fmaxf(mx0, fmaxf(s_cur[8], s_cur[9]));
-        mx1 = fmaxf(mx1, fmaxf(s_cur[10], s_cur[11]));
-        mx2 = fmaxf(mx2, fmaxf(s_cur[12], s_cur[13]));
-        mx3 = fmaxf(mx3, fmaxf(s_cur[14], s_cur[15]));
-        const float mx = pair_max(fmaxf(fmaxf(mx0, mx1), fmaxf(mx2, mx3))) * c;
+        const float mx0 = max3(s_cur[0], s_cur[1], s_cur[2]), mx1 = max3(s_cur[3], s_cur[4], s_cur[5]);
+        const float mx2 = max3(s_cur[6], s_cur[7], s_cur[8]), mx3 = max3(s_cur[9], s_cur[10], s_cur[11]);
+        const float mx4 = max3(s_cur[12], s_cur[13], s_cur[14]);
+        const float mx = pair_max(max3(max3(mx0, mx1, mx2), max3(mx3, mx4, s_cur[15]), -INFINITY)) * c;
         float f = 1.0f;
         if (mx > m + kLRescale) {
             f = exp2_fast(m - mx);
