@@ -33,6 +33,7 @@ constexpr uint32_t kLKRow = 2 * kLD + 16;         // 272: LDS bytes of a K image
 constexpr uint32_t kLKImg = 9 * 1024;             // the K image (8704 bytes) and what its ninth 1 KiB piece spills
 constexpr uint32_t kLVImg = kLKeys * 2 * kLD;     // 8 KiB: the V image
 constexpr uint32_t kLBuf = kLKImg + kLVImg + 64;  // and the tile's 32 validity bytes
+constexpr uint32_t kLMaxSel = 256;                 // list entries a query tile (two cube tiles each)
 constexpr float kLRescale = 8.0f;
 
 struct ListsParams {
@@ -59,16 +60,6 @@ __device__ __forceinline__ void dma16_at(uint32_t m0, uint32_t voff, uint32_t so
                  "s"(rsrc), "s"(soff)
                  : "memory", "m0");
 #pragma clang diagnostic pop
-}
-
-// Whether the 32 bytes at p (4-byte aligned, read-only in the kernel, a wave-uniform address) are all zero: one
-// scalar load.
-__device__ __forceinline__ bool bytes32_zero(const uint8_t* p)
-{
-    typedef uint32_t u32x8a __attribute__((ext_vector_type(8), aligned(4)));
-    typedef const __attribute__((address_space(4))) u32x8a const_u32x8;
-    const u32x8a x = *reinterpret_cast<const_u32x8*>(reinterpret_cast<uintptr_t>(p));
-    return ((x[0] | x[1]) | (x[2] | x[3]) | (x[4] | x[5]) | (x[6] | x[7])) == 0;
 }
 
 // Where 32-byte unit u (head dims 16 u .. 16 u + 15) of V row k sits in its LDS row: u ^ (k % 4) ^ 4 (u % 2), a
@@ -145,6 +136,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     using E = Elem<_Float16>;
     using V8 = f16x8;
     __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * kLBuf];
+    __shared__ uint32_t lst[2 * kLMaxSel];  // the first keys of the cube tiles visited, in list order
+    __shared__ uint32_t lcnt[2];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -169,19 +162,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint32_t ns = cube ? min(uniform_u16(p.nsel, (size_t)h * p.n_cubes + qt), p.max_sel) : 0u;
     const uint32_t dlo = cube ? p.dense0 : 0u, dhi = cube ? p.dense1 : p.n_k;
     const uint32_t nd = dhi > dlo ? (dhi - dlo + kLKeys - 1) / kLKeys : 0u;
-    const uint32_t nt = 2 * ns + nd;
-    auto tile_of = [&](uint32_t t, uint32_t& j0, uint32_t& hi) __attribute__((always_inline)) {
-        if (t < 2 * ns) {
-            const uint32_t c0 = uniform_u16(my_sel, t >> 1) * 64;
-            j0 = c0 + kLKeys * (t & 1);
-            hi = c0 + 64;
-        } else {
-            j0 = dlo + kLKeys * (t - 2 * ns);
-            hi = dhi;
-        }
-        j0 = __builtin_amdgcn_readfirstlane(j0);
-        hi = __builtin_amdgcn_readfirstlane(hi);
-    };
 
     // Sources: the kv head's k_pad rows of K and V, the k_pad validity bytes (offsets past them load zeros).
     u32x4 krs = rsrc_of(static_cast<const _Float16*>(p.k) + (size_t)kvh * p.k_pad * kLD, p.k_pad * 2 * kLD);
@@ -250,22 +230,50 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int d4 = 0; d4 < 4; ++d4)
         vbase[d4] = (8 * g + gj) * (2 * kLD) + 32 * lv_unit(2 * d4 + gg, gj) + 8 * gy;
 
-    // The tile sequence, leaving out cube tiles whose 32 keys are all invalid (the padding halves of partly filled
-    // cubes: one scalar load of their validity bytes) and, causal, tiles past the workgroup's last row. r: the raw
-    // index of the next candidate.
+    // The tile sequence: the cube tiles of the list that hold a valid key (not the padding halves of partly
+    // filled cubes) and, causal, start at or before the workgroup's last row, then the dense tiles. The cube tiles
+    // are found once, before the loop: thread i takes candidate i of each 128 (list entry i / 2, half i % 2), reads
+    // its 32 validity bytes, and the kept ones are packed in order into lst (ballot, then each lane's rank). The
+    // loop then reads one LDS word a tile instead of two dependent scalar loads a candidate.
     const uint32_t wg_last = qt * 64 + 63;
-    auto next_tile = [&](uint32_t& r, uint32_t& j0, uint32_t& hi) __attribute__((always_inline)) {
-        while (r < nt) {
-            const bool is_cube = r < 2 * ns;
-            tile_of(r, j0, hi);
-            ++r;
-            if (CAUSAL && j0 > wg_last)
-                continue;
-            if (is_cube && bytes32_zero(p.valid + j0))
-                continue;
-            return true;
+    uint32_t ncl = 0;
+    for (uint32_t r0 = 0; r0 < 2 * ns; r0 += 128) {
+        const uint32_t r = r0 + tid;
+        bool keep = false;
+        uint32_t j0 = 0;
+        if (r < 2 * ns) {
+            j0 = (uint32_t)my_sel[r >> 1] * 64 + kLKeys * (r & 1);
+            const u32x4 a = *reinterpret_cast<const u32x4*>(p.valid + j0);
+            const u32x4 b = *reinterpret_cast<const u32x4*>(p.valid + j0 + 16);
+            keep = ((a[0] | a[1]) | (a[2] | a[3]) | (b[0] | b[1]) | (b[2] | b[3])) != 0 && (!CAUSAL || j0 <= wg_last);
         }
-        return false;
+        const uint64_t bal = __ballot(keep);
+        if (lane == 0)
+            lcnt[w] = (uint32_t)__builtin_popcountll(bal);
+        __syncthreads();
+        const uint32_t base = ncl + (w == 1 ? lcnt[0] : 0u);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (keep)
+            lst[base + rank] = j0;
+        ncl += lcnt[0] + lcnt[1];
+        __syncthreads();  // lcnt is rewritten by the next round; lst is complete after the last
+    }
+    ncl = __builtin_amdgcn_readfirstlane(ncl);
+    const uint32_t ntl = ncl + nd;
+    auto next_tile = [&](uint32_t& r, uint32_t& j0, uint32_t& hi) __attribute__((always_inline)) {
+        if (r >= ntl)
+            return false;
+        if (r < ncl) {
+            j0 = __builtin_amdgcn_readfirstlane(lst[r]);
+            hi = (j0 | 63u) + 1;  // the cube's end
+        } else {
+            j0 = dlo + kLKeys * (r - ncl);
+            hi = dhi;
+            if (CAUSAL && j0 > wg_last)  // the dense tiles ascend: none after this one either
+                return false;
+        }
+        ++r;
+        return true;
     };
 
     // S^T of the tile whose K image is in buffer buf: register r holds key j0 + 16 (r / 8) + 8 g + r % 8.
@@ -421,7 +429,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 bool sparse_lists_fits(const mako_sparse_args* a, mako_dtype in, const void* valid)
 {
     return in == MAKO_F16 && a->kv_heads && a->heads % a->kv_heads == 0 && a->sel_heads == a->heads &&
-           a->dense0 % 32 == 0 && a->k_pad % 32 == 0 && (reinterpret_cast<uintptr_t>(valid) & 15u) == 0 &&
+           a->max_sel <= kLMaxSel && a->dense0 % 32 == 0 && a->k_pad % 32 == 0 &&
+           (reinterpret_cast<uintptr_t>(valid) & 15u) == 0 &&
            (uint64_t)a->q_pad * 256 < (1ull << 31) && (uint64_t)a->k_pad * 256 < (1ull << 32) &&
            (uint64_t)a->heads * ((a->n_q + 63) / 64) < (1ull << 31);
 }
