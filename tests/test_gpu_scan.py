@@ -80,6 +80,23 @@ def test_kda_scan(T, H, ld, snap):
         assert_close(sn, want_sn, "snapshot")
 
 
+def test_strong_decays_and_growth():
+    """Batches whose decays leave the kernel's rescaling range run unscaled: a channel decaying by -4 a token for a
+    whole batch (-64 over it), single tokens at -50, a channel growing by +3 a token (+48), and weak batches between
+    (rescaled); the last batch partial."""
+    rng = np.random.default_rng(77)
+    T, H = 91, 2
+    q, k, v, g, beta, state = inputs(rng, T, H, scale_state=0.3)
+    g[16:32, 5] = -4.0                   # batch 1: a channel at -64 over the batch
+    g[40, D + 7] = -50.0                 # batch 2: one token, one channel
+    g[70, :D] = -50.0                    # batch 4: one token, every channel of head 0
+    g[48:64, D + 9] = 3.0                # batch 3: growth, +48 over the batch
+    o, st, _ = run(q, k, v, g, beta, state, T=T, H=H)
+    want_o, want_st, _ = O.kda_scan(q, k, v, g, beta, state.astype(np.float64), tokens=T, heads=H)
+    assert_close(o[:T], want_o, "o")
+    assert_close(st, want_st, "state")
+
+
 def test_no_tokens_leaves_the_state():
     rng = np.random.default_rng(3)
     q, k, v, g, beta, state = inputs(rng, 1, 2, scale_state=1.0)
