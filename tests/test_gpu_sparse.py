@@ -274,18 +274,19 @@ def test_shared_lists_grouped(heads, kv, causal, dt):
         G.assert_lse_close(lse[:, rows], want_l[:, rows], "lse")
 
 
-@pytest.mark.parametrize("heads,kv,causal,dt,cubes,dense,cut", [
-    (8, 8, 0, O.F16, 7, 70, 0),     # MHA, heads a multiple of 8 (items dealt by XCD), dense rows past a 32 boundary
-    (16, 4, 1, O.F16, 6, 45, 13),   # GQA with a list per query head, causal, rows past n_q
-    (3, 3, 0, O.F16, 5, 0, 0),      # no dense rows, heads not a multiple of 8
-    (2, 1, 0, O.BF16, 4, 33, 0),    # bf16: the per-head route of the compiled kernel
+@pytest.mark.parametrize("heads,kv,causal,dt,cubes,dense,cut,topk", [
+    (8, 8, 0, O.F16, 7, 70, 0, 4),     # MHA, heads a multiple of 8 (items dealt by XCD), dense rows past a 32 boundary
+    (16, 4, 1, O.F16, 6, 45, 13, 4),   # GQA with a list per query head, causal, rows past n_q
+    (3, 3, 0, O.F16, 5, 0, 0, 4),      # no dense rows, heads not a multiple of 8
+    (2, 1, 0, O.BF16, 4, 33, 0, 4),    # bf16: the per-head route of the compiled kernel
+    (1, 1, 0, O.F16, 72, 40, 0, 70),   # lists of up to 70 entries: more than 128 candidate tiles for one workgroup
+    (2, 2, 1, O.F16, 7, 20, 0, 260),   # lists longer than the f16 route packs (max_sel 260): the compiled kernel
 ])
-def test_per_head_lists(heads, kv, causal, dt, cubes, dense, cut):
+def test_per_head_lists(heads, kv, causal, dt, cubes, dense, cut, topk):
     """A list per query head (sel_heads == heads, as cube_select writes them and MiniMax-H3 calls it): random lists
     of random lengths (some empty), cubes with invalid rows and one with none past its first half, dense rows, query
     tiles past the cubes (every key), rows past n_q, and a map that permutes and drops rows, against the oracle in
     f32 and the input type out."""
-    topk = 4
     cnt = np.full(cubes, 64, np.uint32)
     cnt[1], cnt[-1] = 37, 20  # the last cube's second 32-key tile has no valid key
     n = cubes * 64 + dense
