@@ -334,6 +334,26 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (tb)
         dma_k(jb, 1);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // A wave none of whose 32 rows has an output (the padding rows of a partly filled cube: in H3's layout the
+    // second wave of every cube of the last, one-frame cube layer) computes nothing: it stages its share of each
+    // tile and keeps the barriers of the other wave's loop, then leaves.
+    if (__ballot(live && row < p.n_q && p.map[row] >= 0) == 0) {
+        uint32_t bl = 0;
+        for (bool have_l = ta; have_l;) {
+            uint32_t jc = 0, hc = 0;
+            const bool tc = tb && next_tile(r, jc, hc);
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+            if (tc)
+                dma_k(jc, bl);
+            if (tb)
+                dma_v(jb, bl ^ 1);
+            have_l = tb;
+            tb = tc;
+            jb = jc;
+            bl ^= 1;
+        }
+        return;
+    }
     f32x16 s_cur = k_scores(0);
     mask_scores(s_cur, tile_mask(ja, ha, 0), ja);
     uint32_t b = 0;
