@@ -256,6 +256,12 @@ def staging():
     return dma_issue()
 
 
+def iteration_last_staging():
+    """A wave's last iteration stages its share of tile j + 3 as the others do: the workgroup's longer waves (rows up
+    to three tiles later) read it after barrier j + 1."""
+    return staging()
+
+
 def barrier():
     """The wave's staging of the tile before the last is in LDS and its LDS reads are done (the buffer it read last
     is written after the barrier); then the barrier."""
@@ -824,7 +830,7 @@ def body_rest(e, in_dtype, out_dtype):
         K(j + 2) for the next iteration's phase QK."""
         cur, nxt = par, 1 - par
         tag = f"{variant}{par}"
-        # the staging of tile j + 3: DMA loads spread between phase QK's MFMAs (register staging: in the list)
+        # the staging of tile j + 3: DMA loads spread between phase QK's MFMAs
         dma = dma_groups() if variant != "last" else None
         valu = []
         if variant != "first":
@@ -834,7 +840,10 @@ def body_rest(e, in_dtype, out_dtype):
             n_v = phase(e, "K", k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu, pre=0 if variant == "first" else N_K_AHEAD,
                         nxt=("V", v_reads()), dma=dma)
         else:
-            for op in valu:
+            # the wave's last tile, but the workgroup's other waves may still read tile j + 3 (a wave of 64 rows
+            # sees up to three tiles fewer than the workgroup's last): its share is staged here as in any iteration,
+            # so the barriers' waits keep their meaning (barrier j + 1 waits for it)
+            for op in valu + iteration_last_staging():
                 e(op)
         if variant != "first":
             e(f"v_cmp_nle_f32 {SCMP[0]}, {TMP[0]}, {S256}")

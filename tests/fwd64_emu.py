@@ -155,8 +155,15 @@ class Emu:
         self.prog, self.labels = prog, labels
         self.g = gmem
         self.lds = np.zeros(lds_bytes, np.uint8)
+        self.pend = np.zeros(lds_bytes, np.int32)  # LDS DMA loads in flight over each byte (issued, not landed)
+        self.early = 0   # LDS reads that sampled bytes a DMA load in flight had not yet written
         self.count = 0
         self.conflicts = {}  # instruction text -> worst multiplicity seen
+
+    def check_landed(self, addr, size):
+        idx = np.clip(np.asarray(addr, np.int64)[:, None] + np.arange(size), 0, len(self.lds) - 1)
+        if self.pend[idx].any():
+            self.early += 1
 
     # operand read: returns a (64,) uint32 array (per lane) for scalar-or-vector 32-bit operands
     def rd(self, w, x):
@@ -438,6 +445,7 @@ class Emu:
                 dst[i + q] = 0xFFFFFFFF
 
             def land(dst=dst, i=i, addr=addr):
+                self.check_landed(addr, 16)
                 for q in range(4):
                     dst[i + q] = np.array([self.lds[x + 4 * q: x + 4 * q + 4].view(np.uint32)[0]
                                            if 0 <= x + 4 * q + 4 <= len(self.lds) else 0 for x in addr], np.uint32)
@@ -453,6 +461,7 @@ class Emu:
                 dst[i + q] = 0xFFFFFFFF
 
             def land(dst=dst, i=i, addr=addr):
+                self.check_landed(addr, 8)
                 chunks = np.zeros((64, 4), np.uint32)
                 for l in range(64):
                     x = int(addr[l])
@@ -493,10 +502,12 @@ class Emu:
                     data[l] = self.g.b[base + off[l]: base + off[l] + 16]
             assert 0 <= dst0 and dst0 + 1024 <= len(self.lds), f'LDS DMA to {dst0} out of range'
             self.lds[dst0:dst0 + 1024] = 0xFF
+            self.pend[dst0:dst0 + 1024] += 1
             flat = data.reshape(-1).copy()
 
             def land(d0=dst0, flat=flat):
                 self.lds[d0:d0 + 1024] = flat
+                self.pend[d0:d0 + 1024] -= 1
             w.vmq.append(land)
         elif mn in ('buffer_load_dwordx4', 'buffer_load_dword'):
             kind, i, n, _ = parse_reg(A[0])

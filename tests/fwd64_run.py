@@ -100,6 +100,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
     vbase = lbase + G.NBUF * K_TILE
     t0 = time.time()
     n_instr = 0
+    early = 0
     worst = {}
     for wid in range(n_hg * n_qblk):
         if n_hg % 8 == 0:
@@ -177,6 +178,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
             waves.append(W)
         emu.run_wg(waves)
         n_instr += emu.count
+        early += emu.early
         for k_, v_ in emu.conflicts.items():
             worst[k_] = max(worst.get(k_, 1), v_)
     if verbose:
@@ -196,6 +198,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
     if verbose:
         print(f'h{heads} kv{kv} q{S_q} k{S_k} p{q_pos0} b{block}: out bad {bad.sum()} / {bad.size} (max err {np.nanmax(err):.3g}), '
           f'lse bad {lbad.sum()} (max {np.nanmax(np.where(np.isfinite(want_l), lerr, 0)):.3g})')
-    return dict(out_bad=int(bad.sum()), lse_bad=int(lbad.sum()), lds_worst=worst, max_err=float(np.nanmax(err)))
+    return dict(out_bad=int(bad.sum()), lse_bad=int(lbad.sum()), lds_worst=worst, max_err=float(np.nanmax(err)),
+                early_reads=early)
 
 

@@ -114,6 +114,7 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
     vbase = lbase + G.NBUF * G.K_TILE
     t0 = time.time()
     n_instr = 0
+    early = 0
     big = 0x7FFFFFFF
     for qt in range(n_qt):
         for hg in range(n_hg):
@@ -179,6 +180,7 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
                 waves.append(W)
             emu.run_wg(waves)
             n_instr += emu.count
+            early += emu.early
     if verbose:
         print(f'emulated {n_instr} wave-instructions in {time.time() - t0:.1f} s')
     if so == 4:
@@ -205,4 +207,4 @@ def run(heads, kv, sel, nsel, valid, map_, *, n_q, q_pad, n_k, k_pad, n_cubes, m
         print(f'sparse h{heads} kv{kv} q{n_q} k{n_k} causal{causal}: out bad {int(bad.sum())} / {bad.size} '
               f'(max err {np.nanmax(np.where(written[:, None], err, 0)):.3g}), lse bad {int(lbad.sum())}, '
               f'unmapped rows written {untouched}')
-    return dict(out_bad=int(bad.sum()), lse_bad=int(lbad.sum()), untouched=untouched)
+    return dict(out_bad=int(bad.sum()), lse_bad=int(lbad.sum()), untouched=untouched, early_reads=early)

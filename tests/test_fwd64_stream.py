@@ -6,8 +6,11 @@ with conflict-free LDS access: causal GQA with a query offset and ragged sizes, 
 prefix-causal, f16 in and out, and inputs whose growing scores send most tiles down the exact path. Two planted
 mistakes show the checks have teeth: a dropped wait state after an M0 write, and barriers that let V tiles be read
 before their loads land. The V^T operands come from V's rows in LDS by transpose reads (ds_read_b64_tr_b16), whose
-lane layout the emulator restates as measured on the GPU. (Barriers that let only K tiles be read early are healed by the design: the garbage
-scores fail the row-sum check, and the exact path recomputes the tile after the next barrier, when it has landed.)
+lane layout the emulator restates as measured on the GPU. The emulator also counts LDS reads that sample bytes an LDS
+DMA load in flight has not yet written, and every case requires none: a K tile read early is otherwise healed in the
+emulator (its garbage scores fail the row-sum check and the exact path recomputes the tile once it has landed), while
+on the GPU it would read the buffer's previous tile. The MHA causal case has waves three tiles apart in a workgroup,
+where a wave's last iteration must still stage its share of tile j + 3 for the others.
 The block-sparse stream (flash_sparse_r64) gets the same register and hazard checks, and emulated shared-list cases
 (invalid keys, dense rows, rows past n_q, a map that drops rows; causal and not) against the oracle through the pass
 table restated in tests/sparse64_run.py, with a planted mistake in its validity masks."""
@@ -45,6 +48,8 @@ CASES = [
     # and above (tests/test_gpu_fwd.py checks bf16 P against its rounding bound there); f16 P at the full growth
     dict(heads=4, kv=1, S_q=64, S_k=448, q_pos0=0, block=0, seed=7, kgrow=1.5, ind="f16"),
     dict(heads=4, kv=1, S_q=64, S_k=448, q_pos0=0, block=0, seed=7, kgrow=0.5),
+    # one query head a kv head: a workgroup's four waves hold rows 64 apart, so their last tiles differ by up to three
+    dict(heads=1, kv=1, S_q=512, S_k=512, q_pos0=0, block=U32, seed=3),
 ]
 
 
@@ -52,7 +57,7 @@ CASES = [
 def test_stream_matches_oracle(case):
     taken = E.EXACT_COUNT[0]
     r = R.run(**case, verbose=False)
-    assert r["out_bad"] == 0 and r["lse_bad"] == 0, r
+    assert r["out_bad"] == 0 and r["lse_bad"] == 0 and r["early_reads"] == 0, r
     # the epilogue's 8-byte writes (2-byte outputs) meet 2-way: sixteen lanes of one write cover rows with eight
     # distinct chunk slots; every other LDS access is conflict-free
     assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
@@ -84,7 +89,7 @@ CASES_D64 = [
 def test_d64_stream_matches_oracle(case):
     taken = E.EXACT_COUNT[0]
     r = R.run(**case, d=64, verbose=False)
-    assert r["out_bad"] == 0 and r["lse_bad"] == 0, r
+    assert r["out_bad"] == 0 and r["lse_bad"] == 0 and r["early_reads"] == 0, r
     assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
     if case.get("kgrow"):
         assert E.EXACT_COUNT[0] > taken  # the exact path ran
@@ -108,7 +113,15 @@ def test_planted_barrier_without_lds_wait_is_found(monkeypatch):
 def test_planted_short_barrier_wait_is_found(monkeypatch):
     monkeypatch.setattr(G, "barrier", lambda: [f"s_waitcnt vmcnt({3 * G.DMA_PER_TILE}) lgkmcnt(0)", "s_barrier"])
     r = R.run(4, 1, 64, 448, 0, 0, seed=9, verbose=False)
-    assert r["out_bad"] > 0
+    assert r["out_bad"] > 0 and r["early_reads"] > 0
+
+
+def test_planted_last_iteration_without_staging_is_found(monkeypatch):
+    """A wave whose last iteration leaves out its share of tile j + 3 (staging then falls a barrier behind) lets the
+    longer waves of an MHA workgroup read K tiles before they land: counted as early reads."""
+    monkeypatch.setattr(G, "iteration_last_staging", lambda: [])
+    r = R.run(heads=1, kv=1, S_q=512, S_k=512, q_pos0=0, block=U32, seed=3, verbose=False)
+    assert r["early_reads"] > 0
 
 
 # ---- the block-sparse stream (flash_sparse_r64: tiles, masks and output rows from the pass table and the row map) ----
@@ -156,7 +169,7 @@ def test_sparse_stream_matches_oracle(causal, ind, outd):
 
     args, kw = shared_lists_case(causal, 41 + causal)
     r = SR.run(*args, **kw, ind=ind, outd=outd, verbose=False)
-    assert r == dict(out_bad=0, lse_bad=0, untouched=0), r
+    assert r == dict(out_bad=0, lse_bad=0, untouched=0, early_reads=0), r
 
 
 def test_sparse_planted_mask_shift_is_found(monkeypatch):
