@@ -183,15 +183,11 @@ void Runtime::finish(Encoder* enc)
         stats_.encode_ms += std::chrono::duration<double, std::milli>(t0 - step_start_).count();
         encoding_ = false;
     }
-    if (!marks_.empty()) {  // the last section or part ends here
-        Mark end;
-        end.ev = event();
-        end.section = -1;
-        hip_check(hipEventRecord(end.ev, enc->stream), "hipEventRecord");
-        marks_.push_back(std::move(end));
-    }
+    end_marks(enc);
+    on_committed(enc);
     const hipError_t e = hipStreamSynchronize(enc->stream);
     stats_.gpu_wait_ms += std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+    on_completed();
     if (e != hipSuccess)
         throw std::runtime_error(std::string("launch queue failed: ") + hipGetErrorString(e));
     const hipError_t last = hipGetLastError();
@@ -200,6 +196,36 @@ void Runtime::finish(Encoder* enc)
     resolve_times();
     resolve_sections();
     deliver_probes();
+}
+
+void Runtime::end_marks(Encoder* enc)
+{
+    if (marks_.empty() || marks_.back().section < 0)  // no open section or part
+        return;
+    Mark end;
+    end.ev = event();
+    end.section = -1;
+    hip_check(hipEventRecord(end.ev, enc->stream), "hipEventRecord");
+    marks_.push_back(std::move(end));
+}
+
+void Runtime::submit(Encoder*& enc)
+{
+    finish(enc);
+    enc = encoder();
+}
+
+void Runtime::commit_ahead(Encoder*& enc)
+{
+    if (!commit_ahead_ok())
+        return;
+    const auto now = Clock::now();
+    if (encoding_)
+        stats_.encode_ms += std::chrono::duration<double, std::milli>(now - step_start_).count();
+    step_start_ = now;  // the next stretch's encode time starts here
+    encoding_ = true;
+    end_marks(enc);
+    ++stats_.commits_ahead;
 }
 
 void Runtime::section(Encoder*& enc, uint32_t layer, int section)
@@ -232,10 +258,10 @@ void Runtime::part(Encoder*& enc, std::string_view name)
 void Runtime::resolve_sections()
 {
     for (size_t i = 0; i + 1 < marks_.size(); ++i) {
-        float ms = 0.0f;
-        if (hipEventElapsedTime(&ms, marks_[i].ev, marks_[i + 1].ev) != hipSuccess)
-            continue;
         const Mark& m = marks_[i];
+        float ms = 0.0f;
+        if (m.section < 0 || hipEventElapsedTime(&ms, m.ev, marks_[i + 1].ev) != hipSuccess)
+            continue;  // an end mark opens no interval
         auto sec = std::find_if(sections_.begin(), sections_.end(), [&](const SectionTime& t) {
             return t.layer == m.layer && t.section == m.section;
         });

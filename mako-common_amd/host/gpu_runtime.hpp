@@ -60,7 +60,8 @@ public:
 
     struct Stats {
         double gpu_wait_ms = 0, gpu_exec_ms = 0;  // wait: finish() blocked; exec: timed launches, summed
-        double encode_ms = 0, step_ms = 0;        // encode: step start to finish()
+        double encode_ms = 0, step_ms = 0;        // encode: step start to finish(), less the commit_ahead() gaps
+        uint32_t commits_ahead = 0;               // commit_ahead() calls that ended a stretch
     };
     const Stats& stats() const { return stats_; }
     // Bytes of all scratch buffers allocated so far.
@@ -100,6 +101,19 @@ protected:
     // Waits for every launch of the queue and raises std::runtime_error if one failed (src/gpu/runtime.cpp:453-475);
     // then resolves the step's times and delivers its probes.
     void finish(Encoder* enc);
+    // finish(), then the next launches start a new step on the same queue (src/gpu/runtime.cpp:493-500).
+    void submit(Encoder*& enc);
+    // Ends the step's current stretch without waiting (src/gpu/runtime.cpp:477-491; src/gpu/runtime.hpp:121-123):
+    // the launches made so far are already on the in-order queue and running, so what remains of the reference's
+    // commit is its bookkeeping. The stretch's encode time is added to the stats, a timed section or part ends here
+    // (the launches up to the next section() are untimed, as the reference's encoder of section -1 was), and
+    // finish() waits for and accounts every stretch. Does nothing while commit_ahead_ok() says no.
+    void commit_ahead(Encoder*& enc);
+    // finish()'s hooks (src/gpu/runtime.hpp:124-128): on_committed after the last launch is queued and before the
+    // wait (host work the GPU may be waiting for), on_completed after the wait, before errors are raised.
+    virtual void on_committed(Encoder*) {}
+    virtual void on_completed() {}
+    virtual bool commit_ahead_ok() const { return true; }
     // With a probe set: n f32 values of buf at off bytes copied on the queue (after what was launched before) into
     // host memory, handed to the probe by finish() as (name, layer) (src/gpu/runtime.cpp:502-517).
     void probe(Encoder*& enc, const std::string& name, int layer, Buffer* buf, size_t n, uint64_t off = 0);
@@ -168,6 +182,7 @@ private:
     std::chrono::steady_clock::time_point step_start_;
     bool encoding_ = false;
     hipEvent_t event();
+    void end_marks(Encoder* enc);  // closes an open section or part with an end mark (section -1)
     void resolve_times();
     void resolve_sections();
 };

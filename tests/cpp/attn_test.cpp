@@ -57,6 +57,14 @@ public:
     using TransformerRuntime::section;
     using TransformerRuntime::part;
     using TransformerRuntime::enable_part_timing;
+    using TransformerRuntime::submit;
+    using TransformerRuntime::commit_ahead;
+
+    int committed = 0, completed = 0;
+    bool ahead_ok = true;
+    void on_committed(mako::gpu::Encoder*) override { ++committed; }
+    void on_completed() override { ++completed; }
+    bool commit_ahead_ok() const override { return ahead_ok; }
 };
 
 int failures = 0;
@@ -290,6 +298,37 @@ int main()
             check(hr.repeats("flash_fwd_128") == 3 && hr.repeats("proj BF16") == 1 && kt.size() == 1 &&
                       kt[0].count == 1 && std::memcmp(o.data(), once.data(), n * 4) == 0,
                   "MAKO_REPEAT=flash_fwd:3: attention repeated inside one timed launch, output bit-equal");
+        }
+        // commit_ahead ends a timed section without waiting; submit finishes and starts the next step.
+        {
+            Harness hs(mako::gpu::Telemetry::layers);
+            auto qb = put(hs, "q", q), kb = put(hs, "k", k), vb = put(hs, "v", v);
+            auto ob = hs.scratch("o", n * 4), ob2 = hs.scratch("o2", n * 4);
+            auto* enc = hs.encoder();
+            hs.section(enc, 1, 0);
+            hs.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX, D, opt);
+            hs.commit_ahead(enc);  // section (1, 0) ends here
+            hs.attention(enc, qb, kb, vb, ob2, S, S, S, S, heads, kv, 0, 0, D, opt);  // untimed
+            hs.ahead_ok = false;
+            hs.commit_ahead(enc);  // refused by the hook: no effect
+            hs.section(enc, 2, 0);
+            hs.attention(enc, qb, kb, vb, ob, S, S, S, S, heads, kv, 0, UINT32_MAX, D, opt);
+            const int committed_before = hs.committed;
+            hs.submit(enc);
+            const bool hooks_once = committed_before == 0 && hs.committed == 1 && hs.completed == 1;
+            const auto secs = hs.section_times();
+            const auto o = get<float>(ob, n);
+            hs.attention(enc, qb, kb, vb, ob2, S, S, S, S, heads, kv, 0, UINT32_MAX, D, opt);
+            hs.finish(enc);
+            const auto o2 = get<float>(ob2, n);
+            const bool ok = hooks_once && hs.committed == 2 && hs.completed == 2 && hs.stats().commits_ahead == 1 &&
+                            secs.size() == 2 && secs[0].layer == 1 && secs[0].section == 0 && secs[0].ms > 0 &&
+                            secs[1].layer == 2 && secs[1].section == 0 && secs[1].ms > 0 &&
+                            std::memcmp(o.data(), once.data(), n * 4) == 0 &&
+                            std::memcmp(o2.data(), once.data(), n * 4) == 0 && hs.section_times().empty();
+            check(ok, "commit_ahead ends section (1, 0) without a wait, a refused commit_ahead does nothing, submit "
+                      "finishes once (hooks " + std::to_string(hs.committed) + "/" + std::to_string(hs.completed) +
+                      ", sections " + std::to_string(secs.size()) + "), outputs bit-equal");
         }
         {
             using mako::gpu::RepeatSpec;
