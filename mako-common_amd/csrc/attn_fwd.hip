@@ -634,6 +634,12 @@ template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                  float* lse, hipStream_t s);
 size_t d256_workspace(const mako_attn_args* a);
+// flash_fwd_r32 (attn_fwd_r32.hip): heads of 256 with 32 rows a wave, staged from K and V's rows (no workspace);
+// 1 launched, 0 when a size does not fit its offsets (flash_fwd_d256 then takes the call).
+bool r32_fits(const mako_attn_args* a, uint32_t out_bytes);
+template <class T, class TO>
+int launch_fwd_r32(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+                   float* lse, hipStream_t s);
 template <class T, class TO>
 int launch_fwd_d256(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                     float* lse, hipStream_t s, const void* vt_ready, const Workspace* work);
@@ -657,8 +663,9 @@ bool launch_d(const mako_attn_args* a, uint32_t dim, const FwdParams& p, dim3 gr
     if (!force_fallback()) {
         const int r = dim == 128 ? launch_fwd64<T, TO, 128>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
                       : dim == 64 ? launch_fwd64<T, TO, 64>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
-                                  : launch_fwd_d256<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s, nullptr,
-                                                           &work);
+                      : launch_fwd_r32<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s)
+                          ? 1
+                          : launch_fwd_d256<T, TO>(a, p.scale_log2, p.q, p.k, p.v, p.o, p.lse, s, nullptr, &work);
         if (r)
             return r > 0;
     }
@@ -718,13 +725,14 @@ int attn_check(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype 
     return MAKO_OK;
 }
 
-// The workspace a dense call needs: the split-K partials (heads of 128, a few rows) or the V^T images (heads of 256);
-// the prefill kernels for heads of 64 and 128 need none.
+// The workspace a dense call needs: the split-K partials (heads of 128, a few rows) or, for heads of 256 past
+// flash_fwd_r32's offsets (sized for an f32 output, the larger), flash_fwd_d256's V^T images; the prefill kernels
+// for heads of 64 and 128, and flash_fwd_r32, need none.
 size_t attn_fwd_workspace(const mako_attn_args* a, uint32_t dim)
 {
     if (dim == 128 && splitk_takes(a, dim))
         return splitk_workspace(a);
-    return dim == 256 ? d256_workspace(a) : 0;
+    return dim == 256 && !r32_fits(a, 4) ? d256_workspace(a) : 0;
 }
 
 int attn_fwd_core(const mako_attn_args* a, uint32_t dim, mako_dtype in, mako_dtype out, const void* q, const void* k,
