@@ -392,7 +392,7 @@ def bench_other_dims(torch, M, steps, warmup, with_cpu, names=None):
     heads, 4096 tokens) on flash_fwd. bf16 in and out, LSE."""
     legs = {
         "d256_causal": dict(H=16, KV=2, D=256, S=4096, block=U32_MAX, seed=256,
-                            kernel="vt_image<bf16,256> + flash_fwd_d256<bf16,bf16> (one call, both kernels)",
+                            kernel="flash_fwd_r32<bf16,bf16> (one launch a call)",
                             workload="causal GQA, 16 query heads / 2 kv heads, D 256, S 4096, bf16 in/out, LSE "
                                      "(Qwen3.5 gated attention)"),
         "d64_bidir": dict(H=16, KV=16, D=64, S=4096, block=0, seed=64,

@@ -50,7 +50,11 @@ NKP = (K_TILE // 1024 - 1) // 4                 # K pieces a wave DMAs (w + 4 m)
 NVP = V_TILE // 4096                            # V KiB a wave DMAs (rows 16 w .. 16 w + 15)
 DMA_K = NKP + 1
 DMA_V = NVP
-BAR_AT = 26                                     # 32 fragments in phase PV; reads run AHEAD = 6 fragments ahead
+RING = 8                                        # operand ring slots (4 accumulator registers each, from a192)
+AHEAD = 6                                       # operand reads in flight ahead of their MFMAs
+BAR_AT = 32 - AHEAD                             # phase PV's fragment after which the barrier sits: every V^T read
+                                                # of the phase (fragment f's goes out after fragment f - AHEAD) is
+                                                # issued before it
 LDS_BYTES = 2 * (K_TILE + V_TILE)
 
 NEGMU, LSUM, MAXV, NINF, ZERO, TMP = G.NEGMU[0], G.LSUM[0], G.MAXV[0], G.NINF, G.ZERO, G.TMP
@@ -63,17 +67,17 @@ SKW, SKWW, SVWW = G.SKW, G.SKWW, G.SVWW
 KRS, VRS, ST, SCMP, SJ0, SM0, SMASK = G.KRS, G.VRS, G.ST, G.SCMP, G.SJ0, G.SM0, G.SMASK
 
 CLOBBER_V = 184
-CLOBBER_A = 224
+CLOBBER_A = 192 + 4 * RING
 CLOBBER_S = (60, 100)
 
 
 @contextlib.contextmanager
 def shapes():
     """r64's fragment readers, ring and register helpers at 256 head dims (they read the generator's shape globals)."""
-    names = ("D", "K_ROW", "V_ROW", "K_TILE", "V_TILE", "NKK", "NDB")
+    names = ("D", "K_ROW", "V_ROW", "K_TILE", "V_TILE", "NKK", "NDB", "RING", "AHEAD", "N_K_AHEAD")
     saved = {n: getattr(G, n) for n in names}
     for n in names:
-        setattr(G, n, globals()[n])
+        setattr(G, n, globals()[n] if n != "N_K_AHEAD" else AHEAD)
     try:
         yield
     finally:
@@ -95,6 +99,31 @@ def P(cc, i=None):
     """Probabilities in the input type, 16-key chunk cc: dword i holds keys 16 cc + 8 g + 2 i, + 1."""
     base = 128 + 4 * cc
     return f"v{base + i}" if i is not None else f"v[{base}:{base + 3}]"
+
+
+def v_unit(u, k):
+    """Where 32-byte unit u (head dims 16 u .. 16 u + 15) of V row k sits in the row's LDS image: u ^ (k % 4) ^
+    4 (u % 2), a bijection of each aligned group of 8 units (256 bytes, the 64 banks). A transpose read's 32-lane pass
+    addresses units 2 db and 2 db + 1 of four rows k % 4 = 0 .. 3 (one a 4-lane group): the XOR with k % 4 spreads the
+    rows over four units and the 4 (u % 2) term puts the odd unit's four in the other half of the 256 bytes, so the
+    pass covers the 64 banks once (r64's v_unit covers the 32 banks of one half twice: a 2-way conflict)."""
+    return u ^ (k & 3) ^ (4 * (u & 1))
+
+
+def v_reads():
+    """LDS transpose reads of V^T fragment f = (cc, db) = (f // NDB, f % NDB), the A operand of O^T += V^T P^T: lane
+    l = 32 g + 16 h + i receives head dim 32 db + 16 h + i of keys 16 cc + 8 g .. + 7, in two ds_read_b64_tr_b16 of
+    four keys ({lo}: keys + 0 .. 3, {hi}: + 4 .. 7). In a read, lane i of the group addresses key 16 cc + 8 g + 4 r +
+    i / 4, head dims 16 (2 db + h) + 4 (i % 4) .. + 3: unit v_unit(2 db + h, i / 4) of that row, whose place in the
+    row's 256-byte half depends on db % 4 and the lane, so %[vr0] .. %[vr3] hold the lane's address for db % 4 = 0 ..
+    3; db / 4 adds 256 bytes, cc and r add whole rows."""
+    out = []
+    for f in range(4 * NDB):
+        cc, db = f // NDB, f % NDB
+        base = 16 * cc * V_ROW + 256 * (db >> 2)
+        out.append([f"ds_read_b64_tr_b16 {{{half}}}, %[vr{db & 3}] offset:{base + 4 * r * V_ROW}"
+                    for r, half in ((0, "lo"), (1, "hi"))])
+    return out
 
 
 def VALS(par):
@@ -302,7 +331,7 @@ def toggle_k():
 
 
 def toggle_v():
-    return [f"v_add_u32 %[vr0], {SVRT}, %[vr0]", f"v_add_u32 %[vr1], {SVRT}, %[vr1]", f"s_sub_u32 {SVRT}, 0, {SVRT}"]
+    return [f"v_add_u32 %[vr{i}], {SVRT}, %[vr{i}]" for i in range(4)] + [f"s_sub_u32 {SVRT}, 0, {SVRT}"]
 
 
 def low_part_pass(e):
@@ -323,7 +352,7 @@ def low_part_pass(e):
             ops_c.append(f"v_cvt_pk_bf16_f32 {lr}, {lr}, {tr}")
     for op in ops_a + ops_b + ops_c:
         e(op)
-    G.interleave(e, G.v_reads(), pv_mfmas("bf16", pbase=96), [])
+    G.interleave(e, v_reads(), pv_mfmas("bf16", pbase=96), [])
     e.label("L_nolo")
 
 
@@ -480,7 +509,7 @@ def body_rest(e, in_dtype, out_dtype):
         n_v = 0
         if variant != "last":
             n_v = G.phase(e, "K", G.k_reads("%[kr]"), qk_mfmas(in_dtype, nxt), valu,
-                          pre=0 if variant == "first" else G.N_K_AHEAD, nxt=("V", G.v_reads()), dma=unit_groups())
+                          pre=0 if variant == "first" else G.N_K_AHEAD, nxt=("V", v_reads()), dma=unit_groups())
         else:
             # the wave's last tile; the workgroup's other waves still read what this iteration stages
             for op in valu + staging():
@@ -501,7 +530,7 @@ def body_rest(e, in_dtype, out_dtype):
             kind = masked_next or variant
             m = mask(nxt, SJ0) if kind == "masked" else []
             valu = ["s_nop 7", "s_nop 7"] + m + exps(nxt)
-        n_k = G.phase(e, "V", G.v_reads(), pv_mfmas(in_dtype), valu, pre=n_v,
+        n_k = G.phase(e, "V", v_reads(), pv_mfmas(in_dtype), valu, pre=n_v,
                       nxt=None if variant == "last" else ("K", G.k_reads("%[kr]")), gate_at=BAR_AT, gate=barrier())
         assert variant == "last" or n_k == G.N_K_AHEAD
         for op in toggle_v():
@@ -545,7 +574,7 @@ def body_rest(e, in_dtype, out_dtype):
     e.label("L_last_first")
     for op in staging():
         e(op)
-    G.phase(e, "V", G.v_reads(), pv_mfmas(in_dtype), [], gate_at=BAR_AT, gate=barrier())
+    G.phase(e, "V", v_reads(), pv_mfmas(in_dtype), [], gate_at=BAR_AT, gate=barrier())
     for op in toggle_v():
         e(op)
     e(f"s_add_u32 {SJ}, {SJ}, 1")

@@ -16,7 +16,7 @@ import oracle as O  # noqa: E402
 
 D = 256
 LAST = {}   # the last run's outputs and the oracle's, for a look at a failing case
-VOPS = ['kr', 'vr0', 'vr1'] + [f'kd{m}' for m in range(G.NKP + 1)] + [
+VOPS = ['kr', 'vr0', 'vr1', 'vr2', 'vr3'] + [f'kd{m}' for m in range(G.NKP + 1)] + [
     'vd', 'vdo', 'vd2', 'vdo2', 'lim0', 'qo', 'lo0', 'swp', 'ew', 'er', 'og']
 SOPS = R64.SOPS
 VREG = {n: f'v{G.CLOBBER_V + i}' for i, n in enumerate(VOPS)}
@@ -24,10 +24,11 @@ VREG = {n: f'v{G.CLOBBER_V + i}' for i, n in enumerate(VOPS)}
 
 def vd_lane(lane, r0):
     """The V byte (relative to its 1 KiB piece of two 512-byte rows) lane l's LDS slot holds, for a piece whose first
-    row is r0 mod 4: slot byte 16 l is row r, unit p, half; it holds unit v_unit(p, r0 + r) of that row."""
+    row is r0 mod 4: slot byte 16 l is row r, physical unit p, half; it holds the unit G.v_unit places at p."""
     b = 16 * lane
     r, pos = b // (2 * D), b % (2 * D)
-    u = np.array([G.G.v_unit(int(pp), int(rr) + r0) for pp, rr in zip(pos // 32, r)])
+    x = (pos // 32) ^ ((r + r0) & 3)      # the physical unit's logical unit: x ^ 4 (x % 2) (G.v_unit's inverse)
+    u = x ^ (4 * (x & 1))
     return r * 2 * D + 32 * u + 16 * ((pos // 16) & 1)
 
 
@@ -108,7 +109,9 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
                 lmin = R64.lim_of(p0, S_k, block)
                 lim0 = np.array([R64.lim_of(p0 + cc, S_k, block) for cc in c32]) - 8 * g
                 kr = lbase + c32 * G.K_ROW + 16 * g
-                vr = R64.v_read_regs(vbase, D, lane)
+                hh, ii = (lane >> 4) & 1, lane & 15
+                vr = [vbase + (8 * g + ii // 4) * 2 * D + 8 * (ii % 4) +
+                      32 * np.array([G.v_unit(2 * d + int(a), int(b) // 4) for a, b in zip(hh, ii)]) for d in range(4)]
 
                 def kd_of(i):
                     b = 1024 * i + 16 * lane
@@ -130,7 +133,7 @@ def run(heads, kv, S_q, S_k, q_pos0, block, ind='bf16', outd='f32', seed=0, verb
                 ogs = (64 // lpr) * width * so
                 lo0 = np.where(q0 + c32 < S_q, (h * S_q + q0 + c32) * 4, 0xffffffff)
                 swp = (lane ^ 32) * 4
-                vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], vd=vd, vdo=vdo, vd2=vd + 4096, vdo2=vdo + 4096, lim0=lim0, qo=qo, lo0=lo0, swp=swp,
+                vals = dict(kr=kr, vr0=vr[0], vr1=vr[1], vr2=vr[2], vr3=vr[3], vd=vd, vdo=vdo, vd2=vd + 4096, vdo2=vdo + 4096, lim0=lim0, qo=qo, lo0=lo0, swp=swp,
                             ew=ew, er=er, og=og)
                 vals.update({f'kd{m}': kds[m] for m in range(G.NKP + 1)})
                 for n, arr in vals.items():

@@ -2,7 +2,7 @@
 128 and of 64: every register it names is one its clobber list reserves; no gfx950 software hazard in any of its
 type variants; and,
 on an instruction-level emulator (tests/fwd64_emu.py), outputs and LSE within the attention tolerance of the oracle
-with conflict-free LDS access: causal GQA with a query offset and ragged sizes, bidirectional over eleven tiles,
+with the LDS bank conflicts it allows (LDS_WORST): causal GQA with a query offset and ragged sizes, bidirectional over eleven tiles,
 prefix-causal, f16 in and out, and inputs whose growing scores send most tiles down the exact path. Two planted
 mistakes show the checks have teeth: a dropped wait state after an M0 write, and barriers that let V tiles be read
 before their loads land. The V^T operands come from V's rows in LDS by transpose reads (ds_read_b64_tr_b16), whose
@@ -37,6 +37,14 @@ def test_registers_and_hazards(ind, outd):
     assert Hz.check(lines, f"{ind}->{outd}") == 0
 
 
+# LDS bank-conflict multiplicities allowed (the emulator's model, which SQ_LDS_BANK_CONFLICT bears out): the
+# epilogue's 8-byte writes (2-byte outputs) meet 2-way, sixteen lanes of one write covering rows with eight distinct
+# chunk slots; the V^T transpose reads at 128 head dims 2-way, a 32-lane pass covering the 32 banks of half a row
+# twice (v_unit; at 64 head dims two rows share the 64 banks and the pass covers them once). A layout without the
+# conflict needs four read-address registers instead of two; on the heads-of-256 stream it measured under 1 %.
+# Every other LDS access is conflict-free.
+LDS_WORST = {"ds_write_b64": 2, "ds_read_b64_tr_b16": 2}
+
 CASES = [
     dict(heads=8, kv=2, S_q=100, S_k=330, q_pos0=230, block=U32, seed=1),
     dict(heads=4, kv=1, S_q=64, S_k=700, q_pos0=0, block=0, seed=2),
@@ -58,9 +66,7 @@ def test_stream_matches_oracle(case):
     taken = E.EXACT_COUNT[0]
     r = R.run(**case, verbose=False)
     assert r["out_bad"] == 0 and r["lse_bad"] == 0 and r["early_reads"] == 0, r
-    # the epilogue's 8-byte writes (2-byte outputs) meet 2-way: sixteen lanes of one write cover rows with eight
-    # distinct chunk slots; every other LDS access is conflict-free
-    assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
+    assert all(m <= LDS_WORST.get(op, 1) for op, m in r["lds_worst"].items()), r["lds_worst"]
     if case.get("kgrow"):
         assert E.EXACT_COUNT[0] > taken  # the exact path ran
 
@@ -90,7 +96,8 @@ def test_d64_stream_matches_oracle(case):
     taken = E.EXACT_COUNT[0]
     r = R.run(**case, d=64, verbose=False)
     assert r["out_bad"] == 0 and r["lse_bad"] == 0 and r["early_reads"] == 0, r
-    assert all(m == (2 if op == "ds_write_b64" else 1) or m == 1 for op, m in r["lds_worst"].items()), r["lds_worst"]
+    assert all(m <= (1 if op == "ds_read_b64_tr_b16" else LDS_WORST.get(op, 1)) for op, m in r["lds_worst"].items()), \
+        r["lds_worst"]
     if case.get("kgrow"):
         assert E.EXACT_COUNT[0] > taken  # the exact path ran
 
