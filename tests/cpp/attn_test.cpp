@@ -582,7 +582,7 @@ int main()
         for (int round = 0; round < 3; ++round) {
             auto* enc = h.encoder();
             h.attention(enc, qb, kb, vb, ob, 2, 64, S, S, H, KV, S - 2, UINT32_MAX, D, opt);   // split-K partials
-            h.attention(enc, q2b, k2b, k2b, ob, S2, 256, S2, 256, H2, KV2, 0, UINT32_MAX, D2, opt);  // V^T images
+            h.attention(enc, q2b, k2b, k2b, ob, S2, 256, S2, 256, H2, KV2, 0, UINT32_MAX, D2, opt);  // none (r32)
             h.attention_sparse(enc, qb, kb, vb, ob, S, S, S, S, H, KV, H * D, cubes, 1, S, S, selb, nselb, validb,
                                mapb, sopt);                                                       // pass table
             h.finish(enc);
