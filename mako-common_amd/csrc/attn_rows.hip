@@ -3,13 +3,14 @@
 // :414-418, src/models/h3_vae.cpp:219) as two launches instead of four.
 //
 // qkv_prep, one launch, three kinds of workgroup:
-//   * the value tiles as mako_heads writes them (heads_vec_item; flash_fwd_r64 stages V from its rows), or, for heads
-//     of 256, the V^T tile images flash_fwd_d256 stages from, written straight from the value rows (vt_rows_tiles):
-//     the value tiles are then never written, nor read back by vt_image;
+//   * the value tiles as mako_heads writes them (heads_vec_item; flash_fwd_r64 and flash_fwd_r32 stage V from its
+//     rows), or, for heads of 256 past flash_fwd_r32's offsets, the V^T tile images flash_fwd_d256 stages from,
+//     written straight from the value rows (vt_rows_tiles): the value tiles are then never written, nor read back by
+//     vt_image;
 //   * the key tiles, normed and rotated as mako_heads writes them (heads_vec_item);
 //   * the query tiles, the same.
-// Then the attention kernel over those tiles (launch_fwd64; launch_fwd_d256 with the images ready). Every value is
-// rounded as the separate launches round it, so both give the same bits.
+// Then the attention kernel over those tiles (launch_fwd64, launch_fwd_r32; launch_fwd_d256 with the images ready),
+// the one mako_attn_fwd takes. Every value is rounded as the separate launches round it, so both give the same bits.
 //
 // Bound: HBM for qkv_prep (4 bytes read a value, 2 written), then the attention kernel's MFMA bound.
 #include "fwd64_common.hpp"
@@ -23,6 +24,10 @@ bool splitk_takes(const mako_attn_args* a, uint32_t dim);
 template <int D>
 bool fwd64_fits(const mako_attn_args* a, uint32_t out_bytes);
 bool d256_fits(const mako_attn_args* a);
+bool r32_fits(const mako_attn_args* a, uint32_t out_bytes);
+template <class T, class TO>
+int launch_fwd_r32(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
+                   float* lse, hipStream_t s);
 template <class T, class TO, int D>
 int launch_fwd64(const mako_attn_args* a, float scale_log2, const void* q, const void* k, const void* v, void* o,
                  float* lse, hipStream_t s);
@@ -43,8 +48,8 @@ struct VtRowsParams {
     uint32_t nbx;  // workgroups a kv head (256 / D tiles each)
 };
 
-// Workgroups [0, nbv): value tiles (value items; heads of 256: V^T images of kv head b / nbx); then nbk of key
-// items; then the query items.
+// Workgroups [0, nbv): value tiles (value items; heads of 256 for flash_fwd_d256: V^T images of kv head b / nbx);
+// then nbk of key items; then the query items.
 template <class T, int D>
 __global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const HeadsParams pk, const HeadsParams pvt,
                                                 const VtRowsParams pv, uint32_t nbv, uint32_t nbk)
@@ -52,7 +57,7 @@ __global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const Head
     uint32_t b = blockIdx.x;
     const uint32_t w = threadIdx.x >> 6;
     if (b < nbv) {
-        if constexpr (D == 256)
+        if (D == 256 && pv.img)
             vt_rows_tiles<T, D>(pv.x, pv.ld, pv.col0, pv.stride, pv.img, pv.n_k, pv.n_vt, b % pv.nbx, b / pv.nbx);
         else
             heads_vec_item<T, D / 4>(pvt, (uint64_t)b * kItems + w);
@@ -70,7 +75,9 @@ __global__ __launch_bounds__(256) void qkv_prep(const HeadsParams pq, const Head
 size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // The fused route for heads of D: qkv_prep, then the attention kernel. pvt: the value producer (its tiles at pvt.y,
-// the V the attention kernel reads); heads of 256 write V^T images instead, into images (d256_workspace bytes).
+// the V the attention kernel reads); heads of 256 past flash_fwd_r32's offsets write flash_fwd_d256's V^T images
+// instead, into images (d256_workspace bytes). The kernel is the one mako_attn_fwd takes for the same call, so the
+// fused route gives the separate launches' bits.
 template <class T, class TO, int D>
 int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParams& pk, const HeadsParams& pvt,
                 const mako_heads_args* hv, const float* xv, void* o, float* lse, hipStream_t s,
@@ -78,14 +85,15 @@ int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParam
 {
     using L = R64<D>;
     const uint32_t n_vt = (t->n_k + 63) / 64, nbx = (n_vt + 256 / D - 1) / (256 / D);
+    const bool images_route = D == 256 && !r32_fits(t, sizeof(TO));
     void* vt = nullptr;
-    if constexpr (D == 256) {
+    if (images_route) {
         const size_t vt_bytes = (size_t)t->kv_heads * n_vt * L::kVTile;
         if (vt_bytes && !(vt = images.get(vt_bytes, s)))
             return last_code();
     }
     const VtRowsParams pv{xv, static_cast<uint32_t*>(vt), hv->ld, hv->col0, hv->stride, t->n_k, n_vt, nbx};
-    const uint64_t nbv = D == 256 ? (uint64_t)nbx * t->kv_heads : (pvt.n_items + kItems - 1) / kItems,
+    const uint64_t nbv = images_route ? (uint64_t)nbx * t->kv_heads : (pvt.n_items + kItems - 1) / kItems,
                    nbk = (pk.n_items + kItems - 1) / kItems, nbq = (pq.n_items + kItems - 1) / kItems;
     if (nbv + nbk + nbq > 0x7fffffffu)
         return fail(MAKO_EINVAL, "attention from rows: %llu workgroups exceed the grid",
@@ -95,8 +103,10 @@ int launch_rows(const mako_attn_args* t, const HeadsParams& pq, const HeadsParam
                            (uint32_t)nbv, (uint32_t)nbk);
     const float sl2 = t->scale * 1.4426950408889634f;
     int r;
-    if constexpr (D == 256)
+    if (images_route)
         r = launch_fwd_d256<T, TO>(t, sl2, pq.y, pk.y, pk.y, o, lse, s, vt, &images);
+    else if constexpr (D == 256)
+        r = launch_fwd_r32<T, TO>(t, sl2, pq.y, pk.y, pvt.y, o, lse, s);
     else
         r = launch_fwd64<T, TO, D>(t, sl2, pq.y, pk.y, pvt.y, o, lse, s);
     if (r <= 0)  // (the route was chosen where the kernel fits and its images are given)
@@ -188,7 +198,9 @@ int rows_core(const mako_attn_args* a, const mako_heads_args* hq, const mako_hea
     const size_t q_bytes = round256((size_t)a->heads * a->n_q * dim * 2),
                  k_bytes = round256((size_t)a->kv_heads * a->n_k * dim * 2);
     const uint32_t osz = out == MAKO_F32 ? 4u : 2u;
-    const bool fits = dim == 256 ? d256_fits(&t) : dim == 128 ? fwd64_fits<128>(&t, osz) : fwd64_fits<64>(&t, osz);
+    const bool fits = dim == 256   ? r32_fits(&t, osz) || d256_fits(&t)
+                      : dim == 128 ? fwd64_fits<128>(&t, osz)
+                                   : fwd64_fits<64>(&t, osz);
     const bool fused = fits && !splitk_takes(&t, dim) && heads_vec_takes(&tq, xq, csq, wq, o) &&
                        heads_vec_takes(&tk, xk, cs, wk, o) && tv.rope == 0 && tv.eps == 0.0f &&
                        heads_vec_takes(&tv, xv, nullptr, nullptr, o);
@@ -222,8 +234,10 @@ extern "C" size_t mako_attn_fwd_rows_workspace(const mako_attn_args* a, uint32_t
     if (!a || (dim != 64 && dim != 128 && dim != 256))
         return 0;
     const mako_attn_args t = tiles_call(a);
-    // the fused route's images or the separate calls' attention, whichever the call takes: the larger
-    return tiles_bytes(&t, dim) + std::max(dim == 256 ? d256_workspace(&t) : (size_t)0, attn_fwd_workspace(&t, dim));
+    // the fused route's images (heads of 256 past flash_fwd_r32's offsets, sized for an f32 output, the larger) or
+    // the separate calls' attention, whichever the call takes: the larger
+    const size_t images = dim == 256 && !r32_fits(&t, 4) ? d256_workspace(&t) : 0;
+    return tiles_bytes(&t, dim) + std::max(images, attn_fwd_workspace(&t, dim));
 }
 
 extern "C" int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,

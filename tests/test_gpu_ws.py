@@ -35,8 +35,9 @@ DENSE = [
     ("prefill", 8, 2, 128, 300, 300, 0, U32),
     ("split_k_rows", 32, 8, 128, 1, 3000, 2999, U32),
     ("split_k_4_rows", 32, 8, 128, 4, 700, 696, U32),
-    ("d256", 4, 2, 256, 130, 130, 0, U32),
+    ("d256", 4, 2, 256, 130, 130, 0, U32),   # flash_fwd_r32: no workspace (flash_fwd_d256's images past its offsets)
 ]
+NO_WORKSPACE = ("prefill", "d256")
 
 
 @pytest.mark.parametrize("case", DENSE, ids=lambda c: c[0])
@@ -50,7 +51,7 @@ def test_fwd_ws_matches_library_workspace(case):
     args = dict(n_q=n_q, q_pad=q_pad, n_k=n_k, k_pad=k_pad, heads=heads, kv_heads=kv, q_pos0=q_pos0, block=block,
                 dim=dim)
     need = M.attn_fwd_workspace(**args)
-    assert (need == 0) == (name == "prefill"), need
+    assert (need == 0) == (name in NO_WORKSPACE), need
     outs = []
     for ws in (M.LIBRARY, torch.empty(need, dtype=torch.uint8, device="cuda") if need else None):
         o = torch.full((n_q, heads * dim), float("nan"), dtype=torch.bfloat16, device="cuda")
