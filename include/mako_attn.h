@@ -91,12 +91,13 @@ const char* mako_last_error(void);
  * are masked (their rows need not be zero); fully masked rows give 0 and lse = -inf. Precision: P (the softmax
  * numerators) is rounded to the input type for P V, as the reference rounds it to half (src/kernels/ops.metal:329):
  * f16 inputs f16 P (relative error <= 2^-11 a probability), bf16 inputs bf16 P (<= 2^-8; rows that see fewer than 64
- * keys get probabilities to ~16 bits). V is used in its own type, bf16 V over its whole range, except at dim 256,
- * whose kernel converts bf16 V to f16 rounding toward zero (|v| above 65504 saturates, below 6.1e-5 loses bits).
- * The sums and the LSE add the unrounded f32 exponentials. Heads of 64 and 128 take one of two routes: a few query
- * rows (n_q x heads / kv_heads <= 64, as the reference's decode, attention with n_q = 1) split-K over the keys,
- * with its partials in a workspace; more rows, the prefill kernel, one launch with no workspace. Heads of 256 first
- * write V as f16 V^T tiles into a workspace. mako_attn_fwd keeps that workspace itself, per (device, stream),
+ * keys get probabilities to ~16 bits). V is used in its own type, bf16 V over its whole range, except at dim 256
+ * past the heads-of-256 kernel's 32-bit offsets (calls of several GB), whose kernel converts bf16 V to f16 rounding
+ * toward zero (|v| above 65504 saturates, below 6.1e-5 loses bits). The sums and the LSE add the unrounded f32
+ * exponentials. Heads of 64 and 128 take one of two routes: a few query rows (n_q x heads / kv_heads <= 64, as the
+ * reference's decode, attention with n_q = 1) split-K over the keys, with its partials in a workspace; more rows,
+ * the prefill kernel, one launch with no workspace. Heads of 256 take one launch with no workspace, or past its
+ * offsets first write V as f16 V^T tiles into a workspace. mako_attn_fwd keeps that workspace itself, per (device, stream),
  * allocated stream-ordered the first time a call needs it (or more of it) and held until mako_attn_release(stream);
  * under graph capture a call that would grow it fails with MAKO_EWORKSPACE.
  */
@@ -242,7 +243,8 @@ int mako_heads(const mako_heads_args* a, mako_dtype out, const float* x, const f
  * a->heads, hk->heads and hv->heads a->kv_heads, and the three dims equal (64, 128 or 256).
  * Heads of 64, 128 or 256 with 16-byte aligned rows (mako_heads' vector path), values neither normed nor rotated,
  * and more rows than the split-K route takes run as two launches: one that writes the query, key and value tiles
- * (heads of 256: the f16 V^T images their kernel stages from instead of the value tiles), then the prefill kernel.
+ * (heads of 256 past the prefill kernel's offsets: the f16 V^T images their kernel stages from instead of the value
+ * tiles), then the prefill kernel mako_attn_fwd takes for the same call.
  * Other calls run the four launches above. The tiles live in a workspace (kept as mako_attn_fwd keeps its own).
  */
 int mako_attn_fwd_rows(const mako_attn_args* a, const mako_heads_args* hq, const mako_heads_args* hk,
