@@ -188,9 +188,23 @@ def test_h3_vae_d64_bidirectional_s4096_bf16_sampled():
 
 def test_qwen35_d256_causal_s4096_bf16_sampled():
     """16 query heads over 2 kv heads, D 256, S 4096, causal, bf16 in and out (Qwen3.5 gated attention,
-    flash_fwd_d256): one row of every (head, query tile) and sampled rows against the oracle."""
+    flash_fwd_r32): one row of every (head, query tile) and sampled rows against the oracle."""
     print("causal D256 S4096 bf16", flush=True)
     _sampled(16, 2, 256, 4096, U32, O.BF16, 120, 256)
+
+
+def test_d256_bidirectional_mha_s2048_f16_sampled():
+    """Heads of 256 with one query head a kv head (a workgroup's waves hold rows 32 apart), bidirectional, f16 in
+    and out, S 2048 (flash_fwd_r32): one row of every (head, query tile) and sampled rows against the oracle."""
+    print("bidirectional D256 MHA S2048 f16", flush=True)
+    _sampled(8, 8, 256, 2048, 0, O.F16, 80, 2562)
+
+
+def test_d256_prefix_causal_gqa2_s3000_bf16_sampled():
+    """Heads of 256, two query heads a kv head, prefix-causal (block 1000), ragged S 3000, bf16 (flash_fwd_r32):
+    one row of every (head, query tile) and sampled rows against the oracle."""
+    print("prefix-causal D256 GQA2 S3000 bf16", flush=True)
+    _sampled(8, 4, 256, 3000, 1000, O.BF16, 80, 2563)
 
 
 def test_deterministic_and_row_independent():
