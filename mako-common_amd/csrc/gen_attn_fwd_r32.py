@@ -18,6 +18,9 @@ What differs from r64:
     QK j, and tile j + 1's, written by it), and the exponentials go to a third set E, which phase QK packs into P.
     The exact path therefore reads no LDS and re-issues no operand reads.
   * One row block: the mask, exponentials, sums, checks and epilogue cover 32 rows.
+  * V's 32-byte units are placed so that each 32-lane pass of the transpose reads covers the 64 LDS banks once
+    (v_unit), which takes four V^T read-address registers (one for each db % 4) instead of r64's two.
+  * The grid is persistent, as r64's; the C++ side (attn_fwd_r32.hip) walks the items.
 
 Iteration j (RAW(j) masked raw scores of tile j, E its exponentials against the running maximum):
   phase QK: 32 MFMAs, RAW(j + 1) = K(j + 1) Q^T, beside the staging of K(j + 2) and V(j + 1), P = E rounded to the
