@@ -1011,9 +1011,9 @@ def main():
 
 
 def configs_summary(line, pre, dec, few):
-    """The five configurations and the few-row route in a few numbers each, last in the JSON line (so a record that
-    keeps only the line's tail still holds them): value, unit, kernel ms, fraction of the roofline, and the parity of
-    the sampled rows (within tolerance, max abs error)."""
+    """The five configurations, the other head widths and the few-row route in a few numbers each, last in the JSON
+    line (so a record that keeps only the line's tail still holds them): value, unit, kernel ms, fraction of the
+    roofline, and the parity of the sampled rows (within tolerance, max abs error)."""
     def par(p):
         return {} if not p else {"within_tolerance": p["within_tolerance"], "max_abs_err": round(p["max_abs_err"], 6)}
 
@@ -1032,6 +1032,8 @@ def configs_summary(line, pre, dec, few):
         "C4_block_sparse_s16384": entry(spa["value"], "TFLOP/s", spa["kernel_ms"], spa["roofline"]["frac"],
                                         spa.get("parity")),
         "C5_bidirectional_s16384": entry(bid["value"], "TFLOP/s", bid["kernel_ms"], bid["frac"], bid.get("parity")),
+        **{f"heads_{name}": entry(h["value"], "TFLOP/s", h["kernel_ms"], h["frac"], h.get("parity"))
+           for name, h in line["other_head_widths"].items() if isinstance(h, dict) and "kernel_ms" in h},
         "few_rows_n_q1": entry(f1["gbps"], "GB/s", f1["kernel_ms"], f1["roofline"]["frac"], f1.get("parity")),
         "h3_sparse_per_head_lists": entry(h3s["attention"]["tflops"], "TFLOP/s", h3s["attention"]["kernel_ms"],
                                           h3s["roofline"]["frac"], h3s.get("parity")),
